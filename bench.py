@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the torch_gcu PrivateUse1 op path on one MI355X.
+
+A step is one pass of BASELINE config 2 (row reductions and softmax) over one
+batch of synthetic input already resident in HBM:
+    sum(-1), amax(-1), log_softmax(-1) of bf16 logits [8192, 32000] N(0, 4)
+    mean(0) of fp32 [16384, 4096] N(0, 1)
+all through the gfx950 kernels.  `value` is the step's algorithmic bytes
+(unique inputs read once + outputs written once) divided by the step time,
+in GB/s.  Two input sets alternate between steps so the 256 MiB MALL cannot
+serve a re-read.
+
+The same JSON line carries
+  roofline      the dominant kernel (log_softmax) timed per launch with HIP
+                events on the stream it runs on, against 8 TB/s;
+  cpu_baseline  CPU ATen (the reference's fallback path, run through
+                oracle.aten) on a bounded row sample of the same workload;
+  ops           every other measured op of configs 1 and 3 (GB/s, fraction
+                of HBM peak), each with its own rotation of input sets.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-ops]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "torch-gcu_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "HBM GB/s (elementwise/norm), MFMA TFLOPS (addmm/int8), decoder-layer tok/s"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-ops", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+class EventTimer:
+    """Accumulates device time of launches on the current stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def __enter__(self):
+        self.s = self.torch.cuda.Event(enable_timing=True)
+        self.e = self.torch.cuda.Event(enable_timing=True)
+        self.s.record()
+        return self
+
+    def __exit__(self, *a):
+        self.e.record()
+        self.pairs.append((self.s, self.e))
+
+    def total_ms(self):
+        self.torch.cuda.synchronize()
+        return sum(s.elapsed_time(e) for s, e in self.pairs)
+
+
+def config2_alg_bytes(rows=8192, vocab=32000, mrows=16384, mcols=4096):
+    x = rows * vocab * 2
+    return {
+        "sum": x + rows * 2,
+        "amax": x + rows * 2,
+        "log_softmax": 2 * x,
+        "mean": mrows * mcols * 4 + mcols * 4,
+    }
+
+
+def run_config2(torch, _abi, synthetic, steps, warmup):
+    log("bench: generating config 2 inputs (2 sets)")
+    sets = []
+    for k in range(2):
+        c = synthetic.config2()
+        if k == 1:  # a second, different set for MALL rotation
+            c = {"logits": c["logits"].flip(0).contiguous(), "m": c["m"].flip(0).contiguous()}
+        sets.append({"logits": c["logits"].cuda(), "m": c["m"].cuda()})
+    rows, vocab = sets[0]["logits"].shape
+    outs = {
+        "sum": torch.empty(rows, dtype=torch.bfloat16, device="cuda"),
+        "amax": torch.empty(rows, dtype=torch.bfloat16, device="cuda"),
+        "log_softmax": torch.empty(rows, vocab, dtype=torch.bfloat16, device="cuda"),
+        "mean": torch.empty(sets[0]["m"].shape[1], dtype=torch.float32, device="cuda"),
+    }
+    timers = {k: EventTimer(torch) for k in outs}
+
+    def step(i, timed):
+        s = sets[i % 2]
+        if timed:
+            with timers["sum"]:
+                _abi.sum_(outs["sum"], s["logits"], [-1])
+            with timers["amax"]:
+                _abi.amax(outs["amax"], s["logits"], [-1])
+            with timers["log_softmax"]:
+                _abi.log_softmax(outs["log_softmax"], s["logits"], -1)
+            with timers["mean"]:
+                _abi.mean(outs["mean"], s["m"], [0])
+        else:
+            _abi.sum_(outs["sum"], s["logits"], [-1])
+            _abi.amax(outs["amax"], s["logits"], [-1])
+            _abi.log_softmax(outs["log_softmax"], s["logits"], -1)
+            _abi.mean(outs["mean"], s["m"], [0])
+
+    for i in range(warmup):
+        step(i, False)
+    torch.cuda.synchronize()
+    log(f"bench: warmup done ({warmup} steps), timing {steps} steps")
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i, True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_op_ms = {k: t.total_ms() / steps for k, t in timers.items()}
+    return wall, per_op_ms
+
+
+def cpu_baseline(torch, synthetic, seconds):
+    """CPU ATen on a row sample of config 2 (same distributions and seeds)."""
+    from oracle import aten
+
+    rows, mrows = 256, 1024
+    c = synthetic.config2(rows=rows, mrows=mrows)
+    ab = config2_alg_bytes(rows=rows, mrows=mrows)
+    total = sum(ab.values())
+    # warm up once, then repeat until the budget is spent
+    aten.sum_(c["logits"], -1)
+    aten.amax(c["logits"], -1)
+    aten.log_softmax(c["logits"], -1)
+    aten.mean(c["m"], 0)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        aten.sum_(c["logits"], -1)
+        aten.amax(c["logits"], -1)
+        aten.log_softmax(c["logits"], -1)
+        aten.mean(c["m"], 0)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {
+        "value": round(total * n / el / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"CPU ATen (the reference's CPU fallback path, via oracle.aten) running "
+                   f"sum/amax/log_softmax on bf16 [{rows},32000] and mean(0) on fp32 "
+                   f"[{mrows},4096], {n} passes in {el:.1f} s"),
+    }
+
+
+def bench_op(torch, name, sets, fn, alg_bytes, iters=30):
+    """Per-launch time of fn over rotating input sets (HIP events)."""
+    for s in sets[:2]:
+        fn(s)
+    torch.cuda.synchronize()
+    st = torch.cuda.Event(enable_timing=True)
+    en = torch.cuda.Event(enable_timing=True)
+    st.record()
+    for i in range(iters):
+        fn(sets[i % len(sets)])
+    en.record()
+    torch.cuda.synchronize()
+    ms = st.elapsed_time(en) / iters
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    return {"op": name, "ms": round(ms, 4), "GB/s": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes": alg_bytes}
+
+
+def other_ops(torch, _abi, synthetic):
+    res = []
+    log("bench: config 1 ops")
+    c1 = synthetic.config1()
+    a, b = c1["a"].cuda(), c1["b"].cuda()
+    sets = [{"a": a if k == 0 else a.roll(k, 0), "o": torch.empty_like(a)} for k in range(5)]
+    res.append(bench_op(torch, "c1.mul [4096,4096]x[4096] f32", sets,
+                        lambda s: _abi.mul(s["o"], s["a"], b), 4096 * 4096 * 8 + 4096 * 4))
+    res.append(bench_op(torch, "c1.add [4096,4096]+0.5 f32", sets,
+                        lambda s: _abi.add(s["o"], s["a"], 0.5), 4096 * 4096 * 8))
+    del sets
+    table, idx = c1["table"].cuda(), c1["idx"].cuda()
+    tsets = [{"t": table if k == 0 else table.roll(k, 0), "o": torch.empty(idx.numel(), 8, dtype=torch.int64, device="cuda")}
+             for k in range(8)]
+    res.append(bench_op(torch, "c1.index_select int64 [1048576,8] x 262144", tsets,
+                        lambda s: _abi.index_select(s["o"], s["t"], 0, idx), 35651584))
+    del tsets, table
+    log("bench: config 3 ops")
+    c3 = synthetic.config3()
+    x, w = c3["x"].cuda(), c3["w"].cuda()
+    xs = [{"x": x if k == 0 else x.roll(k, 0), "o": torch.empty_like(x)} for k in range(3)]
+    res.append(bench_op(torch, "c3.rms_norm bf16 [16384,4096]", xs,
+                        lambda s: _abi.rms_norm(s["o"], s["x"], w, 1e-6), 268443648))
+    del xs, x
+    q, k, pos = c3["q"].cuda(), c3["k"].cuda(), c3["pos"].cuda()
+    qs = [{"q": q, "k": k, "qo": torch.empty_like(q), "ko": torch.empty_like(k)},
+          {"q": k, "k": q, "qo": torch.empty_like(q), "ko": torch.empty_like(k)}]
+    res.append(bench_op(torch, "c3.rope q,k bf16 [16384,32,128]", qs,
+                        lambda s: _abi.rope(s["qo"], s["ko"], s["q"], s["k"], pos, 10000.0),
+                        536870912))
+    del qs, q, k
+    gt, up = c3["gate"].cuda(), c3["up"].cuda()
+    gs = [{"g": gt, "u": up, "o": torch.empty_like(gt)}, {"g": up, "u": gt, "o": torch.empty_like(gt)}]
+    res.append(bench_op(torch, "c3.silu_mul bf16 [16384,11008]", gs,
+                        lambda s: _abi.silu_mul(s["o"], s["g"], s["u"]), 1082130432))
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every GPU box "
+              "in this setup has one MI355X.  Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+
+    from torch_gcu import _abi
+    from torch_gcu.utils import synthetic
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.cuda.init()
+    _abi.install_torch_workspace()
+    props = torch.cuda.get_device_properties(0)
+    log(f"bench: device {props.name}, {props.multi_processor_count} CUs")
+
+    wall, per_op_ms = run_config2(torch, _abi, synthetic, args.steps, args.warmup)
+    ab = config2_alg_bytes()
+    total_bytes = sum(ab.values())
+    ms_per_step = wall * 1e3 / args.steps
+    value = total_bytes / (wall / args.steps) / 1e9
+    ls_ms = per_op_ms["log_softmax"]
+    achieved = ab["log_softmax"] / (ls_ms * 1e-3) / 1e9
+    per_op = {k: {"ms": round(v, 4), "GB/s": round(ab[k] / (v * 1e-3) / 1e9, 1),
+                  "frac_hbm": round(ab[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+              for k, v in per_op_ms.items()}
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded CPU generators of BASELINE config 2, copied to HBM)",
+        "config": {"workload": "config2: sum/amax/log_softmax over bf16 [8192,32000] + "
+                               "mean(0) over fp32 [16384,4096]",
+                   "alg_bytes_per_step": total_bytes, "per_op": per_op},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "softmax_reg_kernel (log_softmax)",
+                     "alg_bytes_per_launch": ab["log_softmax"],
+                     "avg_launch_ms": round(ls_ms, 4)},
+    }
+    if not args.no_ops:
+        line["ops"] = other_ops(torch, _abi, synthetic)
+    if not args.no_cpu:
+        log("bench: CPU baseline")
+        line["cpu_baseline"] = cpu_baseline(torch, synthetic, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,224 @@
+/*
+ * mi355x_ops.h -- C ABI of the gfx950 (MI355X) kernel library behind the
+ * torch_gcu PrivateUse1 op path.
+ *
+ * This library takes the place of the closed TopsAten kernel library that the
+ * reference reaches through its bridge templates
+ * (torch_gcu/csrc/aten/aot_ops/topsaten_bridge_define.h:323-427): every entry
+ * point receives preallocated outputs, borrowed inputs, scalar parameters by
+ * value and the stream to enqueue on, and returns a status.  The descriptor
+ * replaces topsatenTensor (built by createTopsatenTensor,
+ * torch_gcu/csrc/gcu/gcu_utils.cpp:79-108) and the scalar replaces
+ * topsatenScalar_t (gcu_utils.cpp:322-430).
+ *
+ * Rules every entry point keeps:
+ *   - plain C types only: no torch, no C++ exceptions across the boundary;
+ *   - outputs are preallocated by the caller and never resized here;
+ *   - enqueue-only on `stream`: no hipMalloc, no synchronous copy and no
+ *     stream synchronisation, so every call can be captured in a hipGraph;
+ *   - temporary device memory comes only from the allocator registered with
+ *     mi_set_workspace_allocator (the reference registers its caching
+ *     allocator with the kernel library the same way,
+ *     torch_gcu/csrc/gcu/gcu_custom_api.cpp:23-31);
+ *   - on failure a status other than MI_OK is returned and mi_last_error()
+ *     gives a message for the calling thread.
+ *   - 64-bit integer and floating types stay 64-bit on the device (the
+ *     reference narrows them, torch_gcu/csrc/gcu/gcu_hardware.h:38-101; this
+ *     library does not).
+ */
+#ifndef MI355X_OPS_H
+#define MI355X_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in HIP headers; 0 is the null stream. */
+typedef void* mi_stream_t;
+
+typedef enum {
+  MI_OK = 0,
+  MI_ERR_INVALID = 1,      /* bad shape, stride, dtype or parameter */
+  MI_ERR_UNSUPPORTED = 2,  /* valid request this library does not implement */
+  MI_ERR_WORKSPACE = 3,    /* no workspace allocator, or it returned NULL */
+  MI_ERR_LAUNCH = 4,       /* the HIP runtime reported an error */
+  MI_ERR_TOO_LARGE = 5     /* a size exceeds a documented maximum */
+} mi_status_t;
+
+/* Data types.  The numeric codes equal c10::ScalarType's so the host passes
+ * tensor.scalar_type() through unchanged. */
+typedef enum {
+  MI_U8 = 0,
+  MI_I8 = 1,
+  MI_I16 = 2,
+  MI_I32 = 3,
+  MI_I64 = 4,
+  MI_F16 = 5,
+  MI_F32 = 6,
+  MI_F64 = 7,
+  MI_BOOL = 11,
+  MI_BF16 = 15
+} mi_dtype_t;
+
+#define MI_MAX_DIMS 8
+
+/* Strided tensor view.  Sizes and strides are in elements; ndim 0 is a
+ * scalar (one element).  Replaces topsatenTensor(dims, strides, dtype, data)
+ * (gcu_utils.cpp:79-108), which caps rank at 8 as this does. */
+typedef struct {
+  void* data;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t sizes[MI_MAX_DIMS];
+  int64_t strides[MI_MAX_DIMS];
+} mi_tensor_t;
+
+/* A host scalar.  dtype is the scalar's own type: a floating dtype selects
+ * f, any other selects i (bools are 0/1).  wrapped != 0 marks a Python
+ * number (ATen's "wrapped number", which takes part in type promotion only
+ * by category and as the default dtype); wrapped == 0 marks the value of a
+ * 0-dim tensor.  Replaces topsatenScalar_t (gcu_utils.cpp:322-430); the CPU
+ * 0-dim operand rule (codegen/gen_backend_stubs.py:1061-1078) hands values
+ * over this way. */
+typedef struct {
+  double f;
+  int64_t i;
+  int32_t dtype;
+  int32_t wrapped;
+} mi_scalar_t;
+
+/* ---- library state ---------------------------------------------------- */
+
+/* Version of this ABI, (major << 16) | minor. */
+int32_t mi_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mi_last_error(void);
+
+/* Stream-ordered workspace allocator used by entry points that need
+ * temporary device memory.  Replaces topsatenMallocAsyncFuncRegister /
+ * topsatenFreeAsyncFuncRegister (torch_gcu/csrc/gcu/gcu_custom_api.cpp:23-31,
+ * implemented at gcu_caching_allocator.cpp:2956-3000).  free_fn is called with
+ * the stream the memory was last used on. */
+typedef void* (*mi_alloc_fn)(size_t bytes, mi_stream_t stream, void* ctx);
+typedef void (*mi_free_fn)(void* ptr, mi_stream_t stream, void* ctx);
+mi_status_t mi_set_workspace_allocator(mi_alloc_fn alloc_fn, mi_free_fn free_fn,
+                                       void* ctx);
+
+/* Number of compute units of the current device (used for launch sizing);
+ * negative on error. */
+int32_t mi_device_cu_count(void);
+
+/* ---- copies and fills --------------------------------------------------- */
+
+/* out[...] = (out.dtype) src[...]; src broadcasts to out.  Same-dtype
+ * contiguous copies become one D2D memcpy.  Replaces topsatenCopy
+ * (torch_gcu/csrc/aten/aot_ops/gcu_copy.cpp:116-150). */
+mi_status_t mi_copy(const mi_tensor_t* out, const mi_tensor_t* src,
+                    mi_stream_t stream);
+
+/* out[...] = value.  Replaces topsatenFill_ (yaml fill_.Scalar :316). */
+mi_status_t mi_fill(const mi_tensor_t* out, mi_scalar_t value,
+                    mi_stream_t stream);
+
+/* ---- binary elementwise (TensorIterator semantics) ----------------------
+ * Inputs broadcast to out.  The common dtype follows ATen's result_type
+ * (dimensioned tensors over 0-dim tensors over wrapped scalars, by
+ * category); the op computes in float for f16/bf16, in the common type
+ * otherwise, and casts to out.dtype on store.
+ * Replace topsatenAdd / topsatenSub / topsatenMul / topsatenDiv
+ * (codegen/gcu_native_functions.yaml add.out :202, mul.out :461; the
+ * scalar forms are the RHS_IS_SCALAR branch,
+ * codegen/gen_backend_stubs.py:1061-1078). */
+mi_status_t mi_add(const mi_tensor_t* out, const mi_tensor_t* self,
+                   const mi_tensor_t* other, mi_scalar_t alpha,
+                   mi_stream_t stream);
+mi_status_t mi_sub(const mi_tensor_t* out, const mi_tensor_t* self,
+                   const mi_tensor_t* other, mi_scalar_t alpha,
+                   mi_stream_t stream);
+mi_status_t mi_mul(const mi_tensor_t* out, const mi_tensor_t* self,
+                   const mi_tensor_t* other, mi_stream_t stream);
+/* True division: integer inputs compute in float32. */
+mi_status_t mi_div(const mi_tensor_t* out, const mi_tensor_t* self,
+                   const mi_tensor_t* other, mi_stream_t stream);
+/* out = self + alpha * other_scalar, other a wrapped number. */
+mi_status_t mi_add_scalar(const mi_tensor_t* out, const mi_tensor_t* self,
+                          mi_scalar_t other, mi_scalar_t alpha,
+                          mi_stream_t stream);
+/* out = self * other_scalar, other a wrapped number. */
+mi_status_t mi_mul_scalar(const mi_tensor_t* out, const mi_tensor_t* self,
+                          mi_scalar_t other, mi_stream_t stream);
+
+/* ---- indexing ---------------------------------------------------------- */
+
+/* out = self.index_select(dim, index); index is 1-D (or 0-D) int32/int64;
+ * negative indices are not wrapped (as in ATen).  The kernel never reads
+ * outside self: a row whose index is out of range is written as zeros and
+ * the host layer raises the IndexError (the reference validates shapes in
+ * torch_gcu/csrc/aten/shape_inference/indexing.cpp:20-69).  Replaces
+ * topsatenIndexSelect (yaml index_select.out :379). */
+mi_status_t mi_index_select(const mi_tensor_t* out, const mi_tensor_t* self,
+                            int64_t dim, const mi_tensor_t* index,
+                            mi_stream_t stream);
+
+/* ---- reductions ----------------------------------------------------------
+ * dims lists the reduced dimensions of self (empty = all).  out holds
+ * self's shape with reduced dims removed (keepdim=0) or set to 1
+ * (keepdim=1).  Floating inputs accumulate in float (double for f64);
+ * integer sums in int64.  Replace topsatenSum (sum.IntList_out :576),
+ * topsatenAmax (amax.out :209), topsatenMean (mean.out :445). */
+mi_status_t mi_sum(const mi_tensor_t* out, const mi_tensor_t* self,
+                   const int64_t* dims, int32_t ndims, int32_t keepdim,
+                   mi_stream_t stream);
+mi_status_t mi_amax(const mi_tensor_t* out, const mi_tensor_t* self,
+                    const int64_t* dims, int32_t ndims, int32_t keepdim,
+                    mi_stream_t stream);
+mi_status_t mi_mean(const mi_tensor_t* out, const mi_tensor_t* self,
+                    const int64_t* dims, int32_t ndims, int32_t keepdim,
+                    mi_stream_t stream);
+
+/* ---- softmax family -------------------------------------------------------
+ * out = softmax / log_softmax of self along dim, computed in float; out may
+ * be float when self is f16/bf16 (half_to_float).  Replace
+ * topsatenSoftmaxForward (_softmax.out :182) and topsatenLogSoftmaxForward
+ * (_log_softmax.out :155). */
+mi_status_t mi_softmax(const mi_tensor_t* out, const mi_tensor_t* self,
+                       int64_t dim, mi_stream_t stream);
+mi_status_t mi_log_softmax(const mi_tensor_t* out, const mi_tensor_t* self,
+                           int64_t dim, mi_stream_t stream);
+
+/* ---- fused efficient ops ---------------------------------------------------
+ * The reference's efficient_ops entry point pattern
+ * (torch_gcu/csrc/efficient_ops/ops.h:14-93, pybind at
+ * torch_gcu/csrc/python/efficient_ops.cpp:12-26) holds one op; these are
+ * new fused ops on the same surface and have no TopsAten counterpart. */
+
+/* out[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * weight, fp32 math,
+ * over the last dim; weight may be NULL data (no scale). */
+mi_status_t mi_rms_norm(const mi_tensor_t* out, const mi_tensor_t* x,
+                        const mi_tensor_t* weight, double eps,
+                        mi_stream_t stream);
+
+/* Rotate-half RoPE on [tokens, heads, head_dim] q and k (k may be NULL data)
+ * with per-token int64/int32 positions:
+ *   inv_freq[i] = theta^(-2i/head_dim), angle = pos * inv_freq[i],
+ *   out[..., i]      = x[i] * cos - x[i + d/2] * sin
+ *   out[..., i+d/2]  = x[i + d/2] * cos + x[i] * sin,   i < d/2.
+ * Outputs may alias inputs (in place). */
+mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out,
+                    const mi_tensor_t* q, const mi_tensor_t* k,
+                    const mi_tensor_t* positions, double theta,
+                    mi_stream_t stream);
+
+/* out = silu(gate) * up, fp32 math: silu(g) = g / (1 + exp(-g)). */
+mi_status_t mi_silu_mul(const mi_tensor_t* out, const mi_tensor_t* gate,
+                        const mi_tensor_t* up, mi_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_OPS_H */

@@ -1,0 +1,130 @@
+"""The reference's own CPU path for each op: CPU ATen.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+Each function takes CPU tensors and returns CPU tensors; the caller copies
+device inputs to the host first, exactly as the boxed fallback does
+(torch_gcu/csrc/aten/aten_cpu_fallback.cpp:342-411 -> at::native::cpu_fallback
+at :390, results copied back by copy_back_to_org_device).  For the fused ops
+that have no reference counterpart (RMSNorm, RoPE, SiLU-mul, int8
+weight-only linear) the oracle is the fp32 closed form built from CPU ATen
+ops, as the north_star defines them.
+"""
+from __future__ import annotations
+
+import torch
+
+
+# ---- config 1: elementwise and indexing ---------------------------------------
+
+def mul(a: torch.Tensor, b) -> torch.Tensor:
+    """aten::mul.out -> topsatenMul (codegen/gcu_native_functions.yaml:461).
+    Pinned by numpy float32 multiply (bit-exact) in tests/test_oracle.py."""
+    return torch.mul(a, b)
+
+
+def add(a: torch.Tensor, b, alpha=1) -> torch.Tensor:
+    """aten::add.out -> topsatenAdd (yaml :202); a CPU scalar operand takes the
+    RHS_IS_SCALAR branch (codegen/gen_backend_stubs.py:1061-1078).
+    Pinned by numpy float32 add (bit-exact)."""
+    return torch.add(a, b, alpha=alpha)
+
+
+def sub(a, b, alpha=1):
+    """aten::sub.out (sub is add with -alpha).  Pinned by numpy."""
+    return torch.sub(a, b, alpha=alpha)
+
+
+def div(a, b):
+    """aten::div.out, true division.  Pinned by numpy float32 divide."""
+    return torch.div(a, b)
+
+
+def index_select(self: torch.Tensor, dim: int, index: torch.Tensor) -> torch.Tensor:
+    """aten::index_select -> topsatenIndexSelect (yaml :377-380; shape rules
+    torch_gcu/csrc/aten/shape_inference/indexing.cpp:20-69).
+    Pinned by numpy.take (bit-exact) and brute force on tiny inputs."""
+    return torch.index_select(self, dim, index)
+
+
+# ---- config 2: reductions and softmax --------------------------------------
+
+def sum_(x: torch.Tensor, dim=None, keepdim=False, dtype=None) -> torch.Tensor:
+    """aten::sum.IntList_out -> topsatenSum (yaml :576), fp32 accumulation for
+    bf16.  Pinned by float64 numpy sums within the fp32/bf16 bars and by the
+    constant-row closed form N*c."""
+    if dim is None:
+        return torch.sum(x, dtype=dtype)
+    return torch.sum(x, dim=dim, keepdim=keepdim, dtype=dtype)
+
+
+def amax(x: torch.Tensor, dim=(), keepdim=False) -> torch.Tensor:
+    """aten::amax.out -> topsatenAmax (yaml :209).  Order independent, so
+    exact.  Pinned by numpy.max (bit-exact) and the single-spike row."""
+    return torch.amax(x, dim=dim, keepdim=keepdim)
+
+
+def mean(x: torch.Tensor, dim=None, keepdim=False) -> torch.Tensor:
+    """aten::mean.out -> topsatenMean (yaml :445).  Pinned by float64 numpy."""
+    if dim is None:
+        return torch.mean(x)
+    return torch.mean(x, dim=dim, keepdim=keepdim)
+
+
+def log_softmax(x: torch.Tensor, dim: int, half_to_float: bool = False) -> torch.Tensor:
+    """aten::_log_softmax.out -> topsatenLogSoftmaxForward (yaml :155-156).
+    Pinned by a float64 numpy log-sum-exp, the constant-row value -ln(N) and
+    the invariant logsumexp(out) == 0."""
+    return torch._log_softmax(x, dim, half_to_float)
+
+
+def softmax(x: torch.Tensor, dim: int, half_to_float: bool = False) -> torch.Tensor:
+    """aten::_softmax.out -> topsatenSoftmaxForward (yaml :182-183).
+    Pinned by float64 numpy and the invariant sum(out) == 1."""
+    return torch._softmax(x, dim, half_to_float)
+
+
+# ---- config 3: fused efficient ops (fp32 closed forms) -------------------------
+
+def rms_norm(x: torch.Tensor, w, eps: float) -> torch.Tensor:
+    """y = x * rsqrt(mean(x^2) + eps) * w in fp32, one cast to x.dtype.
+    torch.rms_norm's CPU kernel computes exactly this for bf16 (checked
+    bit-exact in tests/test_oracle.py).  Pinned by float64 numpy and the
+    golden fixture tests/golden/rms_norm.npz."""
+    xf = x.float()
+    r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    y = xf * r
+    if w is not None:
+        y = y * w.float()
+    return y.to(x.dtype)
+
+
+def rope_tables(positions: torch.Tensor, head_dim: int, theta: float):
+    """fp32 cos/sin of pos * inv_freq, inv_freq = 1 / theta^(2i/d), i < d/2
+    (the rotate-half convention used by HF/NeoX Llama)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+    freqs = positions.float()[:, None] * inv_freq[None, :]
+    return freqs.cos(), freqs.sin()
+
+
+def rope(x: torch.Tensor, positions: torch.Tensor, theta: float) -> torch.Tensor:
+    """Rotate-half RoPE on [tokens, heads, head_dim] in fp32:
+    out[..., :h] = x1*cos - x2*sin, out[..., h:] = x2*cos + x1*sin.
+    Pinned by the invariants (position 0 is the identity, pair norms are
+    preserved), float64 numpy and tests/golden/rope.npz."""
+    d = x.shape[-1]
+    h = d // 2
+    cos, sin = rope_tables(positions, d, theta)
+    cos = cos[:, None, :]
+    sin = sin[:, None, :]
+    xf = x.float()
+    x1, x2 = xf[..., :h], xf[..., h:]
+    out = torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)
+    return out.to(x.dtype)
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up in fp32, one cast (the reference would run silu.out,
+    yaml :561, then mul.out).  Pinned by float64 numpy and
+    tests/golden/silu_mul.npz."""
+    return (torch.nn.functional.silu(gate.float()) * up.float()).to(gate.dtype)

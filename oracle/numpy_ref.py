@@ -1,0 +1,85 @@
+"""numpy restatements of the path's arithmetic, used to pin ``oracle.aten``.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+bfloat16 values are carried as float32 arrays holding exactly representable
+bf16 numbers; ``round_bf16`` applies round-to-nearest-even to 8 mantissa bits
+(the rounding c10::BFloat16 uses).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest-even bfloat16, returned as float32 (NaN -> qNaN)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    out = (r.astype(np.uint32) << 16).view(np.float32)
+    return np.where(np.isnan(x), np.float32(np.nan), out)
+
+
+def mul(a, b):
+    return np.multiply(a, b, dtype=np.float32)
+
+
+def add(a, b, alpha=1.0):
+    if alpha == 1.0:
+        return np.add(a, b, dtype=np.float32)
+    return np.add(a, np.float32(alpha) * np.asarray(b, dtype=np.float32), dtype=np.float32)
+
+
+def index_select(table: np.ndarray, dim: int, idx: np.ndarray) -> np.ndarray:
+    return np.take(table, idx, axis=dim)
+
+
+def index_select_brute(table: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    """Row gather by explicit loops (tiny inputs only)."""
+    out = np.empty((len(idx),) + table.shape[1:], dtype=table.dtype)
+    for i, j in enumerate(idx):
+        out[i] = table[j]
+    return out
+
+
+def sum64(x, axis):
+    return np.sum(np.asarray(x, dtype=np.float64), axis=axis)
+
+
+def mean64(x, axis):
+    return np.mean(np.asarray(x, dtype=np.float64), axis=axis)
+
+
+def log_softmax64(x, axis=-1):
+    x = np.asarray(x, dtype=np.float64)
+    m = np.max(x, axis=axis, keepdims=True)
+    return x - m - np.log(np.sum(np.exp(x - m), axis=axis, keepdims=True))
+
+
+def softmax64(x, axis=-1):
+    return np.exp(log_softmax64(x, axis))
+
+
+def rms_norm64(x, w, eps):
+    x = np.asarray(x, dtype=np.float64)
+    y = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    if w is not None:
+        y = y * np.asarray(w, dtype=np.float64)
+    return y
+
+
+def rope64(x, positions, theta):
+    x = np.asarray(x, dtype=np.float64)
+    d = x.shape[-1]
+    h = d // 2
+    inv = 1.0 / (theta ** (np.arange(0, d, 2, dtype=np.float64) / d))
+    ang = np.asarray(positions, dtype=np.float64)[:, None] * inv[None, :]
+    c = np.cos(ang)[:, None, :]
+    s = np.sin(ang)[:, None, :]
+    x1, x2 = x[..., :h], x[..., h:]
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
+
+
+def silu_mul64(g, u):
+    g = np.asarray(g, dtype=np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(u, dtype=np.float64)

@@ -1,0 +1,410 @@
+"""GPU parity of the gfx950 kernels, called through the C ABI.
+
+Every case runs the same seeded CPU inputs through CPU ATen (the reference's
+own fallback path, via ``oracle.aten``) and through the kernel library, then
+compares: bit-exact for integer/index/amax and single-rounding elementwise
+ops, fp32 rel 1e-5 (+1e-5*max|ref|) for fp32 reductions, bf16 rel 1e-2
+(+1e-2*rms(ref)) for bf16 outputs with fp32 accumulation.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import aten
+from oracle.tolerance import assert_close, assert_exact
+from torch_gcu import _abi
+from torch_gcu.utils import synthetic
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _setup():
+    torch.cuda.init()
+    _abi.install_torch_workspace()
+    yield
+    torch.cuda.synchronize()
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def dev(t):
+    return t.to(DEV)
+
+
+def empty_like_ref(ref):
+    return torch.empty(ref.shape, dtype=ref.dtype, device=DEV)
+
+
+def rand(shape, dtype, seed):
+    if dtype.is_floating_point:
+        return torch.randn(shape, generator=g(seed)).to(dtype)
+    if dtype == torch.bool:
+        return torch.randint(0, 2, shape, generator=g(seed)).bool()
+    lo, hi = (-1000, 1000) if dtype != torch.uint8 else (0, 255)
+    return torch.randint(lo, hi, shape, generator=g(seed)).to(dtype)
+
+
+# ---- elementwise -------------------------------------------------------------------
+
+def test_config1_mul_add_full_size_bit_exact():
+    c = synthetic.config1()
+    a, b = dev(c["a"]), dev(c["b"])
+    t = torch.empty_like(a)
+    out = torch.empty_like(a)
+    _abi.mul(t, a, b)
+    _abi.add(out, t, c["c"])
+    ref = aten.add(aten.mul(c["a"], c["b"]), c["c"])
+    assert_exact(out, ref, "a*b+0.5")
+
+
+BIN_DTYPES = [torch.float32, torch.bfloat16, torch.float16, torch.float64, torch.int32,
+              torch.int64]
+
+
+@pytest.mark.parametrize("dtype", BIN_DTYPES)
+@pytest.mark.parametrize("layout", ["full", "row", "col", "scalar0d", "transposed", "odd"])
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+def test_binary_parity(dtype, layout, op):
+    if op == "div" and not dtype.is_floating_point:
+        pass  # true division promotes to float32
+    shape = (67, 130) if layout != "odd" else (13, 7, 5)
+    a = rand(shape, dtype, 1)
+    if layout == "full" or layout == "odd":
+        b = rand(shape, dtype, 2)
+    elif layout == "row":
+        b = rand(shape[-1:], dtype, 2)
+    elif layout == "col":
+        b = rand((shape[0], 1), dtype, 2)
+    elif layout == "scalar0d":
+        b = rand((), dtype, 2)
+    else:
+        b = rand(shape[::-1], dtype, 2).t()
+    if op == "div" and not dtype.is_floating_point:
+        b = torch.where(b == 0, torch.ones_like(b), b)
+    ref = getattr(aten, op)(a, b)
+    out = empty_like_ref(ref)
+    getattr(_abi, op)(out, dev(a), dev(b))
+    assert_exact(out, ref, f"{op} {dtype} {layout}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.int64,
+                                   torch.int32, torch.uint8])
+@pytest.mark.parametrize("value", [0.5, 0.1, 3, -2])
+def test_scalar_operand_parity(dtype, value):
+    a = rand((129, 33), dtype, 3)
+    ref_add = aten.add(a, value)
+    out = empty_like_ref(ref_add)
+    _abi.add(out, dev(a), value)
+    assert_exact(out, ref_add, f"add {dtype} {value}")
+    ref_mul = aten.mul(a, value)
+    out = empty_like_ref(ref_mul)
+    _abi.mul(out, dev(a), value)
+    assert_exact(out, ref_mul, f"mul {dtype} {value}")
+
+
+def test_mixed_dtype_promotion():
+    a = rand((40, 50), torch.bfloat16, 4)
+    b = rand((40, 50), torch.float32, 5)
+    for x, y in [(a, b), (b, a), (a, rand((), torch.float32, 6)), (rand((40, 50), torch.int32, 7), rand((), torch.float64, 8))]:
+        ref = aten.mul(x, y)
+        out = empty_like_ref(ref)
+        _abi.mul(out, dev(x), dev(y))
+        assert_exact(out, ref, f"mul {x.dtype}x{y.dtype}")
+
+
+def test_add_alpha():
+    a = rand((1000,), torch.float32, 9)
+    b = rand((1000,), torch.float32, 10)
+    ref = aten.add(a, b, alpha=2)
+    out = empty_like_ref(ref)
+    _abi.add(out, dev(a), dev(b), alpha=2)
+    assert_exact(out, ref, "alpha=2")
+    ref = aten.sub(a, b, alpha=0.3)
+    out = empty_like_ref(ref)
+    _abi.sub(out, dev(a), dev(b), alpha=0.3)
+    assert_close(out, ref, "fp32", "alpha=0.3")
+
+
+def test_empty_and_single_element():
+    for shape in [(0,), (0, 5), (1,), ()]:
+        a = rand(shape, torch.float32, 11)
+        ref = aten.add(a, a)
+        out = empty_like_ref(ref)
+        _abi.add(out, dev(a), dev(a))
+        assert_exact(out, ref, f"add {shape}")
+
+
+@pytest.mark.parametrize("src,dst", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                     (torch.float32, torch.float16), (torch.int64, torch.float32),
+                                     (torch.float64, torch.float16), (torch.float32, torch.int32),
+                                     (torch.float32, torch.uint8), (torch.int32, torch.bool),
+                                     (torch.float64, torch.float64), (torch.bfloat16, torch.bfloat16)])
+def test_copy_conversions(src, dst):
+    x = rand((33, 65), src, 12) * (3 if src.is_floating_point else 1)
+    for view in [x, x.t(), x[:, ::2]]:
+        ref = view.to(dst)
+        out = torch.empty(ref.shape, dtype=dst, device=DEV)
+        _abi.copy_(out, _strided_on_device(view))
+        assert_exact(out, ref, f"copy {src}->{dst}")
+
+
+def _strided_on_device(view):
+    """Device tensor with the same (possibly non-contiguous) view."""
+    base = view
+    while base._base is not None:
+        base = base._base
+    d = dev(base)
+    return d.as_strided(view.shape, view.stride(), view.storage_offset())
+
+
+def test_copy_broadcast_and_fill():
+    src = rand((1, 17), torch.float32, 13)
+    out = torch.empty(9, 17, device=DEV)
+    _abi.copy_(out, dev(src))
+    assert_exact(out, src.expand(9, 17).contiguous(), "broadcast copy")
+    for dtype, v in [(torch.float32, 1.5), (torch.bfloat16, 0.1), (torch.int64, -7), (torch.bool, 1),
+                     (torch.float16, 65504.0), (torch.uint8, 255)]:
+        o = torch.empty(1001, dtype=dtype, device=DEV)
+        _abi.fill_(o, v)
+        assert_exact(o, torch.full((1001,), v, dtype=dtype), f"fill {dtype}")
+    o = torch.zeros(10, 10, device=DEV)
+    _abi.fill_(o[:, 3], 2.0)
+    ref = torch.zeros(10, 10)
+    ref[:, 3] = 2.0
+    assert_exact(o, ref, "strided fill")
+
+
+# ---- index_select -----------------------------------------------------------------
+
+def test_config1_index_select_full_size_bit_exact():
+    c = synthetic.config1()
+    ref = aten.index_select(c["table"], 0, c["idx"])
+    out = empty_like_ref(ref)
+    _abi.index_select(out, dev(c["table"]), 0, dev(c["idx"]))
+    assert_exact(out, ref, "index_select int64")
+
+
+@pytest.mark.parametrize("dtype", [torch.int64, torch.bfloat16, torch.float32, torch.uint8])
+@pytest.mark.parametrize("dim", [0, 1, 2])
+@pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
+def test_index_select_parity(dtype, dim, idx_dtype):
+    x = rand((11, 6, 9), dtype, 14)
+    idx = torch.randint(0, x.shape[dim], (13,), generator=g(15)).to(idx_dtype)
+    ref = aten.index_select(x, dim, idx)
+    out = empty_like_ref(ref)
+    _abi.index_select(out, dev(x), dim, dev(idx))
+    assert_exact(out, ref, f"index_select {dtype} dim{dim}")
+    # non-contiguous self
+    xt = x.transpose(0, 2)
+    ref = aten.index_select(xt, dim, idx.clamp(max=xt.shape[dim] - 1))
+    out = empty_like_ref(ref)
+    _abi.index_select(out, _strided_on_device(xt), dim, dev(idx.clamp(max=xt.shape[dim] - 1)))
+    assert_exact(out, ref, "index_select transposed")
+
+
+def test_index_select_embedding_rows_and_edges():
+    emb = rand((320, 4096), torch.bfloat16, 16)
+    ids = torch.randint(0, 320, (1000,), generator=g(17))
+    ref = aten.index_select(emb, 0, ids)
+    out = empty_like_ref(ref)
+    _abi.index_select(out, dev(emb), 0, dev(ids))
+    assert_exact(out, ref, "embedding")
+    # empty index
+    e = torch.empty(0, dtype=torch.int64)
+    ref = aten.index_select(emb, 0, e)
+    out = empty_like_ref(ref)
+    _abi.index_select(out, dev(emb), 0, dev(e))
+    assert out.shape == (0, 4096)
+    # out-of-range rows are written as zeros, never read
+    bad = torch.tensor([0, 320, -1, 5])
+    out = torch.full((4, 4096), 7.0, dtype=torch.bfloat16, device=DEV)
+    _abi.index_select(out, dev(emb), 0, dev(bad))
+    o = out.cpu()
+    assert torch.equal(o[0], emb[0]) and torch.equal(o[3], emb[5])
+    assert (o[1] == 0).all() and (o[2] == 0).all()
+
+
+# ---- reductions -------------------------------------------------------------------
+
+def test_config2_sum_amax_log_softmax_reduced_rows():
+    c = synthetic.config2(rows=512, mrows=2048)
+    x = dev(c["logits"])
+    ref = aten.sum_(c["logits"], -1)
+    out = empty_like_ref(ref)
+    _abi.sum_(out, x, [-1])
+    assert_close(out, ref, "bf16", "sum")
+    ref = aten.amax(c["logits"], -1)
+    out = empty_like_ref(ref)
+    _abi.amax(out, x, [-1])
+    assert_exact(out, ref, "amax")
+    ref = aten.log_softmax(c["logits"], -1)
+    out = empty_like_ref(ref)
+    _abi.log_softmax(out, x, -1)
+    assert_close(out, ref, "bf16", "log_softmax")
+    ref = aten.mean(c["m"], 0)
+    out = empty_like_ref(ref)
+    _abi.mean(out, dev(c["m"]), [0])
+    assert_close(out, ref, "fp32", "mean0")
+
+
+def test_config2_full_size():
+    c = synthetic.config2()
+    x = dev(c["logits"])
+    out = torch.empty(8192, dtype=torch.bfloat16, device=DEV)
+    _abi.amax(out, x, [-1])
+    assert_exact(out, aten.amax(c["logits"], -1), "amax full")
+    _abi.sum_(out, x, [-1])
+    assert_close(out, aten.sum_(c["logits"], -1), "bf16", "sum full")
+    ls = torch.empty_like(x)
+    _abi.log_softmax(ls, x, -1)
+    assert_close(ls, aten.log_softmax(c["logits"], -1), "bf16", "log_softmax full")
+    # size-independent property: every row's log-sum-exp is 0 (bf16 output)
+    lse = torch.logsumexp(ls.float(), -1)
+    assert lse.abs().max().item() < 0.05
+    m = torch.empty(4096, device=DEV)
+    _abi.mean(m, dev(c["m"]), [0])
+    assert_close(m, aten.mean(c["m"], 0), "fp32", "mean0 full")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64, torch.int32, torch.int64])
+@pytest.mark.parametrize("dims,keepdim", [((-1,), False), ((0,), True), ((1,), False), ((0, 2), False),
+                                          ((), False), ((1, 2), True)])
+def test_reduce_parity(dtype, dims, keepdim):
+    x = rand((37, 19, 45), dtype, 18)
+    ref = aten.sum_(x, list(dims) if dims else None, keepdim) if dims else torch.sum(x)
+    out = empty_like_ref(ref)
+    _abi.sum_(out, dev(x), dims, keepdim)
+    if dtype.is_floating_point:
+        assert_close(out, ref, "bf16" if dtype == torch.bfloat16 else "fp32", f"sum {dims}")
+    else:
+        assert_exact(out, ref, f"sum {dims}")
+    ref = aten.amax(x, dims, keepdim)
+    out = empty_like_ref(ref)
+    _abi.amax(out, dev(x), dims, keepdim)
+    assert_exact(out, ref, f"amax {dims}")
+    if dtype.is_floating_point:
+        ref = aten.mean(x, list(dims), keepdim) if dims else torch.mean(x)
+        out = empty_like_ref(ref)
+        _abi.mean(out, dev(x), dims, keepdim)
+        assert_close(out, ref, "bf16" if dtype == torch.bfloat16 else "fp32", f"mean {dims}")
+
+
+def test_reduce_long_rows_and_noncontiguous():
+    x = rand((3, 1 << 20), torch.float32, 19)
+    ref = aten.sum_(x, -1)
+    out = empty_like_ref(ref)
+    _abi.sum_(out, dev(x), [-1])
+    assert_close(out, ref, "fp32", "long rows")
+    ref = torch.sum(x)
+    out = empty_like_ref(ref)
+    _abi.sum_(out, dev(x), [])
+    assert_close(out, ref, "fp32", "reduce all")
+    xt = rand((64, 48), torch.float32, 20).t()
+    ref = aten.amax(xt, 1)
+    out = empty_like_ref(ref)
+    _abi.amax(out, _strided_on_device(xt), [1])
+    assert_exact(out, ref, "transposed amax")
+
+
+def test_amax_nan_and_empty_sum():
+    x = torch.randn(4, 100)
+    x[2, 17] = float("nan")
+    out = torch.empty(4, device=DEV)
+    _abi.amax(out, dev(x), [1])
+    assert_exact(out, aten.amax(x, 1), "nan amax")
+    e = torch.empty(5, 0)
+    out = torch.empty(5, device=DEV)
+    _abi.sum_(out, dev(e), [1])
+    assert_exact(out, torch.zeros(5), "empty sum")
+
+
+# ---- softmax ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("log", [True, False])
+@pytest.mark.parametrize("case", ["bf16", "f32", "bf16_to_f32", "long_f32", "odd", "dim0"])
+def test_softmax_parity(log, case):
+    if case == "bf16":
+        x, dim, h2f = rand((33, 32000), torch.bfloat16, 21) * 4, -1, False
+    elif case == "f32":
+        x, dim, h2f = rand((20, 1000), torch.float32, 22), -1, False
+    elif case == "bf16_to_f32":
+        x, dim, h2f = rand((20, 5000), torch.bfloat16, 23), -1, True
+    elif case == "long_f32":
+        x, dim, h2f = rand((3, 100003), torch.float32, 24), -1, False
+    elif case == "odd":
+        x, dim, h2f = rand((7, 1001), torch.bfloat16, 25), 1, False
+    else:
+        x, dim, h2f = rand((50, 6, 7), torch.float32, 26), 0, False
+    ref = (aten.log_softmax if log else aten.softmax)(x, dim, h2f)
+    out = empty_like_ref(ref)
+    (_abi.log_softmax if log else _abi.softmax)(out, dev(x), dim)
+    kind = "bf16" if ref.dtype == torch.bfloat16 else "fp32"
+    assert_close(out, ref, kind, f"softmax {case}")
+
+
+# ---- fused efficient ops ----------------------------------------------------------
+
+def test_config3_rms_norm_rope_silu_mul_reduced_tokens():
+    c = synthetic.config3(tokens=1024)
+    ref = aten.rms_norm(c["x"], c["w"], c["eps"])
+    out = empty_like_ref(ref)
+    _abi.rms_norm(out, dev(c["x"]), dev(c["w"]), c["eps"])
+    assert_close(out, ref, "bf16", "rms_norm")
+    # torch.rms_norm itself (identical on CPU)
+    assert_close(out, torch.rms_norm(c["x"], [4096], c["w"], c["eps"]), "bf16", "torch.rms_norm")
+    qo = torch.empty_like(dev(c["q"]))
+    ko = torch.empty_like(qo)
+    _abi.rope(qo, ko, dev(c["q"]), dev(c["k"]), dev(c["pos"]), c["theta"])
+    assert_close(qo, aten.rope(c["q"], c["pos"], c["theta"]), "bf16", "rope q")
+    assert_close(ko, aten.rope(c["k"], c["pos"], c["theta"]), "bf16", "rope k")
+    ref = aten.silu_mul(c["gate"], c["up"])
+    out = empty_like_ref(ref)
+    _abi.silu_mul(out, dev(c["gate"]), dev(c["up"]))
+    assert_close(out, ref, "bf16", "silu_mul")
+
+
+def test_config3_full_size():
+    c = synthetic.config3()
+    out = torch.empty(c["x"].shape, dtype=torch.bfloat16, device=DEV)
+    _abi.rms_norm(out, dev(c["x"]), dev(c["w"]), c["eps"])
+    assert_close(out, aten.rms_norm(c["x"], c["w"], c["eps"]), "bf16", "rms_norm full")
+    q = dev(c["q"])
+    _abi.rope(q, None, q, None, dev(c["pos"]), c["theta"])  # in place, q only
+    assert_close(q, aten.rope(c["q"], c["pos"], c["theta"]), "bf16", "rope full")
+    out = torch.empty(c["gate"].shape, dtype=torch.bfloat16, device=DEV)
+    _abi.silu_mul(out, dev(c["gate"]), dev(c["up"]))
+    assert_close(out, aten.silu_mul(c["gate"], c["up"]), "bf16", "silu_mul full")
+
+
+def test_fused_edge_cases():
+    # rms_norm without weight, fp32, odd width (block path), strided rows
+    x = rand((9, 1000), torch.float32, 27)
+    out = torch.empty(9, 1000, device=DEV)
+    _abi.rms_norm(out, dev(x), None, 1e-5)
+    assert_close(out, aten.rms_norm(x, None, 1e-5), "fp32", "rms_norm no weight")
+    big = rand((9, 2048), torch.bfloat16, 28)
+    view = big[:, :1024]
+    w = rand((1024,), torch.bfloat16, 29)
+    out = torch.empty(9, 1024, dtype=torch.bfloat16, device=DEV)
+    _abi.rms_norm(out, _strided_on_device(view), dev(w), 1e-6)
+    assert_close(out, aten.rms_norm(view, w, 1e-6), "bf16", "rms_norm strided rows")
+    # rope: position 0 is the identity; GQA k with fewer heads
+    q = rand((4, 8, 64), torch.bfloat16, 30)
+    k = rand((4, 2, 64), torch.bfloat16, 31)
+    pos = torch.tensor([0, 1, 2, 4095])
+    qo, ko = torch.empty_like(dev(q)), torch.empty_like(dev(k))
+    _abi.rope(qo, ko, dev(q), dev(k), dev(pos.int()), 10000.0)
+    assert torch.equal(qo[0].cpu(), q[0])
+    assert_close(ko, aten.rope(k, pos, 10000.0), "bf16", "rope gqa k")
+    # silu_mul: ragged tail and strided gate
+    gt = rand((3, 1001), torch.bfloat16, 32)
+    up = rand((3, 1001), torch.bfloat16, 33)
+    out = torch.empty(3, 1001, dtype=torch.bfloat16, device=DEV)
+    _abi.silu_mul(out, dev(gt), dev(up))
+    assert_close(out, aten.silu_mul(gt, up), "bf16", "silu_mul ragged")

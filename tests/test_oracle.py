@@ -1,0 +1,182 @@
+"""Pins the CPU oracle before it is trusted (CPU only).
+
+Each oracle function is checked against something that does not share its
+code: a numpy restatement, a closed form, an invariant, brute force on tiny
+inputs, or a committed golden fixture.  A planted mistake (dropped term,
+wrong sign, swapped half, transposed operand) fails at least one of them,
+see test_planted_mistakes_are_caught.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import aten, numpy_ref as npr
+from oracle.tolerance import assert_close, assert_exact
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def g(seed=0):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---- config 1 -----------------------------------------------------------------
+
+def test_mul_add_bit_exact_vs_numpy():
+    a = torch.rand(257, 129, generator=g(1)) * 2 - 1
+    b = torch.rand(129, generator=g(2)) * 2 - 1
+    got = aten.add(aten.mul(a, b), 0.5)
+    want = npr.add(npr.mul(a.numpy(), b.numpy()), np.float32(0.5))
+    assert_exact(got, torch.from_numpy(want), "a*b+0.5")
+
+
+def test_add_alpha_and_sub_vs_numpy():
+    a = torch.randn(1000, generator=g(3))
+    b = torch.randn(1000, generator=g(4))
+    # alpha = 1 and -1 are single roundings
+    assert_exact(aten.sub(a, b), torch.from_numpy(np.subtract(a.numpy(), b.numpy())), "sub")
+    assert_exact(aten.div(a, b), torch.from_numpy(np.divide(a.numpy(), b.numpy())), "div")
+
+
+def test_index_select_vs_numpy_and_brute_force():
+    table = torch.randint(-2**63, 2**63 - 1, (1000, 8), generator=g(5), dtype=torch.int64)
+    idx = torch.randint(0, 1000, (300,), generator=g(6), dtype=torch.int64)
+    got = aten.index_select(table, 0, idx)
+    assert_exact(got, torch.from_numpy(npr.index_select(table.numpy(), 0, idx.numpy())), "take")
+    small = table[:7]
+    sidx = torch.tensor([6, 0, 0, 3, 6], dtype=torch.int64)
+    assert_exact(aten.index_select(small, 0, sidx),
+                 torch.from_numpy(npr.index_select_brute(small.numpy(), sidx.numpy())), "brute")
+    # dim 1 gather
+    assert_exact(aten.index_select(table, 1, torch.tensor([7, 1])),
+                 torch.from_numpy(table.numpy()[:, [7, 1]]), "dim1")
+
+
+# ---- config 2 -------------------------------------------------------------------
+
+def test_sum_amax_bf16_vs_float64():
+    x = (torch.randn(64, 3000, generator=g(7)) * 4).bfloat16()
+    s = aten.sum_(x, -1)
+    assert s.dtype == torch.bfloat16
+    ref = torch.from_numpy(npr.sum64(x.float().numpy(), -1)).bfloat16()
+    assert_close(s, ref, "bf16", "sum")
+    assert_exact(aten.amax(x, -1), torch.from_numpy(x.float().numpy().max(-1)).bfloat16(), "amax")
+
+
+def test_sum_constant_row_closed_form_and_spike():
+    x = torch.full((4, 32000), 0.25, dtype=torch.bfloat16)
+    assert_exact(aten.sum_(x, -1), torch.full((4,), 8000.0, dtype=torch.bfloat16), "N*c")
+    y = torch.zeros(3, 32000, dtype=torch.bfloat16)
+    y[1, 12345] = 7.5
+    assert_exact(aten.amax(y, -1), torch.tensor([0.0, 7.5, 0.0], dtype=torch.bfloat16), "spike")
+
+
+def test_mean_dim0_vs_float64():
+    m = torch.randn(2048, 256, generator=g(8))
+    got = aten.mean(m, 0)
+    ref = torch.from_numpy(npr.mean64(m.numpy(), 0)).float()
+    assert_close(got, ref, "fp32", "mean0")
+
+
+def test_log_softmax_vs_float64_and_invariants():
+    x = (torch.randn(16, 32000, generator=g(9)) * 4).bfloat16()
+    got = aten.log_softmax(x, -1)
+    ref = torch.from_numpy(npr.log_softmax64(x.float().numpy())).bfloat16()
+    assert_close(got, ref, "bf16", "log_softmax")
+    # constant row: every entry is -ln(N)
+    c = torch.full((2, 32000), 3.0)
+    assert torch.allclose(aten.log_softmax(c, -1), torch.full((2, 32000), -math.log(32000.0)))
+    # logsumexp of each output row is 0
+    lse = torch.logsumexp(aten.log_softmax(x.float(), -1).double(), -1)
+    assert lse.abs().max().item() < 1e-5
+    sm = aten.softmax(x.float(), -1)
+    assert (sm.double().sum(-1) - 1).abs().max().item() < 1e-5
+    assert_close(sm, torch.from_numpy(npr.softmax64(x.float().numpy())).float(), "fp32", "softmax")
+
+
+# ---- config 3 ------------------------------------------------------------------
+
+def test_rms_norm_matches_torch_rms_norm_exactly():
+    x = torch.randn(32, 4096, generator=g(10)).bfloat16()
+    w = (torch.randn(4096, generator=g(11)) * 0.02 + 1).bfloat16()
+    assert_exact(aten.rms_norm(x, w, 1e-6), torch.rms_norm(x, [4096], w, 1e-6), "rms_norm")
+    ref = torch.from_numpy(npr.rms_norm64(x.float().numpy(), w.float().numpy(), 1e-6)).bfloat16()
+    assert_close(aten.rms_norm(x, w, 1e-6), ref, "bf16", "rms_norm64")
+
+
+def test_rope_invariants_and_float64():
+    q = torch.randn(64, 4, 128, generator=g(12))
+    pos = torch.arange(64) * 61
+    out = aten.rope(q, pos, 10000.0)
+    # position 0 is the identity
+    assert torch.equal(out[0], q[0])
+    # each (i, i + d/2) pair keeps its norm
+    h = 64
+    n_in = q[..., :h] ** 2 + q[..., h:] ** 2
+    n_out = out[..., :h] ** 2 + out[..., h:] ** 2
+    assert torch.allclose(n_in, n_out, rtol=1e-4, atol=1e-5)
+    # fp32 angles at positions up to ~3900 carry ~1e-4 absolute error
+    ref = torch.from_numpy(npr.rope64(q.numpy(), pos.numpy(), 10000.0)).float()
+    assert (out.double() - ref.double()).abs().max().item() < 2e-3
+    # rotating by p then by -p is the identity (composition law)
+    back = aten.rope(out, -pos, 10000.0)
+    assert torch.allclose(back, q, atol=1e-4)
+
+
+def test_silu_mul_vs_float64():
+    gt = torch.randn(64, 1000, generator=g(13)).bfloat16()
+    up = torch.randn(64, 1000, generator=g(14)).bfloat16()
+    ref = torch.from_numpy(npr.silu_mul64(gt.float().numpy(), up.float().numpy())).bfloat16()
+    assert_close(aten.silu_mul(gt, up), ref, "bf16", "silu_mul")
+    # silu(0) = 0, silu(x) -> x for large x
+    z = torch.tensor([0.0, 20.0, -20.0])
+    assert torch.allclose(aten.silu_mul(z, torch.ones(3)), torch.tensor([0.0, 20.0, -20.0 * math.exp(-20)]),
+                          atol=1e-6)
+
+
+@pytest.mark.parametrize("name", ["rms_norm", "rope", "silu_mul"])
+def test_golden_fixtures(name):
+    path = os.path.join(GOLDEN, f"{name}.npz")
+    data = np.load(path)
+    if name == "rms_norm":
+        got = aten.rms_norm(torch.from_numpy(data["x"]), torch.from_numpy(data["w"]),
+                            float(data["eps"]))
+    elif name == "rope":
+        got = aten.rope(torch.from_numpy(data["x"]), torch.from_numpy(data["pos"]),
+                        float(data["theta"]))
+    else:
+        got = aten.silu_mul(torch.from_numpy(data["gate"]), torch.from_numpy(data["up"]))
+    want = torch.from_numpy(data["expected"])
+    if name == "rope":
+        # the fp32 closed form rounds pos * inv_freq to fp32: at pos 4095 the
+        # angle is off by up to 4095 * 2^-24 rad, so compare absolutely
+        assert (got.double() - want.double()).abs().max().item() < 1e-3
+    else:
+        assert_close(got, want, "fp32", name)
+
+
+def test_planted_mistakes_are_caught():
+    """Mutated oracles must fail the same pins."""
+    q = torch.randn(8, 2, 16, generator=g(15))
+    pos = torch.arange(8)
+    ref = torch.from_numpy(npr.rope64(q.numpy(), pos.numpy(), 10000.0)).float()
+
+    def rope_wrong_sign(x, p, th):
+        d = x.shape[-1]
+        h = d // 2
+        cos, sin = aten.rope_tables(p, d, th)
+        x1, x2 = x[..., :h], x[..., h:]
+        return torch.cat([x1 * cos[:, None] + x2 * sin[:, None], x2 * cos[:, None] + x1 * sin[:, None]], -1)
+
+    assert (rope_wrong_sign(q, pos, 10000.0) - ref).abs().max() > 1e-2
+    x = torch.randn(4, 64, generator=g(16))
+    ref_rms = torch.from_numpy(npr.rms_norm64(x.numpy(), None, 1e-6)).float()
+    dropped_mean = x * torch.rsqrt(x.pow(2).sum(-1, keepdim=True) + 1e-6)
+    assert (dropped_mean - ref_rms).abs().max() > 1e-2
+    table = torch.arange(36).reshape(6, 6)
+    idx = torch.tensor([3, 1, 5])
+    want = torch.from_numpy(npr.index_select(table.numpy(), 0, idx.numpy()))
+    assert not torch.equal(aten.index_select(table, 1, idx), want)  # transposed gather

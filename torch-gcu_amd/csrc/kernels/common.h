@@ -1,0 +1,265 @@
+// Shared device and host helpers of the gfx950 kernel library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "mi355x_ops.h"
+
+namespace mi {
+
+// ---- errors -----------------------------------------------------------------
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+struct Status {
+  mi_status_t code;
+};
+
+#define MI_FAIL(code, ...)     \
+  do {                         \
+    ::mi::set_error(__VA_ARGS__); \
+    return (code);             \
+  } while (0)
+
+#define MI_CHECK_ARG(cond, ...)                        \
+  do {                                                 \
+    if (!(cond)) MI_FAIL(MI_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define MI_RETURN_IF(expr)              \
+  do {                                  \
+    mi_status_t _st = (expr);           \
+    if (_st != MI_OK) return _st;       \
+  } while (0)
+
+// Checks the launch just enqueued.
+mi_status_t check_launch(const char* what);
+
+// ---- workspace ----------------------------------------------------------------
+
+// RAII workspace from the registered allocator.
+class Workspace {
+ public:
+  Workspace() = default;
+  ~Workspace();
+  mi_status_t alloc(size_t bytes, hipStream_t stream);
+  void* get() const { return ptr_; }
+  Workspace(const Workspace&) = delete;
+  Workspace& operator=(const Workspace&) = delete;
+
+ private:
+  void* ptr_ = nullptr;
+  hipStream_t stream_ = nullptr;
+};
+
+int cu_count();
+
+// ---- dtypes -------------------------------------------------------------------
+
+inline int dtype_size(int dt) {
+  switch (dt) {
+    case MI_U8: case MI_I8: case MI_BOOL: return 1;
+    case MI_I16: case MI_F16: case MI_BF16: return 2;
+    case MI_I32: case MI_F32: return 4;
+    case MI_I64: case MI_F64: return 8;
+    default: return 0;
+  }
+}
+inline bool dtype_valid(int dt) { return dtype_size(dt) != 0; }
+inline bool is_floating(int dt) {
+  return dt == MI_F16 || dt == MI_BF16 || dt == MI_F32 || dt == MI_F64;
+}
+inline bool is_integral(int dt, bool include_bool) {
+  return dt == MI_U8 || dt == MI_I8 || dt == MI_I16 || dt == MI_I32 ||
+         dt == MI_I64 || (include_bool && dt == MI_BOOL);
+}
+const char* dtype_name(int dt);
+
+// ATen's promoteTypes over the dtypes above (c10/core/ScalarType.cpp).
+int promote_types(int a, int b);
+
+// ---- tensor views --------------------------------------------------------------
+
+inline int64_t numel(const mi_tensor_t& t) {
+  int64_t n = 1;
+  for (int i = 0; i < t.ndim; ++i) n *= t.sizes[i];
+  return n;
+}
+bool is_contiguous(const mi_tensor_t& t);
+mi_status_t validate(const mi_tensor_t* t, const char* name);
+
+// ---- device-side numerics ---------------------------------------------------
+
+typedef uint16_t bf16_t;
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(((uint32_t)v) << 16);
+}
+// Round to nearest even (hardware v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(bf16_t, b);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t v) {
+  return (float)__builtin_bit_cast(_Float16, v);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Storage type tags used by templated kernels.
+struct BF16 {
+  typedef uint16_t storage;
+};
+struct F16 {
+  typedef uint16_t storage;
+};
+
+template <typename S>
+struct Num;  // storage -> compute conversions
+template <>
+struct Num<float> {
+  typedef float storage;
+  typedef float acc;
+  static __device__ __forceinline__ float load(float v) { return v; }
+  static __device__ __forceinline__ float store(float v) { return v; }
+};
+template <>
+struct Num<double> {
+  typedef double storage;
+  typedef double acc;
+  static __device__ __forceinline__ double load(double v) { return v; }
+  static __device__ __forceinline__ double store(double v) { return v; }
+};
+template <>
+struct Num<BF16> {
+  typedef uint16_t storage;
+  typedef float acc;
+  static __device__ __forceinline__ float load(uint16_t v) { return bf16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t store(float v) { return f32_to_bf16(v); }
+};
+template <>
+struct Num<F16> {
+  typedef uint16_t storage;
+  typedef float acc;
+  static __device__ __forceinline__ float load(uint16_t v) { return f16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t store(float v) { return f32_to_f16(v); }
+};
+
+// Loads element `idx` of a buffer of runtime dtype `dt` as C.
+template <typename C>
+__device__ __forceinline__ C load_as(const void* p, int64_t idx, int dt) {
+  switch (dt) {
+    case MI_U8: return (C)((const uint8_t*)p)[idx];
+    case MI_I8: return (C)((const int8_t*)p)[idx];
+    case MI_I16: return (C)((const int16_t*)p)[idx];
+    case MI_I32: return (C)((const int32_t*)p)[idx];
+    case MI_I64: return (C)((const int64_t*)p)[idx];
+    case MI_F16: return (C)f16_to_f32(((const uint16_t*)p)[idx]);
+    case MI_BF16: return (C)bf16_to_f32(((const uint16_t*)p)[idx]);
+    case MI_F32: return (C)((const float*)p)[idx];
+    case MI_F64: return (C)((const double*)p)[idx];
+    case MI_BOOL: return (C)(((const uint8_t*)p)[idx] != 0);
+    default: return (C)0;
+  }
+}
+
+// Stores `v` (compute type C) into element `idx` of a buffer of dtype dt,
+// converting the way c10::convert does (float to f16/bf16 rounds to nearest
+// even; anything to bool tests != 0).
+template <typename C>
+__device__ __forceinline__ void store_as(void* p, int64_t idx, int dt, C v) {
+  switch (dt) {
+    case MI_U8: ((uint8_t*)p)[idx] = (uint8_t)(int64_t)v; break;
+    case MI_I8: ((int8_t*)p)[idx] = (int8_t)(int64_t)v; break;
+    case MI_I16: ((int16_t*)p)[idx] = (int16_t)(int64_t)v; break;
+    case MI_I32: ((int32_t*)p)[idx] = (int32_t)(int64_t)v; break;
+    case MI_I64: ((int64_t*)p)[idx] = (int64_t)v; break;
+    case MI_F16: ((uint16_t*)p)[idx] = f32_to_f16((float)v); break;
+    case MI_BF16: ((uint16_t*)p)[idx] = f32_to_bf16((float)v); break;
+    case MI_F32: ((float*)p)[idx] = (float)v; break;
+    case MI_F64: ((double*)p)[idx] = (double)v; break;
+    case MI_BOOL: ((uint8_t*)p)[idx] = (v != (C)0) ? 1 : 0; break;
+    default: break;
+  }
+}
+
+// ---- wavefront / block reductions (wave64) -----------------------------------
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    T o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// NaN-propagating max, as ATen's max_impl: a NaN operand wins.
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return (a != a || a > b) ? a : b;
+}
+__device__ __forceinline__ double nan_max(double a, double b) {
+  return (a != a || a > b) ? a : b;
+}
+template <typename T>
+__device__ __forceinline__ T nan_max(T a, T b) {
+  return a > b ? a : b;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_nan_max(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = nan_max(v, (T)__shfl_xor(v, off, 64));
+  return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024); every thread gets
+// the result.  `red` is LDS scratch of at least 16 entries.
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  T r = lane < nw ? red[lane] : (T)0;
+  return wave_sum(r);
+}
+template <typename T>
+__device__ __forceinline__ T block_nan_max(T v, T* red, T ident) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  v = wave_nan_max(v);
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  T r = lane < nw ? red[lane] : ident;
+  return wave_nan_max(r);
+}
+
+// Fast exp/log on the hardware exp2/log2 units (about 1 ulp in fp32).
+__device__ __forceinline__ float fast_exp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+__device__ __forceinline__ float fast_log(float x) {
+  return __builtin_amdgcn_logf(x) * 0.6931471805599453f;
+}
+
+inline unsigned ceil_div_u(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace mi

@@ -1,0 +1,653 @@
+// Elementwise engine: binary arithmetic (add/sub/mul/div), dtype-converting
+// strided copy and fill.
+//
+// Paths, chosen on the host after broadcasting and coalescing (iter.cpp):
+//   - "2-D" path: out is dense [R, C] and every input is dense [R, C], a row
+//     vector [C] broadcast over rows, a column vector [R] broadcast over
+//     columns, or a single value; all of one dtype.  Each thread moves
+//     UNROLL x 16-byte vectors per pass, so one wave issues 4 KiB of loads
+//     per operand at once.  Config 1's a*b with b [4096] broadcast over rows
+//     and +0.5 are this path.
+//   - general path: any strides, any mix of dtypes (loads convert to the
+//     compute type, as TensorIterator's dynamic casting does).
+#include <cstring>
+
+#include "iter.h"
+
+namespace mi {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+enum OpKind { OP_ADD = 0, OP_MUL = 1, OP_DIV = 2 };
+enum Mode { M_FULL = 0, M_ROW = 1, M_COL = 2, M_SCALAR = 3 };
+
+template <int OP, typename A>
+__device__ __forceinline__ A apply(A a, A b, A alpha) {
+  if constexpr (OP == OP_ADD) {
+    if constexpr (std::is_same<A, float>::value) return __builtin_fmaf(b, alpha, a);
+    else if constexpr (std::is_same<A, double>::value) return __builtin_fma(b, alpha, a);
+    else return (A)((uint64_t)a + (uint64_t)alpha * (uint64_t)b);  // wraps
+  } else if constexpr (OP == OP_MUL) {
+    if constexpr (std::is_integral<A>::value) return (A)((uint64_t)a * (uint64_t)b);
+    else return a * b;
+  } else {
+    return a / b;
+  }
+}
+
+// Storage helpers for the typed fast path.
+template <typename Tag>
+struct TypeOf {
+  typedef Tag storage;
+  typedef Tag acc;
+  static __device__ __forceinline__ acc load(storage v) { return v; }
+  static __device__ __forceinline__ storage store(acc v) { return v; }
+};
+template <>
+struct TypeOf<BF16> : Num<BF16> {};
+template <>
+struct TypeOf<F16> : Num<F16> {};
+template <>
+struct TypeOf<int32_t> {
+  typedef int32_t storage;
+  typedef int64_t acc;
+  static __device__ __forceinline__ acc load(storage v) { return v; }
+  static __device__ __forceinline__ storage store(acc v) { return (storage)v; }
+};
+
+template <typename Tag>
+struct Arg2D {
+  const typename TypeOf<Tag>::storage* p;
+  typename TypeOf<Tag>::acc imm;  // used when mode is scalar and p == NULL
+  int mode;
+};
+
+// out[R, C] = op(a, b) with each input in one of the Mode layouts.
+template <typename Tag, int OP>
+__global__ __launch_bounds__(kBlock) void binary_2d_kernel(
+    typename TypeOf<Tag>::storage* __restrict__ out, Arg2D<Tag> a, Arg2D<Tag> b,
+    typename TypeOf<Tag>::acc alpha, int64_t rows, int64_t cols) {
+  typedef typename TypeOf<Tag>::storage St;
+  typedef typename TypeOf<Tag>::acc Acc;
+  constexpr int VEC = 16 / sizeof(St);
+  union V {
+    uint4 u;
+    St s[VEC];
+  };
+  const int64_t vcols = cols / VEC;
+  const int64_t nvec = rows * vcols;
+  const int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x;
+
+  Acc sa = a.imm, sb = b.imm;
+  if (a.mode == M_SCALAR && a.p) sa = TypeOf<Tag>::load(a.p[0]);
+  if (b.mode == M_SCALAR && b.p) sb = TypeOf<Tag>::load(b.p[0]);
+
+  V va[kUnroll], vb[kUnroll];
+  int64_t rowv[kUnroll], colv[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t v = base + (int64_t)u * kBlock;
+    if (v < nvec) {
+      int64_t r = 0, c = v;
+      if (rows > 1) {
+        r = v / vcols;
+        c = v - r * vcols;
+      }
+      rowv[u] = r;
+      colv[u] = c;
+      if (a.mode == M_FULL) va[u].u = ((const uint4*)a.p)[v];
+      else if (a.mode == M_ROW) va[u].u = ((const uint4*)a.p)[c];
+      if (b.mode == M_FULL) vb[u].u = ((const uint4*)b.p)[v];
+      else if (b.mode == M_ROW) vb[u].u = ((const uint4*)b.p)[c];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t v = base + (int64_t)u * kBlock;
+    if (v < nvec) {
+      Acc ca = sa, cb = sb;
+      if (a.mode == M_COL) ca = TypeOf<Tag>::load(a.p[rowv[u]]);
+      if (b.mode == M_COL) cb = TypeOf<Tag>::load(b.p[rowv[u]]);
+      V o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const Acc x = (a.mode == M_FULL || a.mode == M_ROW) ? TypeOf<Tag>::load(va[u].s[e]) : ca;
+        const Acc y = (b.mode == M_FULL || b.mode == M_ROW) ? TypeOf<Tag>::load(vb[u].s[e]) : cb;
+        o.s[e] = TypeOf<Tag>::store(apply<OP, Acc>(x, y, alpha));
+      }
+      ((uint4*)out)[v] = o.u;
+    }
+  }
+}
+
+// General strided path with dynamic dtypes; C is the compute type.
+template <typename C, int OP>
+__global__ __launch_bounds__(kBlock) void binary_general_kernel(
+    char* out, int dt_out, const char* a, int dt_a, const char* b, int dt_b,
+    C sa, C sb, int a_imm, int b_imm, C alpha, int round_a, int round_b,
+    OffsetCalc<3> oc, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    int64_t off[3];
+    oc.get(i, off);
+    C x = a_imm ? sa : load_as<C>(a, off[1], dt_a);
+    C y = b_imm ? sb : load_as<C>(b, off[2], dt_b);
+    // Inputs of another dtype are first cast to the common dtype
+    // (TensorIterator's promote_inputs_to_common_dtype).
+    if constexpr (std::is_same<C, float>::value) {
+      if (round_a == MI_BF16) x = bf16_to_f32(f32_to_bf16(x));
+      else if (round_a == MI_F16) x = f16_to_f32(f32_to_f16(x));
+      if (round_b == MI_BF16) y = bf16_to_f32(f32_to_bf16(y));
+      else if (round_b == MI_F16) y = f16_to_f32(f32_to_f16(y));
+    }
+    store_as<C>(out, off[0], dt_out, apply<OP, C>(x, y, alpha));
+  }
+}
+
+// ---- copy ----------------------------------------------------------------------
+
+template <typename V>
+__device__ __forceinline__ void store_value(char* p, int64_t idx, int dt, V v) {
+  store_as<V>(p, idx, dt, v);
+}
+
+// c10::convert semantics: float -> uint8 goes through int64.
+__device__ __forceinline__ void convert_elem(const char* src, int64_t si, int sdt, char* dst,
+                                             int64_t di, int ddt) {
+  switch (sdt) {
+    case MI_U8: store_value<int64_t>(dst, di, ddt, ((const uint8_t*)src)[si]); break;
+    case MI_I8: store_value<int64_t>(dst, di, ddt, ((const int8_t*)src)[si]); break;
+    case MI_I16: store_value<int64_t>(dst, di, ddt, ((const int16_t*)src)[si]); break;
+    case MI_I32: store_value<int64_t>(dst, di, ddt, ((const int32_t*)src)[si]); break;
+    case MI_I64: {
+      const int64_t v = ((const int64_t*)src)[si];
+      if (ddt == MI_F32) ((float*)dst)[di] = (float)v;
+      else if (ddt == MI_F16) ((uint16_t*)dst)[di] = f32_to_f16((float)v);
+      else if (ddt == MI_BF16) ((uint16_t*)dst)[di] = f32_to_bf16((float)v);
+      else store_value<int64_t>(dst, di, ddt, v);
+      break;
+    }
+    case MI_BOOL: store_value<int64_t>(dst, di, ddt, ((const uint8_t*)src)[si] != 0); break;
+    case MI_F16: store_value<float>(dst, di, ddt, f16_to_f32(((const uint16_t*)src)[si])); break;
+    case MI_BF16: store_value<float>(dst, di, ddt, bf16_to_f32(((const uint16_t*)src)[si])); break;
+    case MI_F32: store_value<float>(dst, di, ddt, ((const float*)src)[si]); break;
+    case MI_F64: {
+      const double v = ((const double*)src)[si];
+      if (ddt == MI_F16) ((uint16_t*)dst)[di] = f32_to_f16((float)v);
+      else if (ddt == MI_BF16) ((uint16_t*)dst)[di] = f32_to_bf16((float)v);
+      else store_value<double>(dst, di, ddt, v);
+      break;
+    }
+    default: break;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void copy_general_kernel(char* out, int dt_out,
+                                                              const char* src, int dt_src,
+                                                              OffsetCalc<2> oc, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    int64_t off[2];
+    oc.get(i, off);
+    convert_elem(src, off[1], dt_src, out, off[0], dt_out);
+  }
+}
+
+// Same-dtype strided copy moving raw elements of size sizeof(T).
+template <typename T>
+__global__ __launch_bounds__(kBlock) void copy_raw_kernel(T* out, const T* src,
+                                                          OffsetCalc<2> oc, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    int64_t off[2];
+    oc.get(i, off);
+    out[off[0]] = src[off[1]];
+  }
+}
+
+// Contiguous float <-> half/bfloat16 conversion, 8 elements per thread.
+template <typename SrcTag, typename DstTag>
+__global__ __launch_bounds__(kBlock) void convert_contig_kernel(
+    typename TypeOf<DstTag>::storage* __restrict__ out,
+    const typename TypeOf<SrcTag>::storage* __restrict__ src, int64_t n) {
+  const int64_t i0 = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 8;
+  if (i0 + 8 <= n) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      out[i0 + e] = TypeOf<DstTag>::store((typename TypeOf<DstTag>::acc)TypeOf<SrcTag>::load(src[i0 + e]));
+  } else {
+    for (int64_t i = i0; i < n; ++i)
+      out[i] = TypeOf<DstTag>::store((typename TypeOf<DstTag>::acc)TypeOf<SrcTag>::load(src[i]));
+  }
+}
+
+// ---- fill ------------------------------------------------------------------------
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void fill_contig_kernel(T* out, T v, int64_t n) {
+  constexpr int VEC = 16 / sizeof(T);
+  union U {
+    uint4 u;
+    T s[VEC];
+  } pack;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) pack.s[e] = v;
+  const int64_t nvec = n / VEC;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nvec; i += stride)
+    ((uint4*)out)[i] = pack.u;
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (t < n - nvec * VEC) out[nvec * VEC + t] = v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void fill_strided_kernel(T* out, T v, OffsetCalc<1> oc,
+                                                              int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    int64_t off[1];
+    oc.get(i, off);
+    out[off[0]] = v;
+  }
+}
+
+unsigned grid_for(int64_t n) {
+  const int64_t want = (n + kBlock - 1) / kBlock;
+  const int64_t cap = (int64_t)cu_count() * 32;
+  return (unsigned)(want < cap ? (want < 1 ? 1 : want) : cap);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Classifies a 2-D iterator operand.
+int mode_2d(const Iter& it, int o, int64_t rows, int64_t cols) {
+  const int64_t s0 = it.ndim == 2 ? it.strides[o][0] : 0;
+  const int64_t s1 = it.ndim == 2 ? it.strides[o][1] : it.strides[o][0];
+  if (s0 == cols && s1 == 1) return M_FULL;
+  if (s0 == 0 && s1 == 1) return M_ROW;
+  if (s0 == 1 && s1 == 0) return M_COL;
+  if (s0 == 0 && s1 == 0) return M_SCALAR;
+  (void)rows;
+  return -1;
+}
+
+struct BinArgs {
+  const mi_tensor_t* out;
+  const mi_tensor_t* a;  // may be NULL when a_scalar is used
+  const mi_tensor_t* b;
+  const mi_scalar_t* a_scalar;
+  const mi_scalar_t* b_scalar;
+  double alpha_f;
+  int64_t alpha_i;
+  int common;  // common dtype
+  int op;
+  bool scalar_round_to_common;  // cast host scalars to the common dtype first
+};
+
+template <typename Tag, int OP>
+mi_status_t launch_2d(const Iter& it, int ia, int ib, const BinArgs& ba, hipStream_t stream) {
+  typedef typename TypeOf<Tag>::storage St;
+  typedef typename TypeOf<Tag>::acc Acc;
+  constexpr int VEC = 16 / sizeof(St);
+  const int64_t rows = it.ndim == 2 ? it.sizes[0] : 1;
+  const int64_t cols = it.ndim == 2 ? it.sizes[1] : it.sizes[0];
+  Arg2D<Tag> a{nullptr, Acc(0), M_SCALAR}, b{nullptr, Acc(0), M_SCALAR};
+  auto fill = [&](Arg2D<Tag>& arg, int idx, const mi_scalar_t* s) {
+    if (idx >= 0) {
+      arg.p = (const St*)it.data[idx];
+      arg.mode = mode_2d(it, idx, rows, cols);
+    } else {
+      double v = scalar_as_double(*s);
+      if (std::is_integral<Acc>::value) {
+        arg.imm = (Acc)scalar_as_int(*s);
+      } else {
+        if (ba.scalar_round_to_common) {
+          if (ba.common == MI_BF16) v = host_bf16_to_f32(host_f32_to_bf16((float)v));
+          else if (ba.common == MI_F16) v = host_f16_to_f32(host_f32_to_f16((float)v));
+        }
+        arg.imm = (Acc)v;
+      }
+    }
+  };
+  fill(a, ia, ba.a_scalar);
+  fill(b, ib, ba.b_scalar);
+  Acc alpha;
+  if (std::is_integral<Acc>::value) alpha = (Acc)ba.alpha_i;
+  else {
+    double al = ba.alpha_f;
+    if (ba.common == MI_BF16) al = host_bf16_to_f32(host_f32_to_bf16((float)al));
+    else if (ba.common == MI_F16) al = host_f16_to_f32(host_f32_to_f16((float)al));
+    alpha = (Acc)al;
+  }
+  const int64_t nvec = rows * (cols / VEC);
+  const unsigned grid = ceil_div_u(nvec, (int64_t)kBlock * kUnroll);
+  hipLaunchKernelGGL((binary_2d_kernel<Tag, OP>), dim3(grid < 1 ? 1 : grid), dim3(kBlock), 0,
+                     stream, (St*)it.data[0], a, b, alpha, rows, cols);
+  return check_launch("binary_2d");
+}
+
+template <typename Tag>
+mi_status_t dispatch_2d_op(const Iter& it, int ia, int ib, const BinArgs& ba, hipStream_t s) {
+  switch (ba.op) {
+    case OP_ADD: return launch_2d<Tag, OP_ADD>(it, ia, ib, ba, s);
+    case OP_MUL: return launch_2d<Tag, OP_MUL>(it, ia, ib, ba, s);
+    default: return launch_2d<Tag, OP_DIV>(it, ia, ib, ba, s);
+  }
+}
+
+template <typename C, int OP>
+mi_status_t launch_general_t(const Iter& it, int ia, int ib, const BinArgs& ba, C sa, C sb,
+                             C alpha, hipStream_t stream) {
+  OffsetCalc<3> oc;
+  oc.ndim = it.ndim;
+  for (int d = 0; d < MI_MAX_DIMS; ++d) {
+    oc.sizes[d] = d < it.ndim ? it.sizes[d] : 1;
+    oc.strides[0][d] = d < it.ndim ? it.strides[0][d] : 0;
+    oc.strides[1][d] = (ia >= 0 && d < it.ndim) ? it.strides[ia][d] : 0;
+    oc.strides[2][d] = (ib >= 0 && d < it.ndim) ? it.strides[ib][d] : 0;
+  }
+  const int dta = ia >= 0 ? it.dtype[ia] : -1, dtb = ib >= 0 ? it.dtype[ib] : -1;
+  const int ra = (ia >= 0 && dta != ba.common) ? ba.common : -1;
+  const int rb = (ib >= 0 && dtb != ba.common) ? ba.common : -1;
+  hipLaunchKernelGGL((binary_general_kernel<C, OP>), dim3(grid_for(it.numel)), dim3(kBlock), 0,
+                     stream, it.data[0], it.dtype[0], ia >= 0 ? it.data[ia] : nullptr, dta,
+                     ib >= 0 ? it.data[ib] : nullptr, dtb, sa, sb, ia < 0 ? 1 : 0,
+                     ib < 0 ? 1 : 0, alpha, ra, rb, oc, it.numel);
+  return check_launch("binary_general");
+}
+
+template <typename C>
+mi_status_t launch_general(const Iter& it, int ia, int ib, const BinArgs& ba, hipStream_t s) {
+  auto sval = [&](const mi_scalar_t* sc) -> C {
+    if (sc == nullptr) return C(0);
+    if (std::is_integral<C>::value) return (C)scalar_as_int(*sc);
+    double v = scalar_as_double(*sc);
+    if (ba.scalar_round_to_common) {
+      if (ba.common == MI_BF16) v = host_bf16_to_f32(host_f32_to_bf16((float)v));
+      else if (ba.common == MI_F16) v = host_f16_to_f32(host_f32_to_f16((float)v));
+    }
+    return (C)v;
+  };
+  C alpha;
+  if (std::is_integral<C>::value) alpha = (C)ba.alpha_i;
+  else {
+    double al = ba.alpha_f;
+    if (ba.common == MI_BF16) al = host_bf16_to_f32(host_f32_to_bf16((float)al));
+    else if (ba.common == MI_F16) al = host_f16_to_f32(host_f32_to_f16((float)al));
+    alpha = (C)al;
+  }
+  const C sa = sval(ba.a_scalar), sb = sval(ba.b_scalar);
+  switch (ba.op) {
+    case OP_ADD: return launch_general_t<C, OP_ADD>(it, ia, ib, ba, sa, sb, alpha, s);
+    case OP_MUL: return launch_general_t<C, OP_MUL>(it, ia, ib, ba, sa, sb, alpha, s);
+    default: return launch_general_t<C, OP_DIV>(it, ia, ib, ba, sa, sb, alpha, s);
+  }
+}
+
+mi_status_t run_binary(const BinArgs& ba, hipStream_t stream) {
+  MI_RETURN_IF(validate(ba.out, "out"));
+  if (ba.a) MI_RETURN_IF(validate(ba.a, "self"));
+  if (ba.b) MI_RETURN_IF(validate(ba.b, "other"));
+  const mi_tensor_t* ins[2];
+  int nin = 0, ia = -1, ib = -1;
+  if (ba.a) {
+    ins[nin] = ba.a;
+    ia = ++nin;
+  }
+  if (ba.b) {
+    ins[nin] = ba.b;
+    ib = ++nin;
+  }
+  Iter it;
+  MI_RETURN_IF(make_iter(it, *ba.out, ins, nin));
+  if (it.numel == 0) return MI_OK;
+  const int c = ba.common;
+  if (ba.op == OP_DIV && !is_floating(c))
+    MI_FAIL(MI_ERR_INVALID, "div: common dtype %s is not floating", dtype_name(c));
+
+  // Typed 2-D fast path.
+  bool same = it.dtype[0] == c && (ia < 0 || it.dtype[ia] == c) && (ib < 0 || it.dtype[ib] == c);
+  if (same && it.ndim <= 2) {
+    const int64_t cols = it.ndim == 2 ? it.sizes[1] : it.sizes[0];
+    const int64_t rows = it.ndim == 2 ? it.sizes[0] : 1;
+    const int esz = dtype_size(c);
+    const int vec = 16 / esz;
+    bool ok = it.op_contiguous(0) && cols % vec == 0 && aligned16(it.data[0]);
+    for (int o : {ia, ib}) {
+      if (!ok || o < 0) continue;
+      const int m = mode_2d(it, o, rows, cols);
+      ok = m >= 0 && ((m != M_FULL && m != M_ROW) || aligned16(it.data[o]));
+    }
+    if (ok) {
+      switch (c) {
+        case MI_F32: return dispatch_2d_op<float>(it, ia, ib, ba, stream);
+        case MI_BF16: return dispatch_2d_op<BF16>(it, ia, ib, ba, stream);
+        case MI_F16: return dispatch_2d_op<F16>(it, ia, ib, ba, stream);
+        case MI_F64: return dispatch_2d_op<double>(it, ia, ib, ba, stream);
+        case MI_I64:
+          if (ba.op != OP_DIV) return dispatch_2d_op<int64_t>(it, ia, ib, ba, stream);
+          break;
+        case MI_I32:
+          if (ba.op != OP_DIV) return dispatch_2d_op<int32_t>(it, ia, ib, ba, stream);
+          break;
+        default: break;
+      }
+    }
+  }
+  if (it.ndim > MI_MAX_DIMS) MI_FAIL(MI_ERR_UNSUPPORTED, "too many dims");
+  if (c == MI_F64) return launch_general<double>(it, ia, ib, ba, stream);
+  if (is_floating(c)) return launch_general<float>(it, ia, ib, ba, stream);
+  return launch_general<int64_t>(it, ia, ib, ba, stream);
+}
+
+mi_scalar_t one_scalar() {
+  mi_scalar_t s;
+  s.f = 1.0;
+  s.i = 1;
+  s.dtype = MI_I64;
+  s.wrapped = 1;
+  return s;
+}
+
+mi_status_t binary_tt(int op, const mi_tensor_t* out, const mi_tensor_t* self,
+                      const mi_tensor_t* other, mi_scalar_t alpha, bool negate_alpha,
+                      mi_stream_t stream) {
+  clear_error();
+  if (!out || !self || !other) MI_FAIL(MI_ERR_INVALID, "NULL descriptor");
+  ResultType rt;
+  rt.add_tensor(*self);
+  rt.add_tensor(*other);
+  int common = rt.get();
+  if (op == OP_DIV && !is_floating(common)) common = MI_F32;
+  if (op == OP_ADD && negate_alpha && common == MI_BOOL)
+    MI_FAIL(MI_ERR_INVALID, "sub: subtraction of bool tensors is not supported");
+  BinArgs ba{};
+  ba.out = out;
+  ba.a = self;
+  ba.b = other;
+  ba.alpha_f = scalar_as_double(alpha) * (negate_alpha ? -1.0 : 1.0);
+  ba.alpha_i = scalar_as_int(alpha) * (negate_alpha ? -1 : 1);
+  ba.common = common;
+  ba.op = op;
+  ba.scalar_round_to_common = false;
+  return run_binary(ba, (hipStream_t)stream);
+}
+
+}  // namespace
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+mi_status_t mi_add(const mi_tensor_t* out, const mi_tensor_t* self, const mi_tensor_t* other,
+                   mi_scalar_t alpha, mi_stream_t stream) {
+  return binary_tt(OP_ADD, out, self, other, alpha, false, stream);
+}
+
+mi_status_t mi_sub(const mi_tensor_t* out, const mi_tensor_t* self, const mi_tensor_t* other,
+                   mi_scalar_t alpha, mi_stream_t stream) {
+  return binary_tt(OP_ADD, out, self, other, alpha, true, stream);
+}
+
+mi_status_t mi_mul(const mi_tensor_t* out, const mi_tensor_t* self, const mi_tensor_t* other,
+                   mi_stream_t stream) {
+  return binary_tt(OP_MUL, out, self, other, one_scalar(), false, stream);
+}
+
+mi_status_t mi_div(const mi_tensor_t* out, const mi_tensor_t* self, const mi_tensor_t* other,
+                   mi_stream_t stream) {
+  return binary_tt(OP_DIV, out, self, other, one_scalar(), false, stream);
+}
+
+// CPU ATen casts a wrapped scalar operand of add to the common dtype before
+// the kernel runs (TensorIteratorBase::compute_types on a CPU iterator),
+// so a bf16 tensor + 0.1 adds bf16(0.1).
+mi_status_t mi_add_scalar(const mi_tensor_t* out, const mi_tensor_t* self, mi_scalar_t other,
+                          mi_scalar_t alpha, mi_stream_t stream) {
+  clear_error();
+  if (!out || !self) MI_FAIL(MI_ERR_INVALID, "NULL descriptor");
+  ResultType rt;
+  rt.add_tensor(*self);
+  rt.add_scalar(other);
+  BinArgs ba{};
+  ba.out = out;
+  ba.a = self;
+  ba.b = nullptr;
+  ba.b_scalar = &other;
+  ba.alpha_f = scalar_as_double(alpha);
+  ba.alpha_i = scalar_as_int(alpha);
+  ba.common = rt.get();
+  ba.op = OP_ADD;
+  ba.scalar_round_to_common = true;
+  return run_binary(ba, (hipStream_t)stream);
+}
+
+// CPU ATen's mul kernel reads a scalar operand of a reduced-float multiply in
+// float without first rounding it to the tensor's dtype (mul_kernel's
+// original_scalar_value branch), so the scalar is kept in the compute type.
+mi_status_t mi_mul_scalar(const mi_tensor_t* out, const mi_tensor_t* self, mi_scalar_t other,
+                          mi_stream_t stream) {
+  clear_error();
+  if (!out || !self) MI_FAIL(MI_ERR_INVALID, "NULL descriptor");
+  ResultType rt;
+  rt.add_tensor(*self);
+  rt.add_scalar(other);
+  BinArgs ba{};
+  ba.out = out;
+  ba.a = self;
+  ba.b = nullptr;
+  ba.b_scalar = &other;
+  ba.alpha_f = 1.0;
+  ba.alpha_i = 1;
+  ba.common = rt.get();
+  ba.op = OP_MUL;
+  ba.scalar_round_to_common = false;
+  return run_binary(ba, (hipStream_t)stream);
+}
+
+mi_status_t mi_copy(const mi_tensor_t* out, const mi_tensor_t* src, mi_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = (hipStream_t)stream_;
+  MI_RETURN_IF(validate(out, "out"));
+  MI_RETURN_IF(validate(src, "src"));
+  const mi_tensor_t* ins[1] = {src};
+  Iter it;
+  MI_RETURN_IF(make_iter(it, *out, ins, 1));
+  if (it.numel == 0) return MI_OK;
+  const int esz = dtype_size(out->dtype);
+  if (out->dtype == src->dtype) {
+    if (it.op_contiguous(0) && it.op_contiguous(1)) {
+      if (hipMemcpyAsync(it.data[0], it.data[1], (size_t)it.numel * esz, hipMemcpyDeviceToDevice,
+                         stream) != hipSuccess)
+        MI_FAIL(MI_ERR_LAUNCH, "copy: hipMemcpyAsync failed: %s",
+                hipGetErrorString(hipGetLastError()));
+      return MI_OK;
+    }
+    OffsetCalc<2> oc = make_offset_calc<2>(it);
+    const unsigned g = grid_for(it.numel);
+    switch (esz) {
+      case 1: hipLaunchKernelGGL(copy_raw_kernel<uint8_t>, dim3(g), dim3(kBlock), 0, stream, (uint8_t*)it.data[0], (const uint8_t*)it.data[1], oc, it.numel); break;
+      case 2: hipLaunchKernelGGL(copy_raw_kernel<uint16_t>, dim3(g), dim3(kBlock), 0, stream, (uint16_t*)it.data[0], (const uint16_t*)it.data[1], oc, it.numel); break;
+      case 4: hipLaunchKernelGGL(copy_raw_kernel<uint32_t>, dim3(g), dim3(kBlock), 0, stream, (uint32_t*)it.data[0], (const uint32_t*)it.data[1], oc, it.numel); break;
+      default: hipLaunchKernelGGL(copy_raw_kernel<uint64_t>, dim3(g), dim3(kBlock), 0, stream, (uint64_t*)it.data[0], (const uint64_t*)it.data[1], oc, it.numel); break;
+    }
+    return check_launch("copy_raw");
+  }
+  if (it.op_contiguous(0) && it.op_contiguous(1)) {
+    const unsigned g = ceil_div_u(it.numel, (int64_t)kBlock * 8);
+    const int so = src->dtype, d = out->dtype;
+    bool done = true;
+    if (so == MI_F32 && d == MI_BF16) hipLaunchKernelGGL((convert_contig_kernel<float, BF16>), dim3(g), dim3(kBlock), 0, stream, (uint16_t*)it.data[0], (const float*)it.data[1], it.numel);
+    else if (so == MI_BF16 && d == MI_F32) hipLaunchKernelGGL((convert_contig_kernel<BF16, float>), dim3(g), dim3(kBlock), 0, stream, (float*)it.data[0], (const uint16_t*)it.data[1], it.numel);
+    else if (so == MI_F32 && d == MI_F16) hipLaunchKernelGGL((convert_contig_kernel<float, F16>), dim3(g), dim3(kBlock), 0, stream, (uint16_t*)it.data[0], (const float*)it.data[1], it.numel);
+    else if (so == MI_F16 && d == MI_F32) hipLaunchKernelGGL((convert_contig_kernel<F16, float>), dim3(g), dim3(kBlock), 0, stream, (float*)it.data[0], (const uint16_t*)it.data[1], it.numel);
+    else done = false;
+    if (done) return check_launch("convert_contig");
+  }
+  OffsetCalc<2> oc = make_offset_calc<2>(it);
+  hipLaunchKernelGGL(copy_general_kernel, dim3(grid_for(it.numel)), dim3(kBlock), 0, stream,
+                     it.data[0], out->dtype, (const char*)it.data[1], src->dtype, oc, it.numel);
+  return check_launch("copy_general");
+}
+
+mi_status_t mi_fill(const mi_tensor_t* out, mi_scalar_t value, mi_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = (hipStream_t)stream_;
+  MI_RETURN_IF(validate(out, "out"));
+  const int64_t n = numel(*out);
+  if (n == 0) return MI_OK;
+  // Bit pattern of the value converted to out's dtype (c10::convert).
+  uint64_t bits = 0;
+  const double v = scalar_as_double(value);
+  const int64_t iv = scalar_as_int(value);
+  const bool vf = is_floating(value.dtype);
+  switch (out->dtype) {
+    case MI_U8: bits = (uint8_t)(vf ? (int64_t)v : iv); break;
+    case MI_I8: bits = (uint8_t)(int8_t)(vf ? (int64_t)v : iv); break;
+    case MI_I16: bits = (uint16_t)(int16_t)(vf ? (int64_t)v : iv); break;
+    case MI_I32: bits = (uint32_t)(int32_t)(vf ? (int64_t)v : iv); break;
+    case MI_I64: bits = (uint64_t)(vf ? (int64_t)v : iv); break;
+    case MI_BOOL: bits = (vf ? v != 0.0 : iv != 0) ? 1 : 0; break;
+    case MI_F16: bits = host_f32_to_f16((float)v); break;
+    case MI_BF16: bits = host_f32_to_bf16((float)v); break;
+    case MI_F32: {
+      float f = (float)v;
+      uint32_t u;
+      std::memcpy(&u, &f, 4);
+      bits = u;
+      break;
+    }
+    case MI_F64: std::memcpy(&bits, &v, 8); break;
+    default: MI_FAIL(MI_ERR_UNSUPPORTED, "fill: dtype");
+  }
+  const int esz = dtype_size(out->dtype);
+  if (is_contiguous(*out) && aligned16(out->data)) {
+    const unsigned g = grid_for((n * esz + 15) / 16);
+    switch (esz) {
+      case 1: hipLaunchKernelGGL(fill_contig_kernel<uint8_t>, dim3(g), dim3(kBlock), 0, stream, (uint8_t*)out->data, (uint8_t)bits, n); break;
+      case 2: hipLaunchKernelGGL(fill_contig_kernel<uint16_t>, dim3(g), dim3(kBlock), 0, stream, (uint16_t*)out->data, (uint16_t)bits, n); break;
+      case 4: hipLaunchKernelGGL(fill_contig_kernel<uint32_t>, dim3(g), dim3(kBlock), 0, stream, (uint32_t*)out->data, (uint32_t)bits, n); break;
+      default: hipLaunchKernelGGL(fill_contig_kernel<uint64_t>, dim3(g), dim3(kBlock), 0, stream, (uint64_t*)out->data, (uint64_t)bits, n); break;
+    }
+    return check_launch("fill_contig");
+  }
+  const mi_tensor_t* none[1] = {nullptr};
+  Iter it;
+  MI_RETURN_IF(make_iter(it, *out, none, 0));
+  OffsetCalc<1> oc = make_offset_calc<1>(it);
+  const unsigned g = grid_for(n);
+  switch (esz) {
+    case 1: hipLaunchKernelGGL(fill_strided_kernel<uint8_t>, dim3(g), dim3(kBlock), 0, stream, (uint8_t*)out->data, (uint8_t)bits, oc, n); break;
+    case 2: hipLaunchKernelGGL(fill_strided_kernel<uint16_t>, dim3(g), dim3(kBlock), 0, stream, (uint16_t*)out->data, (uint16_t)bits, oc, n); break;
+    case 4: hipLaunchKernelGGL(fill_strided_kernel<uint32_t>, dim3(g), dim3(kBlock), 0, stream, (uint32_t*)out->data, (uint32_t)bits, oc, n); break;
+    default: hipLaunchKernelGGL(fill_strided_kernel<uint64_t>, dim3(g), dim3(kBlock), 0, stream, (uint64_t*)out->data, (uint64_t)bits, oc, n); break;
+  }
+  return check_launch("fill_strided");
+}
+
+}  // extern "C"

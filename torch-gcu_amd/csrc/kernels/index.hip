@@ -1,0 +1,205 @@
+// index_select: out = self.index_select(dim, index).
+//
+// self is viewed as [outer, S, inner] around `dim`, out as [outer, N, inner].
+// When self and out are dense, a selected slice is a run of inner*esize
+// bytes (64 B for config 1's int64 [1048576, 8] table, 8 KiB for a bf16
+// embedding row of 4096), moved in 16-byte pieces by consecutive lanes so a
+// wave reads whole rows with coalesced loads.  Any other layout takes the
+// general path (one element per lane, full offset arithmetic).
+#include "iter.h"
+
+namespace mi {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <typename IdxT>
+__device__ __forceinline__ int64_t read_index(const IdxT* idx, int64_t i, int64_t istride) {
+  return (int64_t)idx[i * istride];
+}
+
+// Dense rows, moved as 16-byte (W = uint4) or 8/4/2/1-byte words.
+template <typename W, typename IdxT>
+__global__ __launch_bounds__(kBlock) void gather_rows_kernel(
+    W* __restrict__ out, const W* __restrict__ self, const IdxT* __restrict__ idx,
+    int64_t istride, int64_t outer, int64_t n_idx, int64_t src_rows, int64_t words_per_row) {
+  const int64_t total = outer * n_idx * words_per_row;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  const bool small = total < 0x7fffffffLL;
+  for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
+    int64_t row, w, o, i;
+    if (small) {  // 32-bit division is several times cheaper
+      const uint32_t r32 = (uint32_t)t / (uint32_t)words_per_row;
+      w = (uint32_t)t - r32 * (uint32_t)words_per_row;
+      row = r32;
+    } else {
+      row = t / words_per_row;
+      w = t - row * words_per_row;
+    }
+    if (outer == 1) {
+      o = 0;
+      i = row;
+    } else {
+      o = row / n_idx;
+      i = row - o * n_idx;
+    }
+    const int64_t s = read_index(idx, i, istride);
+    W v;
+    if (s >= 0 && s < src_rows) {
+      v = self[(o * src_rows + s) * words_per_row + w];
+    } else {
+      v = W{};
+    }
+    out[t] = v;
+  }
+}
+
+// General layout: iterate over out elements; coordinates decoded per element.
+struct GatherGeneral {
+  int ndim;
+  int dim;
+  int64_t sizes[MI_MAX_DIMS];  // out sizes
+  int64_t ostrides[MI_MAX_DIMS];
+  int64_t sstrides[MI_MAX_DIMS];
+  int64_t src_dim_size;
+};
+
+template <typename T, typename IdxT>
+__global__ __launch_bounds__(kBlock) void gather_general_kernel(T* out, const T* self,
+                                                                const IdxT* idx,
+                                                                int64_t istride,
+                                                                GatherGeneral g, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < n; t += stride) {
+    int64_t lin = t, oo = 0, so = 0;
+    bool ok = true;
+    for (int d = g.ndim - 1; d >= 0; --d) {
+      const int64_t c = lin % g.sizes[d];
+      lin /= g.sizes[d];
+      oo += c * g.ostrides[d];
+      if (d == g.dim) {
+        const int64_t s = read_index(idx, c, istride);
+        ok = s >= 0 && s < g.src_dim_size;
+        so += s * g.sstrides[d];
+      } else {
+        so += c * g.sstrides[d];
+      }
+    }
+    out[oo] = ok ? self[so] : T{};
+  }
+}
+
+unsigned grid_for(int64_t n) {
+  const int64_t want = (n + kBlock - 1) / kBlock;
+  const int64_t cap = (int64_t)cu_count() * 64;
+  return (unsigned)(want < cap ? (want < 1 ? 1 : want) : cap);
+}
+
+template <typename IdxT>
+mi_status_t launch_rows(const mi_tensor_t* out, const mi_tensor_t* self, const IdxT* idx,
+                        int64_t istride, int64_t outer, int64_t n_idx, int64_t src_rows,
+                        int64_t row_bytes, hipStream_t stream) {
+  const uintptr_t align = (uintptr_t)out->data | (uintptr_t)self->data;
+  auto go = [&](auto word) -> mi_status_t {
+    typedef decltype(word) W;
+    const int64_t wpr = row_bytes / (int64_t)sizeof(W);
+    const int64_t total = outer * n_idx * wpr;
+    hipLaunchKernelGGL((gather_rows_kernel<W, IdxT>), dim3(grid_for(total)), dim3(kBlock), 0,
+                       stream, (W*)out->data, (const W*)self->data, idx, istride, outer, n_idx,
+                       src_rows, wpr);
+    return check_launch("index_select rows");
+  };
+  if (row_bytes % 16 == 0 && align % 16 == 0) return go(uint4{});
+  if (row_bytes % 8 == 0 && align % 8 == 0) return go(uint2{});
+  if (row_bytes % 4 == 0 && align % 4 == 0) return go(uint32_t{});
+  if (row_bytes % 2 == 0 && align % 2 == 0) return go(uint16_t{});
+  return go(uint8_t{});
+}
+
+template <typename IdxT>
+mi_status_t launch_general(const mi_tensor_t* out, const mi_tensor_t* self, int dim,
+                           const IdxT* idx, int64_t istride, hipStream_t stream) {
+  GatherGeneral g;
+  g.ndim = out->ndim;
+  g.dim = dim;
+  for (int d = 0; d < MI_MAX_DIMS; ++d) {
+    g.sizes[d] = d < out->ndim ? out->sizes[d] : 1;
+    g.ostrides[d] = d < out->ndim ? out->strides[d] : 0;
+    g.sstrides[d] = d < self->ndim ? self->strides[d] : 0;
+  }
+  g.src_dim_size = self->sizes[dim];
+  const int64_t n = numel(*out);
+  const unsigned grid = grid_for(n);
+  switch (dtype_size(out->dtype)) {
+    case 1: hipLaunchKernelGGL((gather_general_kernel<uint8_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint8_t*)out->data, (const uint8_t*)self->data, idx, istride, g, n); break;
+    case 2: hipLaunchKernelGGL((gather_general_kernel<uint16_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint16_t*)out->data, (const uint16_t*)self->data, idx, istride, g, n); break;
+    case 4: hipLaunchKernelGGL((gather_general_kernel<uint32_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint32_t*)out->data, (const uint32_t*)self->data, idx, istride, g, n); break;
+    default: hipLaunchKernelGGL((gather_general_kernel<uint64_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint64_t*)out->data, (const uint64_t*)self->data, idx, istride, g, n); break;
+  }
+  return check_launch("index_select general");
+}
+
+template <typename IdxT>
+mi_status_t index_select_t(const mi_tensor_t* out, const mi_tensor_t* self, int dim,
+                           const mi_tensor_t* index, hipStream_t stream) {
+  const IdxT* idx = (const IdxT*)index->data;
+  const int64_t istride = index->ndim == 1 ? index->strides[0] : 1;
+  const int64_t n_idx = index->ndim == 1 ? index->sizes[0] : 1;
+  if (self->ndim == 0) {
+    // 0-dim self: every index must be 0; out is 0-dim or [n_idx] of one value
+    mi_tensor_t s1 = *self, o1 = *out;
+    s1.ndim = 1;
+    s1.sizes[0] = 1;
+    s1.strides[0] = 1;
+    if (o1.ndim == 0) {
+      o1.ndim = 1;
+      o1.sizes[0] = 1;
+      o1.strides[0] = 1;
+    }
+    return launch_general<IdxT>(&o1, &s1, 0, idx, istride, stream);
+  }
+  int64_t outer = 1, inner = 1;
+  for (int d = 0; d < dim; ++d) outer *= self->sizes[d];
+  for (int d = dim + 1; d < self->ndim; ++d) inner *= self->sizes[d];
+  if (is_contiguous(*self) && is_contiguous(*out))
+    return launch_rows<IdxT>(out, self, idx, istride, outer, n_idx, self->sizes[dim],
+                             inner * dtype_size(self->dtype), stream);
+  return launch_general<IdxT>(out, self, dim, idx, istride, stream);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" mi_status_t mi_index_select(const mi_tensor_t* out, const mi_tensor_t* self,
+                                       int64_t dim, const mi_tensor_t* index,
+                                       mi_stream_t stream) {
+  clear_error();
+  MI_RETURN_IF(validate(out, "out"));
+  MI_RETURN_IF(validate(self, "self"));
+  MI_RETURN_IF(validate(index, "index"));
+  MI_CHECK_ARG(index->ndim <= 1, "index_select(): Index is supposed to be a vector");
+  MI_CHECK_ARG(index->dtype == MI_I64 || index->dtype == MI_I32,
+               "index_select(): Expected dtype int32 or int64 for index");
+  MI_CHECK_ARG(out->dtype == self->dtype, "index_select(): out dtype %s != self dtype %s",
+               dtype_name(out->dtype), dtype_name(self->dtype));
+  const int nd = self->ndim == 0 ? 1 : self->ndim;
+  if (dim < 0) dim += nd;
+  MI_CHECK_ARG(dim >= 0 && dim < nd, "index_select(): dim out of range");
+  const int64_t n_idx = index->ndim == 1 ? index->sizes[0] : 1;
+  if (self->ndim > 0) {
+    MI_CHECK_ARG(out->ndim == self->ndim, "index_select(): out rank mismatch");
+    for (int d = 0; d < self->ndim; ++d) {
+      const int64_t want = d == dim ? n_idx : self->sizes[d];
+      MI_CHECK_ARG(out->sizes[d] == want, "index_select(): out size %lld at dim %d, expected %lld",
+                   (long long)out->sizes[d], d, (long long)want);
+    }
+  }
+  if (numel(*out) == 0) return MI_OK;
+  MI_CHECK_ARG(self->ndim == 0 || self->sizes[dim] > 0,
+               "index_select(): cannot select from an empty dimension");
+  if (index->dtype == MI_I64)
+    return index_select_t<int64_t>(out, self, (int)dim, index, (hipStream_t)stream);
+  return index_select_t<int32_t>(out, self, (int)dim, index, (hipStream_t)stream);
+}

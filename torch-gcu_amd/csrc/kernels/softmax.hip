@@ -1,0 +1,298 @@
+// softmax / log_softmax along one dim, computed in float.
+//
+// Rows along a dense last dim (config 2: bf16 [8192, 32000], 64,000 B per
+// row) are read from HBM once: a 256-lane block holds its row in registers
+// (up to 32 x 16-byte vectors per lane), takes the row max and the sum of
+// exp(x - max) with wave64 shuffles plus an LDS combine, then writes
+//   log_softmax: x - max - log(sum)      softmax: exp(x - max) * (1 / sum)
+// which is the same sequence of float operations ATen's CPU kernel uses
+// (aten/src/ATen/native/cpu/SoftMaxKernel.cpp, _vec_log_softmax_lastdim).
+// Longer or unaligned rows use a two-read block kernel with an online
+// (max, sum) pair; a non-last dim uses one lane per column.
+#include <cmath>
+
+#include "iter.h"
+
+namespace mi {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <typename Tag>
+struct ST {
+  typedef Tag storage;
+  static __device__ __forceinline__ float load(storage v) { return (float)v; }
+  static __device__ __forceinline__ storage store(float v) { return (storage)v; }
+};
+template <>
+struct ST<BF16> {
+  typedef uint16_t storage;
+  static __device__ __forceinline__ float load(uint16_t v) { return bf16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t store(float v) { return f32_to_bf16(v); }
+};
+template <>
+struct ST<F16> {
+  typedef uint16_t storage;
+  static __device__ __forceinline__ float load(uint16_t v) { return f16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t store(float v) { return f32_to_f16(v); }
+};
+
+// exp used inside the kernels: hardware exp2 for 16-bit inputs (outputs are
+// rounded to 8 or 11 mantissa bits), the accurate library expf for float.
+template <typename Tag>
+__device__ __forceinline__ float kexp(float x) {
+  if constexpr (std::is_same<Tag, float>::value) return expf(x);
+  else return fast_exp(x);
+}
+
+__device__ __forceinline__ float block_max_f(float v, float* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  v = wave_nan_max(v);
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = nan_max(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float block_sum_f(float v, float* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  v = wave_sum(v);
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r += red[w];
+  __syncthreads();
+  return r;
+}
+
+// Register-resident row: VPT 16-byte vectors per lane.
+template <typename InTag, typename OutTag, int VPT, bool LOG>
+__global__ __launch_bounds__(kBlock) void softmax_reg_kernel(
+    typename ST<OutTag>::storage* __restrict__ out,
+    const typename ST<InTag>::storage* __restrict__ in, int64_t D, int64_t in_row_stride,
+    int64_t out_row_stride) {
+  typedef typename ST<InTag>::storage Si;
+  typedef typename ST<OutTag>::storage So;
+  constexpr int VEC = 16 / sizeof(Si);
+  __shared__ float red[16];
+  union Vi {
+    uint4 u;
+    Si s[VEC];
+  };
+  constexpr int kWords = sizeof(So) * VEC / 16;
+  union Vo {
+    So s[VEC];
+    uint4 u[kWords];
+  };
+  const int64_t row = blockIdx.x;
+  const Vi* pin = (const Vi*)(in + row * in_row_stride);
+  const int64_t nv = D / VEC;
+  Vi x[VPT];
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int64_t v = threadIdx.x + (int64_t)k * kBlock;
+    if (v < nv) {
+      x[k] = pin[v];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) m = nan_max(m, ST<InTag>::load(x[k].s[e]));
+    }
+  }
+  m = block_max_f(m, red);
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int64_t v = threadIdx.x + (int64_t)k * kBlock;
+    if (v < nv) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += kexp<InTag>(ST<InTag>::load(x[k].s[e]) - m);
+    }
+  }
+  s = block_sum_f(s, red);
+  So* po = out + row * out_row_stride;
+  if constexpr (LOG) {
+    const float lse = logf(s);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int64_t v = threadIdx.x + (int64_t)k * kBlock;
+      if (v < nv) {
+        Vo o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          o.s[e] = ST<OutTag>::store((ST<InTag>::load(x[k].s[e]) - m) - lse);
+#pragma unroll
+        for (int w = 0; w < kWords; ++w) ((uint4*)(po + v * VEC))[w] = o.u[w];
+      }
+    }
+  } else {
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int64_t v = threadIdx.x + (int64_t)k * kBlock;
+      if (v < nv) {
+        Vo o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          o.s[e] = ST<OutTag>::store(kexp<InTag>(ST<InTag>::load(x[k].s[e]) - m) * inv);
+#pragma unroll
+        for (int w = 0; w < kWords; ++w) ((uint4*)(po + v * VEC))[w] = o.u[w];
+      }
+    }
+  }
+}
+
+// Any row length / alignment: online (max, sum) in one read, output in a
+// second read.
+template <typename InTag, typename OutTag, bool LOG>
+__global__ __launch_bounds__(kBlock) void softmax_row_kernel(
+    typename ST<OutTag>::storage* __restrict__ out,
+    const typename ST<InTag>::storage* __restrict__ in, int64_t D, int64_t in_row_stride,
+    int64_t out_row_stride) {
+  __shared__ float red[16];
+  __shared__ float red2[16];
+  const int64_t row = blockIdx.x;
+  const typename ST<InTag>::storage* p = in + row * in_row_stride;
+  float m = -INFINITY, s = 0.f;
+  for (int64_t j = threadIdx.x; j < D; j += kBlock) {
+    const float x = ST<InTag>::load(p[j]);
+    if (x != x) {
+      m = x;  // NaN propagates through max and sum
+    } else if (x > m) {
+      s = s * kexp<InTag>(m - x) + 1.f;
+      m = x;
+    } else if (x > -INFINITY) {
+      s += kexp<InTag>(x - m);
+    }
+  }
+  // combine (m, s) pairs across the block
+  const float gm = block_max_f(m, red);
+  float ls = (m == -INFINITY) ? 0.f : s * kexp<InTag>(m - gm);
+  (void)red2;
+  const float gs = block_sum_f(ls, red);
+  typename ST<OutTag>::storage* po = out + row * out_row_stride;
+  if constexpr (LOG) {
+    const float lse = logf(gs);
+    for (int64_t j = threadIdx.x; j < D; j += kBlock)
+      po[j] = ST<OutTag>::store((ST<InTag>::load(p[j]) - gm) - lse);
+  } else {
+    const float inv = 1.0f / gs;
+    for (int64_t j = threadIdx.x; j < D; j += kBlock)
+      po[j] = ST<OutTag>::store(kexp<InTag>(ST<InTag>::load(p[j]) - gm) * inv);
+  }
+}
+
+// [outer, D, inner] with inner > 1: one lane per (outer, inner) column.
+template <typename InTag, typename OutTag, bool LOG>
+__global__ __launch_bounds__(kBlock) void softmax_col_kernel(
+    typename ST<OutTag>::storage* __restrict__ out,
+    const typename ST<InTag>::storage* __restrict__ in, int64_t outer, int64_t D,
+    int64_t inner) {
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (t >= outer * inner) return;
+  const int64_t o = t / inner, i = t - o * inner;
+  const typename ST<InTag>::storage* p = in + o * D * inner + i;
+  typename ST<OutTag>::storage* q = out + o * D * inner + i;
+  float m = -INFINITY;
+  for (int64_t j = 0; j < D; ++j) m = nan_max(m, ST<InTag>::load(p[j * inner]));
+  float s = 0.f;
+  for (int64_t j = 0; j < D; ++j) s += kexp<InTag>(ST<InTag>::load(p[j * inner]) - m);
+  if constexpr (LOG) {
+    const float lse = logf(s);
+    for (int64_t j = 0; j < D; ++j)
+      q[j * inner] = ST<OutTag>::store((ST<InTag>::load(p[j * inner]) - m) - lse);
+  } else {
+    const float inv = 1.0f / s;
+    for (int64_t j = 0; j < D; ++j)
+      q[j * inner] = ST<OutTag>::store(kexp<InTag>(ST<InTag>::load(p[j * inner]) - m) * inv);
+  }
+}
+
+template <typename InTag, typename OutTag, bool LOG>
+mi_status_t launch_t(const mi_tensor_t* out, const mi_tensor_t* self, int dim,
+                     hipStream_t stream) {
+  typedef typename ST<InTag>::storage Si;
+  const int nd = self->ndim;
+  int64_t outer = 1, inner = 1;
+  const int64_t D = nd == 0 ? 1 : self->sizes[dim];
+  for (int d = 0; d < dim; ++d) outer *= self->sizes[d];
+  for (int d = dim + 1; d < nd; ++d) inner *= self->sizes[d];
+  if (outer * inner == 0 || D == 0) return MI_OK;
+  if (inner == 1) {
+    constexpr int VEC = 16 / sizeof(Si);
+    const bool aligned = ((uintptr_t)self->data % 16 == 0) &&
+                         ((uintptr_t)out->data % 16 == 0) && (D % VEC == 0);
+    const int64_t nv = D / VEC;
+    auto run_reg = [&](auto vpt_c) -> mi_status_t {
+      constexpr int VPT = decltype(vpt_c)::value;
+      hipLaunchKernelGGL((softmax_reg_kernel<InTag, OutTag, VPT, LOG>), dim3((unsigned)outer),
+                         dim3(kBlock), 0, stream, (typename ST<OutTag>::storage*)out->data,
+                         (const Si*)self->data, D, D, D);
+      return check_launch("softmax_reg");
+    };
+    if (aligned && nv <= (int64_t)kBlock * 32 && outer <= 0x7fffffff) {
+      if (nv <= kBlock * 1) return run_reg(std::integral_constant<int, 1>());
+      if (nv <= kBlock * 2) return run_reg(std::integral_constant<int, 2>());
+      if (nv <= kBlock * 4) return run_reg(std::integral_constant<int, 4>());
+      if (nv <= kBlock * 8) return run_reg(std::integral_constant<int, 8>());
+      if (nv <= kBlock * 16) return run_reg(std::integral_constant<int, 16>());
+      return run_reg(std::integral_constant<int, 32>());
+    }
+    hipLaunchKernelGGL((softmax_row_kernel<InTag, OutTag, LOG>), dim3((unsigned)outer),
+                       dim3(kBlock), 0, stream, (typename ST<OutTag>::storage*)out->data,
+                       (const Si*)self->data, D, D, D);
+    return check_launch("softmax_row");
+  }
+  hipLaunchKernelGGL((softmax_col_kernel<InTag, OutTag, LOG>),
+                     dim3(ceil_div_u(outer * inner, kBlock)), dim3(kBlock), 0, stream,
+                     (typename ST<OutTag>::storage*)out->data, (const Si*)self->data, outer, D,
+                     inner);
+  return check_launch("softmax_col");
+}
+
+template <bool LOG>
+mi_status_t run_softmax(const mi_tensor_t* out, const mi_tensor_t* self, int64_t dim,
+                        hipStream_t stream) {
+  clear_error();
+  MI_RETURN_IF(validate(out, "out"));
+  MI_RETURN_IF(validate(self, "self"));
+  const int nd = self->ndim;
+  const int lim = nd == 0 ? 1 : nd;
+  if (dim < 0) dim += lim;
+  MI_CHECK_ARG(dim >= 0 && dim < lim, "softmax: dim out of range");
+  MI_CHECK_ARG(out->ndim == nd, "softmax: out rank mismatch");
+  for (int d = 0; d < nd; ++d)
+    MI_CHECK_ARG(out->sizes[d] == self->sizes[d], "softmax: out shape mismatch");
+  if (numel(*self) == 0) return MI_OK;
+  // Dense operands only; the host makes other layouts dense first.
+  if (!is_contiguous(*self) || !is_contiguous(*out))
+    MI_FAIL(MI_ERR_UNSUPPORTED, "softmax: operands must be contiguous");
+  const int di = self->dtype, dout = out->dtype;
+  const int d = nd == 0 ? 0 : (int)dim;
+  if (di == MI_BF16 && dout == MI_BF16) return launch_t<BF16, BF16, LOG>(out, self, d, stream);
+  if (di == MI_BF16 && dout == MI_F32) return launch_t<BF16, float, LOG>(out, self, d, stream);
+  if (di == MI_F16 && dout == MI_F16) return launch_t<F16, F16, LOG>(out, self, d, stream);
+  if (di == MI_F16 && dout == MI_F32) return launch_t<F16, float, LOG>(out, self, d, stream);
+  if (di == MI_F32 && dout == MI_F32) return launch_t<float, float, LOG>(out, self, d, stream);
+  MI_FAIL(MI_ERR_UNSUPPORTED, "softmax: dtype %s -> %s", dtype_name(di), dtype_name(dout));
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+mi_status_t mi_softmax(const mi_tensor_t* out, const mi_tensor_t* self, int64_t dim,
+                       mi_stream_t stream) {
+  return run_softmax<false>(out, self, dim, (hipStream_t)stream);
+}
+
+mi_status_t mi_log_softmax(const mi_tensor_t* out, const mi_tensor_t* self, int64_t dim,
+                           mi_stream_t stream) {
+  return run_softmax<true>(out, self, dim, (hipStream_t)stream);
+}
+
+}  // extern "C"

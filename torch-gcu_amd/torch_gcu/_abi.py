@@ -1,0 +1,296 @@
+"""ctypes view of the gfx950 kernel library's C ABI (``include/mi355x_ops.h``).
+
+This is the binding a Python caller of the library uses directly (the tests
+and the benchmark call through it); the PrivateUse1 host in ``torch_gcu._C``
+links the same library from C++.  Tensors handed to it must live on the GPU;
+here that memory comes from any torch device tensor (``data_ptr``), and the
+stream is passed explicitly.
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback behind this module.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Iterable, Optional, Sequence
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libmi355x_ops.so")
+
+MI_MAX_DIMS = 8
+
+MI_OK = 0
+STATUS_NAMES = {0: "MI_OK", 1: "MI_ERR_INVALID", 2: "MI_ERR_UNSUPPORTED",
+                3: "MI_ERR_WORKSPACE", 4: "MI_ERR_LAUNCH", 5: "MI_ERR_TOO_LARGE"}
+
+# dtype codes equal c10::ScalarType's
+DTYPE_CODES = {
+    torch.uint8: 0, torch.int8: 1, torch.int16: 2, torch.int32: 3, torch.int64: 4,
+    torch.float16: 5, torch.float32: 6, torch.float64: 7, torch.bool: 11,
+    torch.bfloat16: 15,
+}
+MI_F64, MI_I64, MI_BOOL = 7, 4, 11
+
+
+class MiTensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("sizes", ctypes.c_int64 * MI_MAX_DIMS),
+                ("strides", ctypes.c_int64 * MI_MAX_DIMS)]
+
+
+class MiScalar(ctypes.Structure):
+    _fields_ = [("f", ctypes.c_double), ("i", ctypes.c_int64), ("dtype", ctypes.c_int32),
+                ("wrapped", ctypes.c_int32)]
+
+
+class MiError(RuntimeError):
+    """A kernel-library call returned a status other than MI_OK."""
+
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn} failed with {STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+_ALLOC_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p)
+_FREE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p)
+
+_T = ctypes.POINTER(MiTensor)
+_S = ctypes.c_void_p
+_SIGNATURES = {
+    "mi_abi_version": ([], ctypes.c_int32),
+    "mi_last_error": ([], ctypes.c_char_p),
+    "mi_set_workspace_allocator": ([_ALLOC_FN, _FREE_FN, ctypes.c_void_p], ctypes.c_int),
+    "mi_device_cu_count": ([], ctypes.c_int32),
+    "mi_copy": ([_T, _T, _S], ctypes.c_int),
+    "mi_fill": ([_T, MiScalar, _S], ctypes.c_int),
+    "mi_add": ([_T, _T, _T, MiScalar, _S], ctypes.c_int),
+    "mi_sub": ([_T, _T, _T, MiScalar, _S], ctypes.c_int),
+    "mi_mul": ([_T, _T, _T, _S], ctypes.c_int),
+    "mi_div": ([_T, _T, _T, _S], ctypes.c_int),
+    "mi_add_scalar": ([_T, _T, MiScalar, MiScalar, _S], ctypes.c_int),
+    "mi_mul_scalar": ([_T, _T, MiScalar, _S], ctypes.c_int),
+    "mi_index_select": ([_T, _T, ctypes.c_int64, _T, _S], ctypes.c_int),
+    "mi_sum": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
+               ctypes.c_int),
+    "mi_amax": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
+                ctypes.c_int),
+    "mi_mean": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
+                ctypes.c_int),
+    "mi_softmax": ([_T, _T, ctypes.c_int64, _S], ctypes.c_int),
+    "mi_log_softmax": ([_T, _T, ctypes.c_int64, _S], ctypes.c_int),
+    "mi_rms_norm": ([_T, _T, _T, ctypes.c_double, _S], ctypes.c_int),
+    "mi_rope": ([_T, _T, _T, _T, _T, ctypes.c_double, _S], ctypes.c_int),
+    "mi_silu_mul": ([_T, _T, _T, _S], ctypes.c_int),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def declared_symbols() -> list[str]:
+    return sorted(_SIGNATURES)
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the kernel library (torch is imported first so that the HIP
+    runtime torch ships is the one the library binds to)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(_LIB_PATH):
+                raise RuntimeError(
+                    f"kernel library not built: {_LIB_PATH} is missing "
+                    "(run `python torch-gcu_amd/build.py`)")
+            handle = ctypes.CDLL(_LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+            for name, (args, res) in _SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = handle
+        return _lib
+
+
+# ---- descriptors ---------------------------------------------------------------
+
+def desc(t: Optional[torch.Tensor]) -> MiTensor:
+    d = MiTensor()
+    if t is None:
+        return d
+    if t.dim() > MI_MAX_DIMS:
+        raise ValueError(f"tensor rank {t.dim()} exceeds {MI_MAX_DIMS}")
+    d.data = t.data_ptr() if t.numel() > 0 else None
+    d.dtype = DTYPE_CODES[t.dtype]
+    d.ndim = t.dim()
+    for i, (s, st) in enumerate(zip(t.shape, t.stride())):
+        d.sizes[i] = s
+        d.strides[i] = st
+    return d
+
+
+def scalar(v, dtype: Optional[torch.dtype] = None, wrapped: bool = True) -> MiScalar:
+    s = MiScalar()
+    if dtype is None:
+        if isinstance(v, bool):
+            dtype = torch.bool
+        elif isinstance(v, int):
+            dtype = torch.int64
+        else:
+            dtype = torch.float64
+    s.dtype = DTYPE_CODES[dtype]
+    if dtype.is_floating_point:
+        s.f = float(v)
+    else:
+        s.i = int(v)
+    s.wrapped = 1 if wrapped else 0
+    return s
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def check(fn: str, status: int) -> None:
+    if status != MI_OK:
+        raise MiError(fn, status, lib().mi_last_error().decode(errors="replace"))
+
+
+# ---- workspace allocator backed by torch device memory ------------------------
+
+class _TorchWorkspace:
+    """Keeps workspace tensors alive until the library frees them.  Memory is
+    taken on the stream the call runs on and returned to torch's caching
+    allocator in stream order."""
+
+    def __init__(self):
+        self.live: dict[int, torch.Tensor] = {}
+        self._alloc = _ALLOC_FN(self.alloc)
+        self._free = _FREE_FN(self.free)
+
+    def alloc(self, nbytes, stream, ctx):
+        try:
+            t = torch.empty(int(nbytes), dtype=torch.uint8, device="cuda")
+        except Exception:  # out of memory: the library reports MI_ERR_WORKSPACE
+            return None
+        p = t.data_ptr()
+        self.live[p] = t
+        return p
+
+    def free(self, ptr, stream, ctx):
+        self.live.pop(ptr, None)
+
+
+_workspace: Optional[_TorchWorkspace] = None
+
+
+def install_torch_workspace() -> None:
+    global _workspace
+    if _workspace is None:
+        _workspace = _TorchWorkspace()
+        check("mi_set_workspace_allocator",
+              lib().mi_set_workspace_allocator(_workspace._alloc, _workspace._free, None))
+
+
+# ---- thin op wrappers (out tensors are preallocated by the caller) --------------
+
+def _dims(dims: Sequence[int]):
+    arr = (ctypes.c_int64 * max(1, len(dims)))(*dims)
+    return arr, len(dims)
+
+
+def copy_(out, src):
+    check("mi_copy", lib().mi_copy(desc(out), desc(src), stream_of(out)))
+    return out
+
+
+def fill_(out, value, dtype=None):
+    check("mi_fill", lib().mi_fill(desc(out), scalar(value, dtype), stream_of(out)))
+    return out
+
+
+def add(out, a, b, alpha=1):
+    if isinstance(b, torch.Tensor):
+        check("mi_add", lib().mi_add(desc(out), desc(a), desc(b), scalar(alpha), stream_of(out)))
+    else:
+        check("mi_add_scalar",
+              lib().mi_add_scalar(desc(out), desc(a), scalar(b), scalar(alpha), stream_of(out)))
+    return out
+
+
+def sub(out, a, b, alpha=1):
+    if isinstance(b, torch.Tensor):
+        check("mi_sub", lib().mi_sub(desc(out), desc(a), desc(b), scalar(alpha), stream_of(out)))
+    else:
+        check("mi_add_scalar",
+              lib().mi_add_scalar(desc(out), desc(a), scalar(b), scalar(-alpha), stream_of(out)))
+    return out
+
+
+def mul(out, a, b):
+    if isinstance(b, torch.Tensor):
+        check("mi_mul", lib().mi_mul(desc(out), desc(a), desc(b), stream_of(out)))
+    else:
+        check("mi_mul_scalar", lib().mi_mul_scalar(desc(out), desc(a), scalar(b), stream_of(out)))
+    return out
+
+
+def div(out, a, b):
+    check("mi_div", lib().mi_div(desc(out), desc(a), desc(b), stream_of(out)))
+    return out
+
+
+def index_select(out, self, dim, index):
+    check("mi_index_select",
+          lib().mi_index_select(desc(out), desc(self), dim, desc(index), stream_of(out)))
+    return out
+
+
+def _reduce(name, out, self, dims, keepdim):
+    arr, n = _dims(list(dims))
+    check(name, getattr(lib(), name)(desc(out), desc(self), arr, n, int(keepdim),
+                                     stream_of(out)))
+    return out
+
+
+def sum_(out, self, dims: Iterable[int] = (), keepdim=False):
+    return _reduce("mi_sum", out, self, dims, keepdim)
+
+
+def amax(out, self, dims: Iterable[int] = (), keepdim=False):
+    return _reduce("mi_amax", out, self, dims, keepdim)
+
+
+def mean(out, self, dims: Iterable[int] = (), keepdim=False):
+    return _reduce("mi_mean", out, self, dims, keepdim)
+
+
+def softmax(out, self, dim):
+    check("mi_softmax", lib().mi_softmax(desc(out), desc(self), dim, stream_of(out)))
+    return out
+
+
+def log_softmax(out, self, dim):
+    check("mi_log_softmax", lib().mi_log_softmax(desc(out), desc(self), dim, stream_of(out)))
+    return out
+
+
+def rms_norm(out, x, weight, eps):
+    check("mi_rms_norm", lib().mi_rms_norm(desc(out), desc(x), desc(weight), eps, stream_of(out)))
+    return out
+
+
+def rope(q_out, k_out, q, k, positions, theta):
+    check("mi_rope", lib().mi_rope(desc(q_out), desc(k_out), desc(q), desc(k), desc(positions),
+                                   theta, stream_of(q_out)))
+    return q_out, k_out
+
+
+def silu_mul(out, gate, up):
+    check("mi_silu_mul", lib().mi_silu_mul(desc(out), desc(gate), desc(up), stream_of(out)))
+    return out
