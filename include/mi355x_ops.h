@@ -151,6 +151,9 @@ mi_status_t mi_add_scalar(const mi_tensor_t* out, const mi_tensor_t* self,
 /* out = self * other_scalar, other a wrapped number. */
 mi_status_t mi_mul_scalar(const mi_tensor_t* out, const mi_tensor_t* self,
                           mi_scalar_t other, mi_stream_t stream);
+/* out = self / other_scalar (true division), other a wrapped number. */
+mi_status_t mi_div_scalar(const mi_tensor_t* out, const mi_tensor_t* self,
+                          mi_scalar_t other, mi_stream_t stream);
 
 /* ---- indexing ---------------------------------------------------------- */
 

@@ -75,12 +75,16 @@ def log_softmax(x: torch.Tensor, dim: int, half_to_float: bool = False) -> torch
     """aten::_log_softmax.out -> topsatenLogSoftmaxForward (yaml :155-156).
     Pinned by a float64 numpy log-sum-exp, the constant-row value -ln(N) and
     the invariant logsumexp(out) == 0."""
+    if half_to_float:  # CPU ATen has no half_to_float kernel; the upcast is exact
+        return torch._log_softmax(x.float(), dim, False)
     return torch._log_softmax(x, dim, half_to_float)
 
 
 def softmax(x: torch.Tensor, dim: int, half_to_float: bool = False) -> torch.Tensor:
     """aten::_softmax.out -> topsatenSoftmaxForward (yaml :182-183).
     Pinned by float64 numpy and the invariant sum(out) == 1."""
+    if half_to_float:
+        return torch._softmax(x.float(), dim, False)
     return torch._softmax(x, dim, half_to_float)
 
 

@@ -1,0 +1,210 @@
+"""The "gcu" PrivateUse1 device end to end on the GPU: ordinary torch code on
+gcu tensors runs through the generated registrations, the caching allocator,
+the streams and the gfx950 kernels, and must match CPU ATen (the reference's
+fallback path) on the same inputs."""
+import pytest
+import torch
+
+import torch_gcu
+from oracle import aten
+from oracle.tolerance import assert_close, assert_exact
+from torch_gcu.utils import synthetic
+
+pytestmark = pytest.mark.gpu
+
+C = torch_gcu._C
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+@pytest.fixture(autouse=True)
+def _clean_debug():
+    C._set_op_debug_config("")
+    yield
+    C._set_op_debug_config("")
+    torch.gcu.synchronize()
+
+
+def test_round_trip_all_dtypes_no_narrowing():
+    for dt in [torch.float32, torch.float64, torch.bfloat16, torch.float16, torch.int64,
+               torch.int32, torch.int16, torch.int8, torch.uint8, torch.bool]:
+        if dt == torch.int64:
+            x = torch.randint(-2**63, 2**63 - 1, (513, 7), generator=g(1), dtype=torch.int64)
+        elif dt == torch.bool:
+            x = torch.randint(0, 2, (513, 7), generator=g(1)).bool()
+        elif dt.is_floating_point:
+            x = torch.randn(513, 7, generator=g(1), dtype=torch.float64).to(dt)
+        else:
+            x = torch.randint(-100, 100, (513, 7), generator=g(1)).to(dt)
+        d = x.to("gcu")
+        assert d.device.type == "gcu" and d.dtype == dt
+        assert_exact(d.cpu(), x, f"round trip {dt}")
+        assert_exact(x.t().to("gcu").cpu(), x.t().contiguous(), f"transposed H2D {dt}")
+        assert_exact(d.t().cpu(), x.t().contiguous(), f"transposed D2H {dt}")
+    y = torch.randn(64, 33, generator=g(2))
+    assert_exact(y.to("gcu", torch.bfloat16).cpu(), y.to(torch.bfloat16), "H2D with cast")
+    assert_exact(y.to("gcu").to(torch.float16).cpu(), y.to(torch.float16), "D2D cast")
+
+
+def test_config1_through_torch_ops():
+    c = synthetic.config1(rows=1024, cols=4096, table_rows=65536, n_idx=16384)
+    a, b = c["a"].to("gcu"), c["b"].to("gcu")
+    out = a * b + c["c"]
+    assert out.device.type == "gcu"
+    assert_exact(out.cpu(), aten.add(aten.mul(c["a"], c["b"]), c["c"]), "a*b+0.5")
+    t, i = c["table"].to("gcu"), c["idx"].to("gcu")
+    assert_exact(torch.index_select(t, 0, i).cpu(), aten.index_select(c["table"], 0, c["idx"]),
+                 "index_select")
+    # a 1-D host index is on another device (as for any accelerator in ATen)
+    with pytest.raises(RuntimeError, match="same device"):
+        torch.index_select(t, 0, torch.tensor([0, 1]))
+    # a 0-dim host index is a scalar and is range-checked on the host
+    with pytest.raises(IndexError):
+        torch.index_select(t, 0, torch.tensor(65536))
+    assert_exact(torch.index_select(t, 0, torch.tensor(5)).cpu(), c["table"][5:6], "0-dim index")
+
+
+def test_config2_through_torch_ops():
+    c = synthetic.config2(rows=256, mrows=1024)
+    x = c["logits"].to("gcu")
+    assert_close(x.sum(-1).cpu(), aten.sum_(c["logits"], -1), "bf16", "sum")
+    assert_exact(x.amax(-1).cpu(), aten.amax(c["logits"], -1), "amax")
+    assert_close(torch.log_softmax(x, -1).cpu(), aten.log_softmax(c["logits"], -1), "bf16",
+                 "log_softmax")
+    assert_close(torch.softmax(x.float(), -1).cpu(), aten.softmax(c["logits"].float(), -1), "fp32",
+                 "softmax")
+    m = c["m"].to("gcu")
+    assert_close(m.mean(0).cpu(), aten.mean(c["m"], 0), "fp32", "mean0")
+    assert_close(m.sum().cpu(), c["m"].sum(), "fp32", "sum all")
+
+
+def test_views_inplace_and_mixed_scalars():
+    x = torch.randn(8, 16, 32, generator=g(3))
+    d = x.to("gcu")
+    v = d.transpose(0, 2)[1:5].reshape(4, -1)
+    assert_exact(v.cpu(), x.transpose(0, 2)[1:5].reshape(4, -1), "views")
+    e = d.clone()
+    e.mul_(2.0).add_(d, alpha=3)
+    assert_exact(e.cpu(), (x * 2.0).add(x, alpha=3), "in-place")
+    assert_exact((d[:, 0] * d[:, 1]).cpu(), x[:, 0] * x[:, 1], "strided operands")
+    s = torch.tensor(0.3)
+    assert_exact((d.bfloat16() * s).cpu(), x.bfloat16() * s, "0-dim CPU tensor operand")
+    assert_exact((s * d.bfloat16()).cpu(), s * x.bfloat16(), "0-dim CPU tensor first")
+    assert_exact((d / 7).cpu(), x / 7, "div scalar")
+    n = torch.arange(12).reshape(3, 4)
+    assert_exact((n.to("gcu") + 5).cpu(), n + 5, "int + scalar")
+    assert_exact((n.to("gcu") / 2).cpu(), n / 2, "int true division")
+
+
+def test_unregistered_op_runs_on_cpu_fallback():
+    x = torch.randn(100, generator=g(4))
+    d = x.to("gcu")
+    assert_close(torch.cos(d).cpu(), torch.cos(x), "fp32", "cos via fallback")
+    assert torch.equal(torch.argmax(d).cpu(), torch.argmax(x))
+
+
+def test_efficient_ops():
+    c = synthetic.config3(tokens=256)
+    x, w = c["x"].to("gcu"), c["w"].to("gcu")
+    assert_close(torch.gcu.efficient.rms_norm(x, w, 1e-6).cpu(),
+                 torch.rms_norm(c["x"], [4096], c["w"], 1e-6), "bf16", "rms_norm")
+    q, k, pos = c["q"].to("gcu"), c["k"].to("gcu"), c["pos"].to("gcu")
+    qo, ko = torch.gcu.efficient.rope(q, k, pos, 10000.0)
+    assert_close(qo.cpu(), aten.rope(c["q"], c["pos"], 10000.0), "bf16", "rope")
+    torch.gcu.efficient.rope_(q, None, pos, 10000.0)
+    assert_exact(q.cpu(), qo.cpu(), "rope_ in place == rope")
+    out = torch.gcu.efficient.silu_mul(c["gate"].to("gcu"), c["up"].to("gcu"))
+    assert_close(out.cpu(), aten.silu_mul(c["gate"], c["up"]), "bf16", "silu_mul")
+    emb = torch.randn(50, 8, generator=g(5)).to("gcu")
+    i32 = torch.tensor([3, 49, 0], dtype=torch.int32).to("gcu")
+    assert_exact(torch.gcu.efficient.gcu_index(emb, [i32]).cpu(), emb.cpu()[[3, 49, 0]], "gcu_index")
+
+
+def test_op_debug_forced_fallback_op_check_and_statistics():
+    x = torch.randn(300, 7, generator=g(6))
+    d = x.to("gcu")
+    C._set_op_debug_config("op_statistics=true")
+    C._clear_op_statistics()
+    d * d
+    torch.cos(d)
+    stats = C._op_statistics()
+    assert stats["mul.Tensor"][0] >= 1, stats           # native
+    # functional cos reaches the fallback as cos.out (structured delegate)
+    assert stats.get("cos", (0, 0))[1] + stats.get("cos.out", (0, 0))[1] >= 1, stats
+    C._set_op_debug_config("fallback_cpu=mul op_statistics=true")
+    C._clear_op_statistics()
+    assert_exact((d * d).cpu(), x * x, "forced fallback")
+    assert C._op_statistics()["mul.Tensor"][1] >= 1
+    C._set_op_debug_config("op_check=all_ops")
+    y = (d * 3 + d).sum(0)
+    assert_close(y.cpu(), (x * 3 + x).sum(0), "fp32", "op_check run")
+
+
+def test_allocator_stats_and_empty_cache():
+    torch.gcu.synchronize()
+    torch.gcu.empty_cache()
+    base = torch.gcu.memory_allocated()
+    t = torch.empty(64 << 20, dtype=torch.uint8, device="gcu")
+    assert torch.gcu.memory_allocated() == base + (64 << 20)
+    assert torch.gcu.memory_reserved() >= torch.gcu.memory_allocated()
+    del t
+    assert torch.gcu.memory_allocated() == base
+    reserved = torch.gcu.memory_reserved()
+    torch.gcu.empty_cache()
+    assert torch.gcu.memory_reserved() <= reserved - (64 << 20)
+    free_b, total = torch.gcu.mem_get_info()
+    assert 0 < free_b <= total
+
+
+def test_streams_and_events():
+    s = torch.gcu.Stream()
+    x = torch.randn(1 << 20, generator=g(7)).to("gcu")
+    torch.gcu.synchronize()
+    e0 = torch.gcu.Event(enable_timing=True)
+    e1 = torch.gcu.Event(enable_timing=True)
+    with torch.gcu.stream(s):
+        assert torch.gcu.current_stream().stream_id == s.stream_id
+        e0.record()
+        y = x * 2
+        e1.record()
+    assert torch.gcu.current_stream().stream_id == 0
+    e1.synchronize()
+    assert e0.elapsed_time(e1) >= 0.0
+    torch.gcu.current_stream().wait_stream(s)
+    y.record_stream(torch.gcu.current_stream())
+    assert_exact(y.cpu(), x.cpu() * 2, "side stream")
+
+
+def test_graph_replay_matches_eager():
+    x = torch.randn(1024, 512, generator=g(8)).to("gcu")
+    w = torch.randn(512, generator=g(9)).to("gcu")
+    eager = torch.log_softmax(x * w + 0.5, -1)
+    graph = torch.gcu.GCUGraph()
+    torch.gcu.synchronize()
+    with torch.gcu.graph(graph):
+        out = torch.log_softmax(x * w + 0.5, -1)
+    assert graph.num_nodes() >= 3
+    for k in range(3):
+        graph.replay()
+        torch.gcu.synchronize()
+        assert_exact(out.cpu(), eager.cpu(), f"replay {k}")
+    # new data in the static input flows through the next replay
+    x.copy_(torch.randn(1024, 512, generator=g(10)).to("gcu"))
+    graph.replay()
+    torch.gcu.synchronize()
+    assert_exact(out.cpu(), torch.log_softmax(x * w + 0.5, -1).cpu(), "replay with new input")
+    graph.reset()
+
+
+def test_graph_capture_rejects_default_stream_and_cpu_fallback():
+    gr = torch.gcu.GCUGraph()
+    with pytest.raises(RuntimeError, match="non-default stream"):
+        gr.capture_begin()
+    x = torch.randn(16, generator=g(11)).to("gcu")
+    gr2 = torch.gcu.GCUGraph()
+    with pytest.raises(RuntimeError):
+        with torch.gcu.graph(gr2):
+            torch.cos(x)
+    torch.gcu.synchronize()

@@ -24,7 +24,7 @@ DEV = "cuda"
 @pytest.fixture(scope="module", autouse=True)
 def _setup():
     torch.cuda.init()
-    _abi.install_torch_workspace()
+    _abi.install_workspace()
     yield
     torch.cuda.synchronize()
 
@@ -111,11 +111,24 @@ def test_scalar_operand_parity(dtype, value):
 def test_mixed_dtype_promotion():
     a = rand((40, 50), torch.bfloat16, 4)
     b = rand((40, 50), torch.float32, 5)
-    for x, y in [(a, b), (b, a), (a, rand((), torch.float32, 6)), (rand((40, 50), torch.int32, 7), rand((), torch.float64, 8))]:
-        ref = aten.mul(x, y)
-        out = empty_like_ref(ref)
-        _abi.mul(out, dev(x), dev(y))
-        assert_exact(out, ref, f"mul {x.dtype}x{y.dtype}")
+    s32 = rand((), torch.float32, 6) * 0.3
+    cases = [(a, b), (b, a), (a, s32), (s32, a), (rand((40, 50), torch.int32, 7), rand((), torch.float64, 8))]
+    for op in ["mul", "add", "div"]:
+        for x, y in cases:
+            ref = getattr(aten, op)(x, y)
+            out = empty_like_ref(ref)
+            getattr(_abi, op)(out, dev(x), dev(y))
+            assert_exact(out, ref, f"{op} {x.dtype}[{x.dim()}]x{y.dtype}[{y.dim()}]")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.int32])
+@pytest.mark.parametrize("value", [0.1, 0.3, 7.0, 3])
+def test_div_by_scalar(dtype, value):
+    a = rand((70, 30), dtype, 35)
+    ref = aten.div(a, value)
+    out = empty_like_ref(ref)
+    _abi.div(out, dev(a), value)
+    assert_exact(out, ref, f"div {dtype} {value}")
 
 
 def test_add_alpha():

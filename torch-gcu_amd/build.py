@@ -45,6 +45,16 @@ HIP_FLAGS = [
 ]
 
 
+INCREMENTAL = False  # development only: skip objects newer than their sources
+
+
+def _up_to_date(src: str, obj: str, deps: list[str]) -> bool:
+    if not INCREMENTAL or not os.path.exists(obj):
+        return False
+    t = os.path.getmtime(obj)
+    return all(os.path.getmtime(d) < t for d in [src, *deps])
+
+
 def _run(cmd: list[str], what: str) -> None:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(
@@ -70,6 +80,8 @@ def build_kernels(jobs: int) -> str:
         o = os.path.join(BUILD, "kernels", os.path.basename(s) + ".o")
         objs.append(o)
         lang = ["-x", "hip"] if s.endswith(".hip") else []
+        if _up_to_date(s, o, _sources(KERNEL_DIR, (".h",)) + [os.path.join(INCLUDE, "mi355x_ops.h")]):
+            continue
         cmds.append(([HIPCC, *HIP_FLAGS, *lang, "-I", INCLUDE, "-I", KERNEL_DIR, "-c", s, "-o", o],
                      os.path.basename(s)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
@@ -113,6 +125,8 @@ def build_host(jobs: int) -> str:
     for s in srcs:
         o = os.path.join(BUILD, "host", os.path.basename(s) + ".o")
         objs.append(o)
+        if _up_to_date(s, o, _sources(HOST_DIR, (".h",)) + [os.path.join(gen_dir, "aotops.h")]):
+            continue
         cmds.append((["g++", *cflags, "-I", INCLUDE, "-I", HOST_DIR, "-I", gen_dir, "-c", s,
                       "-o", o], os.path.basename(s)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
@@ -125,7 +139,7 @@ def build_host(jobs: int) -> str:
 
 def build(kernels_only: bool = False, jobs: int | None = None) -> None:
     jobs = jobs or min(8, os.cpu_count() or 4)
-    if os.path.isdir(BUILD):
+    if os.path.isdir(BUILD) and not INCREMENTAL:
         shutil.rmtree(BUILD)
     build_kernels(jobs)
     if not kernels_only and os.path.isdir(HOST_DIR) and _sources(HOST_DIR, (".cpp",)):
@@ -136,6 +150,9 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("--incremental", action="store_true",
+                    help="development: reuse objects newer than their sources")
     a = ap.parse_args()
+    INCREMENTAL = a.incremental
     build(a.kernels_only, a.j)
     print("built", KERNEL_LIB, "" if a.kernels_only else HOST_LIB)

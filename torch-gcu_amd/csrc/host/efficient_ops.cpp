@@ -1,0 +1,140 @@
+// efficient_ops: fused entry points outside the aten namespace.
+//
+// The reference exposes its one efficient op through pybind only
+// (torch_gcu/csrc/efficient_ops/ops.cpp:335-342, python/efficient_ops.cpp:12-26);
+// here every op is also a dispatcher op in the `torch_gcu` namespace
+// (torch.ops.torch_gcu.<op>) with a PrivateUse1 kernel, so it can be captured
+// in a GCUGraph and shows up in profiles.  The fused ops are new (RMSNorm,
+// RoPE, SiLU-mul); int32_indices_index keeps the reference's op.
+#include <ATen/ATen.h>
+#include <torch/library.h>
+
+#include "dispatch_util.h"
+#include "efficient_ops.h"
+
+namespace torch_gcu {
+namespace efficient {
+
+at::Tensor rms_norm(const at::Tensor& x, const std::optional<at::Tensor>& weight, double eps) {
+  TORCH_CHECK(is_gcu(x), "rms_norm: x must be a gcu tensor");
+  TORCH_CHECK(x.dim() >= 1, "rms_norm: x must have at least one dim");
+  const c10::DeviceGuard g(x.device());
+  at::Tensor xc = x;
+  if (x.stride(-1) != 1) xc = x.contiguous();
+  at::Tensor out = at::empty(x.sizes(), x.options());
+  const mi_tensor_t o = desc(out), xi = desc(xc);
+  mi_tensor_t w{};
+  at::Tensor wc;
+  if (weight.has_value() && weight->defined()) {
+    TORCH_CHECK(is_gcu(*weight), "rms_norm: weight must be a gcu tensor");
+    TORCH_CHECK(weight->numel() == x.size(-1), "rms_norm: weight has ", weight->numel(),
+                " elements, expected ", x.size(-1));
+    wc = weight->contiguous();
+    w = desc(wc);
+  }
+  mi_status_t st = mi_rms_norm(&o, &xi, wc.defined() ? &w : nullptr, eps, mi_stream(out));
+  if (st == MI_ERR_UNSUPPORTED) {
+    // rows without a uniform stride: make x dense and retry
+    at::Tensor dense = xc.contiguous();
+    const mi_tensor_t xd = desc(dense);
+    st = mi_rms_norm(&o, &xd, wc.defined() ? &w : nullptr, eps, mi_stream(out));
+  }
+  check_mi(st, "rms_norm");
+  after_op();
+  return out;
+}
+
+namespace {
+void check_qk(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(is_gcu(t), "rope: ", name, " must be a gcu tensor");
+  TORCH_CHECK(t.dim() == 3, "rope: ", name, " must be [tokens, heads, head_dim]");
+}
+}  // namespace
+
+void rope_(at::Tensor& q, const std::optional<at::Tensor>& k, const at::Tensor& positions,
+           double theta) {
+  check_qk(q, "q");
+  const c10::DeviceGuard g(q.device());
+  at::Tensor pos = is_gcu(positions) ? positions : positions.to(q.device());
+  const mi_tensor_t qd = desc(q), pd = desc(pos);
+  mi_tensor_t kd{};
+  if (k.has_value() && k->defined()) {
+    check_qk(*k, "k");
+    kd = desc(*k);
+  }
+  check_mi(mi_rope(&qd, k.has_value() ? &kd : nullptr, &qd, k.has_value() ? &kd : nullptr, &pd,
+                   theta, mi_stream(q)),
+           "rope");
+  after_op();
+}
+
+std::tuple<at::Tensor, at::Tensor> rope(const at::Tensor& q, const at::Tensor& k,
+                                        const at::Tensor& positions, double theta) {
+  check_qk(q, "q");
+  check_qk(k, "k");
+  const c10::DeviceGuard g(q.device());
+  at::Tensor pos = is_gcu(positions) ? positions : positions.to(q.device());
+  at::Tensor qo = at::empty(q.sizes(), q.options()), ko = at::empty(k.sizes(), k.options());
+  const at::Tensor qi = q.stride(2) == 1 ? q : q.contiguous();
+  const at::Tensor ki = k.stride(2) == 1 ? k : k.contiguous();
+  const mi_tensor_t qod = desc(qo), kod = desc(ko), qd = desc(qi), kd = desc(ki), pd = desc(pos);
+  check_mi(mi_rope(&qod, &kod, &qd, &kd, &pd, theta, mi_stream(qo)), "rope");
+  after_op();
+  return {qo, ko};
+}
+
+at::Tensor silu_mul(const at::Tensor& gate, const at::Tensor& up) {
+  TORCH_CHECK(is_gcu(gate) && is_gcu(up), "silu_mul: gate and up must be gcu tensors");
+  TORCH_CHECK(gate.scalar_type() == up.scalar_type(), "silu_mul: gate and up dtypes differ");
+  const c10::DeviceGuard g(gate.device());
+  const auto shape = at::infer_size_dimvector(gate.sizes(), up.sizes());
+  at::Tensor out = at::empty(shape, gate.options());
+  const mi_tensor_t o = desc(out), gd = desc(gate), ud = desc(up);
+  check_mi(mi_silu_mul(&o, &gd, &ud, mi_stream(out)), "silu_mul");
+  after_op();
+  return out;
+}
+
+// Advanced index with int32 indices (torch_gcu/csrc/efficient_ops/ops.cpp:221-342):
+// one index tensor selecting along dim 0 is an index_select; other patterns
+// run through aten::index after the indices are widened.
+at::Tensor int32_indices_index(const at::Tensor& self,
+                               const c10::List<std::optional<at::Tensor>>& indices) {
+  TORCH_CHECK(is_gcu(self), "int32_indices_index: self must be a gcu tensor");
+  for (const auto& oi : indices) {
+    const std::optional<at::Tensor> i = oi;
+    if (i.has_value() && i->defined())
+      TORCH_CHECK(i->scalar_type() == at::kInt,
+                  "int32_indices_index: indices must be int32 tensors, got ", i->scalar_type());
+  }
+  if (indices.size() == 1) {
+    const std::optional<at::Tensor> i0 = indices.get(0);
+    if (i0.has_value() && i0->defined() && i0->dim() == 1)
+      return at::index_select(self, 0, *i0);
+  }
+  c10::List<std::optional<at::Tensor>> wide;
+  for (const auto& oi : indices) {
+    const std::optional<at::Tensor> i = oi;
+    wide.push_back(i.has_value() && i->defined() ? std::optional<at::Tensor>(i->to(at::kLong)) : i);
+  }
+  return at::index(self, wide);
+}
+
+}  // namespace efficient
+}  // namespace torch_gcu
+
+TORCH_LIBRARY(torch_gcu, m) {
+  m.def("rms_norm(Tensor x, Tensor? weight, float eps=1e-06) -> Tensor");
+  m.def("rope(Tensor q, Tensor k, Tensor positions, float theta=10000.0) -> (Tensor, Tensor)");
+  m.def("rope_(Tensor(a!) q, Tensor(b!)? k, Tensor positions, float theta=10000.0) -> ()");
+  m.def("silu_mul(Tensor gate, Tensor up) -> Tensor");
+  m.def("int32_indices_index(Tensor self, Tensor?[] indices) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(torch_gcu, PrivateUse1, m) {
+  m.impl("rms_norm", TORCH_FN(torch_gcu::efficient::rms_norm));
+  m.impl("rope", TORCH_FN(torch_gcu::efficient::rope));
+  m.impl("rope_", TORCH_FN(torch_gcu::efficient::rope_));
+  m.impl("silu_mul", TORCH_FN(torch_gcu::efficient::silu_mul));
+  m.impl("int32_indices_index", TORCH_FN(torch_gcu::efficient::int32_indices_index));
+}

@@ -28,7 +28,13 @@ void set_error(const char* fmt, ...) {
   g_last_error = buf;
 }
 
-void clear_error() { g_last_error.clear(); }
+// Called at the start of every entry point: forgets this thread's previous
+// message and any runtime error left by an unrelated earlier HIP call, so
+// check_launch reports only the launch it follows.
+void clear_error() {
+  g_last_error.clear();
+  (void)hipGetLastError();
+}
 
 mi_status_t check_launch(const char* what) {
   hipError_t e = hipGetLastError();

@@ -285,6 +285,10 @@ struct BinArgs {
   int common;  // common dtype
   int op;
   bool scalar_round_to_common;  // cast host scalars to the common dtype first
+  // A 0-dim `other` of a reduced-float multiply/divide is read in float
+  // without first rounding it to the common dtype, as CPU ATen's mul and
+  // div kernels do for their second operand (original_scalar_value).
+  bool b_keeps_precision;
 };
 
 template <typename Tag, int OP>
@@ -351,7 +355,7 @@ mi_status_t launch_general_t(const Iter& it, int ia, int ib, const BinArgs& ba, 
   }
   const int dta = ia >= 0 ? it.dtype[ia] : -1, dtb = ib >= 0 ? it.dtype[ib] : -1;
   const int ra = (ia >= 0 && dta != ba.common) ? ba.common : -1;
-  const int rb = (ib >= 0 && dtb != ba.common) ? ba.common : -1;
+  const int rb = (ib >= 0 && dtb != ba.common && !ba.b_keeps_precision) ? ba.common : -1;
   hipLaunchKernelGGL((binary_general_kernel<C, OP>), dim3(grid_for(it.numel)), dim3(kBlock), 0,
                      stream, it.data[0], it.dtype[0], ia >= 0 ? it.data[ia] : nullptr, dta,
                      ib >= 0 ? it.data[ib] : nullptr, dtb, sa, sb, ia < 0 ? 1 : 0,
@@ -473,6 +477,8 @@ mi_status_t binary_tt(int op, const mi_tensor_t* out, const mi_tensor_t* self,
   ba.common = common;
   ba.op = op;
   ba.scalar_round_to_common = false;
+  ba.b_keeps_precision = (op == OP_MUL || op == OP_DIV) && other->ndim == 0 &&
+                         (common == MI_BF16 || common == MI_F16);
   return run_binary(ba, (hipStream_t)stream);
 }
 
@@ -546,6 +552,28 @@ mi_status_t mi_mul_scalar(const mi_tensor_t* out, const mi_tensor_t* self, mi_sc
   ba.alpha_i = 1;
   ba.common = rt.get();
   ba.op = OP_MUL;
+  ba.scalar_round_to_common = false;
+  return run_binary(ba, (hipStream_t)stream);
+}
+
+// True division by a wrapped scalar, read in float like mi_mul_scalar.
+mi_status_t mi_div_scalar(const mi_tensor_t* out, const mi_tensor_t* self, mi_scalar_t other,
+                          mi_stream_t stream) {
+  clear_error();
+  if (!out || !self) MI_FAIL(MI_ERR_INVALID, "NULL descriptor");
+  ResultType rt;
+  rt.add_tensor(*self);
+  rt.add_scalar(other);
+  BinArgs ba{};
+  ba.out = out;
+  ba.a = self;
+  ba.b = nullptr;
+  ba.b_scalar = &other;
+  ba.alpha_f = 1.0;
+  ba.alpha_i = 1;
+  ba.common = rt.get();
+  if (!is_floating(ba.common)) ba.common = MI_F32;
+  ba.op = OP_DIV;
   ba.scalar_round_to_common = false;
   return run_binary(ba, (hipStream_t)stream);
 }

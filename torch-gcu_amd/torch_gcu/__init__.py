@@ -1,10 +1,34 @@
-"""torch_gcu for MI355X: the "gcu" PrivateUse1 device backed by hand-written
+"""torch_gcu for MI355X: the "gcu" PrivateUse1 device, backed by hand-written
 gfx950 HIP kernels.
 
-Importing the package loads the kernel library (``torch_gcu._abi``).  The
-PrivateUse1 host extension (``torch_gcu._C``) is loaded by
-``torch_gcu._backend``.
+``import torch_gcu`` loads the C++ host (``torch_gcu._C``: runtime, caching
+allocator, GCUGraph, the generated aten registrations and the efficient ops)
+and the kernel library it links, renames PrivateUse1 to "gcu" and installs
+``torch.gcu`` -- the same steps as the reference's package init
+(torch_gcu/__init__.py:11-16 and :79-106).  There is no fallback when the
+extension is missing: the import fails.
 """
-from . import _abi  # noqa: F401
+import os as _os
 
-__all__ = ["_abi"]
+import torch as _torch
+
+from . import _abi  # noqa: F401  (kernel library; loaded first)
+
+try:
+    from . import _C  # noqa: F401
+except ImportError as _e:  # pragma: no cover - exercised only on a broken install
+    raise ImportError(
+        "torch_gcu._C is not built (run `python torch-gcu_amd/build.py`): " + str(_e)) from _e
+
+_torch.utils.rename_privateuse1_backend("gcu")
+
+from . import gcu  # noqa: E402
+
+_torch._register_device_module("gcu", gcu)
+_torch.utils.generate_methods_for_privateuse1_backend(for_tensor=True, for_module=True,
+                                                      for_storage=True)
+_C._init()
+
+from .gcu import efficient  # noqa: E402,F401
+
+__all__ = ["gcu", "efficient"]

@@ -72,6 +72,7 @@ _SIGNATURES = {
     "mi_div": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_add_scalar": ([_T, _T, MiScalar, MiScalar, _S], ctypes.c_int),
     "mi_mul_scalar": ([_T, _T, MiScalar, _S], ctypes.c_int),
+    "mi_div_scalar": ([_T, _T, MiScalar, _S], ctypes.c_int),
     "mi_index_select": ([_T, _T, ctypes.c_int64, _T, _S], ctypes.c_int),
     "mi_sum": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
                ctypes.c_int),
@@ -161,40 +162,15 @@ def check(fn: str, status: int) -> None:
         raise MiError(fn, status, lib().mi_last_error().decode(errors="replace"))
 
 
-# ---- workspace allocator backed by torch device memory ------------------------
+# ---- workspace ------------------------------------------------------------------
 
-class _TorchWorkspace:
-    """Keeps workspace tensors alive until the library frees them.  Memory is
-    taken on the stream the call runs on and returned to torch's caching
-    allocator in stream order."""
+def install_workspace() -> None:
+    """Registers the gcu caching allocator (torch_gcu._C) as the library's
+    stream-ordered workspace allocator; direct C-ABI callers need it for the
+    entry points that take temporary memory (split reductions)."""
+    from . import _C
 
-    def __init__(self):
-        self.live: dict[int, torch.Tensor] = {}
-        self._alloc = _ALLOC_FN(self.alloc)
-        self._free = _FREE_FN(self.free)
-
-    def alloc(self, nbytes, stream, ctx):
-        try:
-            t = torch.empty(int(nbytes), dtype=torch.uint8, device="cuda")
-        except Exception:  # out of memory: the library reports MI_ERR_WORKSPACE
-            return None
-        p = t.data_ptr()
-        self.live[p] = t
-        return p
-
-    def free(self, ptr, stream, ctx):
-        self.live.pop(ptr, None)
-
-
-_workspace: Optional[_TorchWorkspace] = None
-
-
-def install_torch_workspace() -> None:
-    global _workspace
-    if _workspace is None:
-        _workspace = _TorchWorkspace()
-        check("mi_set_workspace_allocator",
-              lib().mi_set_workspace_allocator(_workspace._alloc, _workspace._free, None))
+    _C._init()
 
 
 # ---- thin op wrappers (out tensors are preallocated by the caller) --------------
@@ -241,7 +217,10 @@ def mul(out, a, b):
 
 
 def div(out, a, b):
-    check("mi_div", lib().mi_div(desc(out), desc(a), desc(b), stream_of(out)))
+    if isinstance(b, torch.Tensor):
+        check("mi_div", lib().mi_div(desc(out), desc(a), desc(b), stream_of(out)))
+    else:
+        check("mi_div_scalar", lib().mi_div_scalar(desc(out), desc(a), scalar(b), stream_of(out)))
     return out
 
 
