@@ -164,7 +164,10 @@ def cpu_baseline(torch, synthetic, seconds):
     }
 
 
-def bench_op(torch, name, sets, fn, alg_bytes, iters=30):
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_op(torch, name, sets, fn, alg_bytes, iters=30, flops=None, bound="hbm"):
     """Per-launch time of fn over rotating input sets (HIP events)."""
     for s in sets[:2]:
         fn(s)
@@ -178,8 +181,51 @@ def bench_op(torch, name, sets, fn, alg_bytes, iters=30):
     torch.cuda.synchronize()
     ms = st.elapsed_time(en) / iters
     gbs = alg_bytes / (ms * 1e-3) / 1e9
-    return {"op": name, "ms": round(ms, 4), "GB/s": round(gbs, 1),
-            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes": alg_bytes}
+    r = {"op": name, "ms": round(ms, 4), "GB/s": round(gbs, 1),
+         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes": alg_bytes}
+    if flops is not None:
+        tf = flops / (ms * 1e-3) / 1e12
+        r.update({"TFLOP/s": round(tf, 1), "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                  "flops": flops, "bound": bound})
+    return r
+
+
+def gemm_ops(torch, _abi):
+    """Config 4: bf16 addmm M8192 N4096 K4096 and the int8 weight-only linear
+    (W int8 [11008, 4096], fp32 scales) at M = 16, 256, 4096."""
+    res = []
+    log("bench: config 4 ops")
+    gen = torch.Generator().manual_seed(20261204)
+    M, N, K = 8192, 4096, 4096
+    A = [(torch.randn(M, K, generator=gen) * 0.02).bfloat16().cuda() for _ in range(2)]
+    B = [(torch.randn(K, N, generator=gen) * 0.02).bfloat16().cuda() for _ in range(2)]
+    bias = (torch.randn(N, generator=gen) * 0.02).bfloat16().cuda()
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    sets = [{"a": A[i], "b": B[i]} for i in range(2)]
+    res.append(bench_op(torch, "c4.addmm bf16 M8192 N4096 K4096 (B row-major [K,N])", sets,
+                        lambda s: _abi.addmm(out, bias, s["a"], s["b"]),
+                        (M * K + K * N + M * N) * 2 + N * 2, iters=10, flops=2 * M * N * K,
+                        bound="mfma"))
+    Bt = [b.t().contiguous().t() for b in B]  # the nn.Linear layout: W [N, K], B = W^T
+    sets = [{"a": A[i], "b": Bt[i]} for i in range(2)]
+    res.append(bench_op(torch, "c4.addmm bf16 M8192 N4096 K4096 (B = W^T, K-contiguous)", sets,
+                        lambda s: _abi.addmm(out, bias, s["a"], s["b"]),
+                        (M * K + K * N + M * N) * 2 + N * 2, iters=10, flops=2 * M * N * K,
+                        bound="mfma"))
+    del A, B, Bt, out, sets
+    N, K = 11008, 4096
+    W = [torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8).cuda() for _ in range(4)]
+    scales = (torch.rand(N, generator=gen) * 0.009 + 0.001).cuda()
+    for M in (16, 256, 4096):
+        x = torch.randn(M, K, generator=gen).bfloat16().cuda()
+        o = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        sets = [{"w": w} for w in W]
+        alg = N * K + N * 4 + M * K * 2 + M * N * 2
+        res.append(bench_op(torch, f"c4.int8_linear M={M} W int8 [11008,4096]", sets,
+                            lambda s: _abi.int8_linear(o, x, s["w"], scales), alg,
+                            iters=20 if M < 4096 else 10, flops=2 * M * N * K,
+                            bound="hbm" if M == 16 else "mfma"))
+    return res
 
 
 def other_ops(torch, _abi, synthetic):
@@ -217,6 +263,8 @@ def other_ops(torch, _abi, synthetic):
     gs = [{"g": gt, "u": up, "o": torch.empty_like(gt)}, {"g": up, "u": gt, "o": torch.empty_like(gt)}]
     res.append(bench_op(torch, "c3.silu_mul bf16 [16384,11008]", gs,
                         lambda s: _abi.silu_mul(s["o"], s["g"], s["u"]), 1082130432))
+    del gs, gt, up, c3
+    res.extend(gemm_ops(torch, _abi))
     return res
 
 

@@ -193,6 +193,41 @@ mi_status_t mi_softmax(const mi_tensor_t* out, const mi_tensor_t* self,
 mi_status_t mi_log_softmax(const mi_tensor_t* out, const mi_tensor_t* self,
                            int64_t dim, mi_stream_t stream);
 
+/* ---- dense contractions ------------------------------------------------------
+ * bf16 / fp16 operands run on MFMA (v_mfma_f32_32x32x16) with fp32
+ * accumulation and one rounding of the result; fp32 operands on the VALU.
+ * mat1, mat2 and out share a dtype.  A layout the MFMA kernel cannot read
+ * directly (mat1 not K-contiguous, mat2 not K-contiguous as [N, K] rows, a
+ * leading dim that is not a multiple of 8) is first copied densely into
+ * workspace.  Replace topsatenAddmm (addmm.out :205), topsatenMm (mm.out
+ * :452) and topsatenBmm (bmm.out :260); baddbmm.out is yaml :238. */
+
+/* out = beta * self + alpha * (mat1 @ mat2); mat1 [M, K], mat2 [K, N], self
+ * broadcasts to [M, N] and is ignored when beta == 0. */
+mi_status_t mi_addmm(const mi_tensor_t* out, const mi_tensor_t* self,
+                     const mi_tensor_t* mat1, const mi_tensor_t* mat2,
+                     double beta, double alpha, mi_stream_t stream);
+/* out = self @ mat2, [M, K] x [K, N]. */
+mi_status_t mi_mm(const mi_tensor_t* out, const mi_tensor_t* self,
+                  const mi_tensor_t* mat2, mi_stream_t stream);
+/* out[b] = self[b] @ mat2[b], [B, M, K] x [B, K, N]. */
+mi_status_t mi_bmm(const mi_tensor_t* out, const mi_tensor_t* self,
+                   const mi_tensor_t* mat2, mi_stream_t stream);
+/* out[b] = beta * self[b] + alpha * (batch1[b] @ batch2[b]). */
+mi_status_t mi_baddbmm(const mi_tensor_t* out, const mi_tensor_t* self,
+                       const mi_tensor_t* batch1, const mi_tensor_t* batch2,
+                       double beta, double alpha, mi_stream_t stream);
+
+/* int8 weight-only linear: out[m, n] = scales[n] * sum_k x[m, k] * w[n, k]
+ * (+ bias[n]); x and out bf16 or fp16 [M, K] / [M, N], w int8 [N, K], scales
+ * fp32 [N], bias (optional, NULL data for none) broadcast to [M, N].  The
+ * weight is widened to bf16/fp16 exactly on its way into LDS and multiplied
+ * on MFMA with fp32 accumulation.  New efficient op: no TopsAten
+ * counterpart. */
+mi_status_t mi_int8_linear(const mi_tensor_t* out, const mi_tensor_t* x,
+                           const mi_tensor_t* weight, const mi_tensor_t* scales,
+                           const mi_tensor_t* bias, mi_stream_t stream);
+
 /* ---- fused efficient ops ---------------------------------------------------
  * The reference's efficient_ops entry point pattern
  * (torch_gcu/csrc/efficient_ops/ops.h:14-93, pybind at

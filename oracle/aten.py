@@ -127,6 +127,32 @@ def rope(x: torch.Tensor, positions: torch.Tensor, theta: float) -> torch.Tensor
     return out.to(x.dtype)
 
 
+def addmm(bias, a, b, beta=1.0, alpha=1.0):
+    """aten::addmm.out -> topsatenAddmm (yaml :205), as the fp32 closed form
+    beta*bias + alpha*(a @ b) over upcast inputs with one cast to a.dtype
+    (CPU ATen's bf16 addmm accumulates in fp32 too).  Pinned by float64
+    numpy matmul and the row-sampling identity C[rows] = A[rows] @ B."""
+    out = (a.float() @ b.float()) * alpha
+    if bias is not None and beta != 0:
+        out = out + beta * bias.float()
+    return out.to(a.dtype)
+
+
+def bmm(a, b):
+    """aten::bmm.out -> topsatenBmm (yaml :260), fp32 closed form."""
+    return torch.bmm(a.float(), b.float()).to(a.dtype)
+
+
+def int8_linear(x, w, scales, bias=None):
+    """int8 weight-only linear, fp32 closed form (x @ W^T) * scales (+ bias)
+    with one cast; new efficient op, no reference counterpart.  Pinned by
+    float64 numpy and by aten::_weight_int8pack_mm with bf16 scales."""
+    y = (x.float() @ w.float().t()) * scales.float()
+    if bias is not None:
+        y = y + bias.float()
+    return y.to(x.dtype)
+
+
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up in fp32, one cast (the reference would run silu.out,
     yaml :561, then mul.out).  Pinned by float64 numpy and

@@ -1,0 +1,140 @@
+"""GPU parity of the MFMA contractions (addmm / mm / bmm / baddbmm and the
+int8 weight-only linear) through the C ABI, against the fp32 closed form on
+CPU (bf16 outputs: |d| <= 1e-2*|ref| + 1e-2*rms(ref); fp32: 1e-5 bars scaled
+by the K-term sum)."""
+import pytest
+import torch
+
+from oracle import aten
+from oracle.tolerance import assert_close
+from torch_gcu import _abi
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _setup():
+    torch.cuda.init()
+    _abi.install_workspace()
+    yield
+    torch.cuda.synchronize()
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rn(shape, seed, dtype=torch.bfloat16, std=0.02):
+    return (torch.randn(shape, generator=g(seed)) * std).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (512, 768, 1024), (300, 200, 136),
+                                   (37, 1000, 72), (1, 512, 256), (1024, 64, 4096), (77, 77, 8)])
+@pytest.mark.parametrize("b_layout", ["kn", "nk"])
+def test_mm_parity(dtype, M, N, K, b_layout):
+    a = rn((M, K), 1, dtype, 1.0)
+    b = rn((K, N), 2, dtype, 1.0) if b_layout == "kn" else rn((N, K), 2, dtype, 1.0).t()
+    ref = aten.addmm(None, a, b, beta=0.0)
+    out = torch.empty(M, N, dtype=dtype, device="cuda")
+    _abi.mm(out, a.cuda(), b.cuda() if b_layout == "kn" else b.t().contiguous().cuda().t())
+    assert_close(out, ref, "bf16", f"mm {M}x{N}x{K} {b_layout}")
+
+
+@pytest.mark.parametrize("bias_shape", ["row", "full", "col"])
+def test_addmm_bias_alpha_beta(bias_shape):
+    M, N, K = 384, 640, 512
+    a, b = rn((M, K), 3), rn((K, N), 4)
+    bias = {"row": rn((N,), 5), "full": rn((M, N), 5), "col": rn((M, 1), 5)}[bias_shape]
+    for alpha, beta in [(1.0, 1.0), (0.5, 2.0), (1.0, 0.0)]:
+        ref = aten.addmm(bias, a, b, beta=beta, alpha=alpha)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        _abi.addmm(out, bias.cuda(), a.cuda(), b.cuda(), beta=beta, alpha=alpha)
+        assert_close(out, ref, "bf16", f"addmm {bias_shape} a={alpha} b={beta}")
+    # fp32 bias with bf16 operands
+    bf = torch.randn(N, generator=g(6))
+    ref = aten.addmm(bf, a, b)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _abi.addmm(out, bf.cuda(), a.cuda(), b.cuda())
+    assert_close(out, ref, "bf16", "addmm fp32 bias")
+
+
+def test_config4_addmm_full_size_row_sample():
+    """M8192 N4096 K4096: every output checked on 64 sampled rows (exact
+    subset of the closed form) plus a column checksum."""
+    M, N, K = 8192, 4096, 4096
+    a, b, bias = rn((M, K), 7), rn((K, N), 8), rn((N,), 9)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _abi.addmm(out, bias.cuda(), a.cuda(), b.cuda())
+    rows = torch.randperm(M, generator=g(10))[:64]
+    ref = aten.addmm(bias, a[rows], b)
+    assert_close(out.cpu()[rows], ref, "bf16", "addmm sampled rows")
+    # checksum: sum over rows of C equals (sum of A rows) @ B + M * bias
+    colsum = out.float().sum(0).cpu()
+    want = (a.float().sum(0) @ b.float()) + M * bias.float()
+    rel = ((colsum - want).norm() / want.norm()).item()
+    assert rel < 2e-2, rel
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_bmm_and_baddbmm(dtype):
+    B, M, N, K = 6, 130, 96, 200
+    a, b = rn((B, M, K), 11, dtype, 1.0), rn((B, K, N), 12, dtype, 1.0)
+    ref = aten.bmm(a, b)
+    out = torch.empty(B, M, N, dtype=dtype, device="cuda")
+    _abi.bmm(out, a.cuda(), b.cuda())
+    assert_close(out, ref, "bf16" if dtype == torch.bfloat16 else "fp32", "bmm")
+    # transposed second operand as attention uses it (q @ k^T)
+    kt = rn((B, N, K), 13, dtype, 1.0)
+    out2 = torch.empty(B, M, N, dtype=dtype, device="cuda")
+    _abi.bmm(out2, a.cuda(), kt.cuda().transpose(1, 2))
+    assert_close(out2, aten.bmm(a, kt.transpose(1, 2).contiguous()),
+                 "bf16" if dtype == torch.bfloat16 else "fp32", "bmm kt")
+    bias = rn((B, M, N), 14, dtype, 1.0)
+    out3 = torch.empty(B, M, N, dtype=dtype, device="cuda")
+    _abi.baddbmm(out3, bias.cuda(), a.cuda(), b.cuda(), beta=0.5, alpha=2.0)
+    ref3 = (0.5 * bias.float() + 2.0 * torch.bmm(a.float(), b.float())).to(dtype)
+    assert_close(out3, ref3, "bf16" if dtype == torch.bfloat16 else "fp32", "baddbmm")
+
+
+def test_fp32_mm_and_empty_k():
+    a, b = torch.randn(70, 33, generator=g(15)), torch.randn(33, 45, generator=g(16))
+    out = torch.empty(70, 45, device="cuda")
+    _abi.mm(out, a.cuda(), b.cuda())
+    assert_close(out, a @ b, "fp32", "fp32 mm")
+    z = torch.empty(5, 0, dtype=torch.bfloat16)
+    w = torch.empty(0, 7, dtype=torch.bfloat16)
+    out = torch.full((5, 7), 3.0, dtype=torch.bfloat16, device="cuda")
+    _abi.mm(out, z.cuda(), w.cuda())
+    assert (out.cpu() == 0).all()
+
+
+def int8_inputs(M, N=11008, K=4096, seed=20):
+    w = torch.randint(-127, 128, (N, K), generator=g(seed), dtype=torch.int8)
+    scales = torch.rand(N, generator=g(seed + 1)) * 0.009 + 0.001
+    x = torch.randn(M, K, generator=g(seed + 2)).to(torch.bfloat16)
+    return x, w, scales
+
+
+@pytest.mark.parametrize("M", [16, 256])
+def test_config4_int8_linear(M):
+    x, w, scales = int8_inputs(M)
+    out = torch.empty(M, w.shape[0], dtype=torch.bfloat16, device="cuda")
+    _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda())
+    assert_close(out, aten.int8_linear(x, w, scales), "bf16", f"int8 linear M={M}")
+
+
+def test_config4_int8_linear_m4096_row_sample():
+    x, w, scales = int8_inputs(4096)
+    out = torch.empty(4096, w.shape[0], dtype=torch.bfloat16, device="cuda")
+    _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda())
+    rows = torch.randperm(4096, generator=g(30))[:48]
+    assert_close(out.cpu()[rows], aten.int8_linear(x[rows], w, scales), "bf16", "int8 M=4096 rows")
+
+
+def test_int8_linear_edges_and_bias():
+    x, w, scales = int8_inputs(33, N=300, K=200, seed=40)
+    bias = torch.randn(300, generator=g(41)).to(torch.bfloat16)
+    out = torch.empty(33, 300, dtype=torch.bfloat16, device="cuda")
+    _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda(), bias.cuda())
+    assert_close(out, aten.int8_linear(x, w, scales, bias), "bf16", "int8 ragged + bias")

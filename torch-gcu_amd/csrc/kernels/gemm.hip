@@ -1,0 +1,746 @@
+// Dense contractions on gfx950 MFMA: addmm / mm / bmm / baddbmm and the int8
+// weight-only linear.
+//
+// One kernel template, v_mfma_f32_32x32x16_{bf16,f16} with fp32 accumulation:
+//   - a block owns a BM x BN output tile and walks K in steps of 64;
+//   - WM x WN waves each own a (BM/WM) x (BN/WN) sub-tile, i.e. a grid of
+//     32 x 32 MFMA tiles (the 256 x 256 configuration gives every wave
+//     16 tiles = 256 fp32 accumulators, which live in AGPRs);
+//   - A rows and B rows (B is read as [N, K], K contiguous) are staged
+//     through LDS with a 72-element row pitch (16 bytes of padding) so the
+//     16-byte operand reads of 32 consecutive rows fall in distinct banks;
+//     two LDS stages let the global loads of step k+1 overlap the MFMAs of
+//     step k with one barrier per step;
+//   - for the int8 weight-only linear, B tiles arrive as int8 (half the
+//     bytes) and are widened to bf16 on the way into LDS (an int8 value is
+//     exactly a bf16 whose low 16 fp32 bits are zero), and the epilogue
+//     multiplies by the per-output-channel fp32 scale.
+// MFMA operand layout (checked on the device): lane l supplies
+//   A[m = l % 32][k = 8 * (l / 32) + i] and B[k = 8 * (l / 32) + i][n = l % 32],
+//   i < 8, and receives D[m = 8 * (r / 4) + 4 * (l / 32) + r % 4][n = l % 32]
+//   in accumulator r < 16.
+// Workgroups are renumbered so that each of the 8 XCDs (which receive
+// workgroups round robin) gets a contiguous run of tiles, walked in groups
+// of 8 row panels, so tiles sharing A and B panels meet in one L2.
+// fp32 inputs take a VALU tiled kernel.
+#include <algorithm>
+
+#include "iter.h"
+
+namespace mi {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BK = 64;
+constexpr int PITCH = BK + 8;  // LDS row pitch in elements
+
+template <typename T>
+struct MfmaOp;
+template <>
+struct MfmaOp<BF16> {
+  typedef bf16x8 vec;
+  static __device__ __forceinline__ f32x16 mma(vec a, vec b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t store(float v) { return f32_to_bf16(v); }
+  static __device__ __forceinline__ float load(uint16_t v) { return bf16_to_f32(v); }
+};
+template <>
+struct MfmaOp<F16> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ f32x16 mma(vec a, vec b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t store(float v) { return f32_to_f16(v); }
+  static __device__ __forceinline__ float load(uint16_t v) { return f16_to_f32(v); }
+};
+
+struct GemmArgs {
+  const uint16_t* a;  // [batch][M][lda], K contiguous
+  const void* b;      // [batch][N][ldb], K contiguous (16-bit or int8)
+  uint16_t* c;        // [batch][M][ldc], N contiguous
+  const void* bias;   // element (m, n) at bias + b*bias_sb + m*bias_sm + n*bias_sn
+  const float* scale; // int8 path: per-N fp32 scale
+  int bias_dtype;
+  int64_t bias_sm, bias_sn, bias_sb;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;
+  int64_t sa, sb, sc;  // batch strides (elements)
+  float alpha, beta;
+  int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int total = tiles_m * tiles_n;
+  constexpr int XCD = 8;
+  int id = bid;
+  if (total % XCD == 0) {
+    const int per = total / XCD;
+    id = (bid % XCD) * per + bid / XCD;
+  }
+  constexpr int GROUP_M = 8;
+  const int group = id / (GROUP_M * tiles_n);
+  const int first_m = group * GROUP_M;
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int in_group = id - group * GROUP_M * tiles_n;
+  *tm = first_m + in_group % gsize;
+  *tn = in_group / gsize;
+}
+
+// Per-lane loader of a ROWS x 64 tile of a K-contiguous 16-bit matrix: V
+// 16-byte vectors per lane, 8 lanes per 128-byte row segment; vector i of a
+// lane covers tile row row0 + i * (NT / 8).  Rows past the end of the matrix
+// are clamped to its last row: their products only reach output rows or
+// columns that are never stored.  The last, partial K step (load_tail) reads
+// the elements at k >= K as zero.  Addresses are formed at load time so that
+// no per-vector pointer stays live across the main loop.
+template <int ROWS, int NT>
+struct Tile16 {
+  static constexpr int V = ROWS * 8 / NT;
+  static constexpr int RS = NT / 8;  // rows between a lane's vectors
+  const uint16_t* base;
+  int64_t ld, last, row0;
+  int kc;
+  uint4 r[V];
+  __device__ __forceinline__ void init(const uint16_t* b, int64_t ld_, int64_t rows, int64_t r0) {
+    base = b;
+    ld = ld_;
+    last = rows - 1;
+    row0 = r0 + (threadIdx.x >> 3);
+    kc = (threadIdx.x & 7) * 8;
+  }
+  __device__ __forceinline__ const uint16_t* at(int i, int64_t k0) const {
+    const int64_t gr = min(row0 + (int64_t)i * RS, last);
+    return base + gr * ld + kc + k0;
+  }
+  __device__ __forceinline__ void load_full(int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) r[i] = *(const uint4*)at(i, k0);
+  }
+  __device__ __forceinline__ void load_tail(int64_t k0, int64_t K) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const uint16_t* q = at(i, k0);
+      const int64_t gk = k0 + kc;
+      union {
+        uint4 u;
+        uint16_t h[8];
+      } t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t.h[e] = (gk + e < K) ? q[e] : (uint16_t)0;
+      r[i] = t.u;
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+    uint16_t* d = lds + (threadIdx.x >> 3) * PITCH + kc;
+#pragma unroll
+    for (int i = 0; i < V; ++i) *(uint4*)(d + i * RS * PITCH) = r[i];
+  }
+};
+
+// int8 rows: ROWS x 64 bytes = ROWS*4 vectors of 16 values per tile, widened
+// to bf16 when written to LDS (same clamping and tail rules).
+template <int ROWS, int NT>
+struct Tile8 {
+  static constexpr int V = ROWS * 4 / NT;
+  static constexpr int RS = NT / 4;
+  const int8_t* base;
+  int64_t ld, last, row0;
+  int kc;
+  uint4 r[V];
+  __device__ __forceinline__ void init(const int8_t* b, int64_t ld_, int64_t rows, int64_t r0) {
+    base = b;
+    ld = ld_;
+    last = rows - 1;
+    row0 = r0 + (threadIdx.x >> 2);
+    kc = (threadIdx.x & 3) * 16;
+  }
+  __device__ __forceinline__ const int8_t* at(int i, int64_t k0) const {
+    const int64_t gr = min(row0 + (int64_t)i * RS, last);
+    return base + gr * ld + kc + k0;
+  }
+  __device__ __forceinline__ void load_full(int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) r[i] = *(const uint4*)at(i, k0);
+  }
+  __device__ __forceinline__ void load_tail(int64_t k0, int64_t K) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int8_t* q = at(i, k0);
+      const int64_t gk = k0 + kc;
+      union {
+        uint4 u;
+        int8_t b[16];
+      } t;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) t.b[e] = (gk + e < K) ? q[e] : (int8_t)0;
+      r[i] = t.u;
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* lds) const {
+    uint16_t* d = lds + (threadIdx.x >> 2) * PITCH + kc;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      union {
+        uint4 u;
+        int8_t b[16];
+      } in;
+      in.u = r[i];
+      union {
+        uint4 u[2];
+        uint16_t h[16];
+      } out;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) out.h[e] = (uint16_t)(__float_as_uint((float)in.b[e]) >> 16);
+      *(uint4*)(d + i * RS * PITCH) = out.u[0];
+      *(uint4*)(d + i * RS * PITCH + 8) = out.u[1];
+    }
+  }
+};
+
+template <typename T, int BM, int BN, int WM, int WN, bool B_INT8, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_mfma_kernel(GemmArgs p) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;  // per-wave sub-tile
+  constexpr int FM = TM / 32, FN = TN / 32;  // MFMA tiles per wave
+  typedef typename MfmaOp<T>::vec vec;
+  extern __shared__ __align__(16) uint16_t smem[];
+  // stage s: A at smem + s*BM*PITCH, B at smem + 2*BM*PITCH + s*BN*PITCH
+  auto As = [&](int s) { return smem + s * BM * PITCH; };
+  auto Bs = [&](int s) { return smem + 2 * BM * PITCH + s * BN * PITCH; };
+
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  const int64_t batch = blockIdx.y;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lrow = lane & 31, lk = (lane >> 5) * 8;
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+
+  Tile16<BM, NT> ta;
+  typename std::conditional<B_INT8, Tile8<BN, NT>, Tile16<BN, NT>>::type tb;
+  ta.init(p.a + batch * p.sa, p.lda, p.M, m0);
+  if constexpr (B_INT8)
+    tb.init((const int8_t*)p.b + batch * p.sb, p.ldb, p.N, n0);
+  else
+    tb.init((const uint16_t*)p.b + batch * p.sb, p.ldb, p.N, n0);
+
+  // MFMAs over one LDS stage, operand fragments double-buffered across the
+  // four 16-deep substeps.
+  auto compute = [&](int st) {
+    const uint16_t* a_s = As(st) + (wm * TM + lrow) * PITCH + lk;
+    const uint16_t* b_s = Bs(st) + (wn * TN + lrow) * PITCH + lk;
+    vec af[2][FM], bf[2][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[0][i] = *(const vec*)(a_s + i * 32 * PITCH);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[0][j] = *(const vec*)(b_s + j * 32 * PITCH);
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int c = s & 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          af[c ^ 1][i] = *(const vec*)(a_s + i * 32 * PITCH + (s + 1) * 16);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          bf[c ^ 1][j] = *(const vec*)(b_s + j * 32 * PITCH + (s + 1) * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MfmaOp<T>::mma(af[c][i], bf[c][j], acc[i][j]);
+    }
+  };
+
+  // Steps 0 .. KF-1 are full 64-deep steps, step KF (if K % 64) is partial.
+  // The main loop only ever prefetches full steps, so it has no branch.
+  const int KF = (int)(p.K / BK);
+  const bool tail = KF * (int64_t)BK < p.K;
+  if (KF > 0) {
+    ta.load_full(0);
+    tb.load_full(0);
+  } else {
+    ta.load_tail(0, p.K);
+    tb.load_tail(0, p.K);
+  }
+  ta.store(As(0));
+  tb.store(Bs(0));
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < KF; ++kt) {
+    ta.load_full((int64_t)(kt + 1) * BK);
+    tb.load_full((int64_t)(kt + 1) * BK);
+    // keep the next step's global loads issued ahead of this step's MFMAs
+    // (the scheduler would otherwise sink them next to their LDS stores and
+    // expose their latency)
+    __builtin_amdgcn_sched_barrier(0);
+    compute(kt & 1);
+    ta.store(As((kt + 1) & 1));
+    tb.store(Bs((kt + 1) & 1));
+    __syncthreads();
+  }
+  if (tail && KF > 0) {
+    ta.load_tail((int64_t)KF * BK, p.K);
+    tb.load_tail((int64_t)KF * BK, p.K);
+    compute(kt & 1);
+    ta.store(As((kt + 1) & 1));
+    tb.store(Bs((kt + 1) & 1));
+    __syncthreads();
+    ++kt;
+  }
+  compute(kt & 1);
+
+  // epilogue: out = alpha * acc (* scale[n]) + beta * bias, rounded once.  The
+  // bias is fp32 or of the output's type (the host converts anything else).
+  uint16_t* C = p.c + batch * p.sc;
+  const bool bias_f32 = p.bias_dtype == MI_F32;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t n = n0 + wn * TN + j * 32 + lrow;
+    if (n >= p.N) continue;
+    const int64_t bcol = batch * p.bias_sb + n * p.bias_sn;
+    const float colscale = B_INT8 ? p.alpha * p.scale[n] : p.alpha;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < p.M) {
+          float v = colscale * acc[i][j][r];
+          if (HAS_BIAS) {
+            const int64_t bo = bcol + m * p.bias_sm;
+            const float bv = bias_f32 ? ((const float*)p.bias)[bo]
+                                      : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo]);
+            v += p.beta * bv;
+          }
+          C[m * p.ldc + n] = MfmaOp<T>::store(v);
+        }
+      }
+    }
+  }
+}
+
+// ---- fp32: VALU tiled kernel (64 x 64 tile, 4 x 4 outputs per lane) ----------------
+
+struct GemmF32Args {
+  const float* a;
+  const float* b;
+  float* c;
+  const void* bias;
+  int bias_dtype;
+  int64_t bias_sm, bias_sn, bias_sb;
+  int64_t M, N, K;
+  int64_t a_sm, a_sk, b_sk, b_sn, ldc;
+  int64_t sa, sb, sc;
+  float alpha, beta;
+};
+
+template <bool HAS_BIAS>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32Args p) {
+  __shared__ float As[16][64 + 4];
+  __shared__ float Bs[16][64 + 4];
+  const int64_t batch = blockIdx.z;
+  const float* A = p.a + batch * p.sa;
+  const float* B = p.b + batch * p.sb;
+  const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < p.K; k0 += 16) {
+    for (int v = threadIdx.x; v < 16 * 64; v += 256) {
+      const int kk = v / 64, mm = v % 64;
+      const int64_t gm = m0 + mm, gk = k0 + kk;
+      As[kk][mm] = (gm < p.M && gk < p.K) ? A[gm * p.a_sm + gk * p.a_sk] : 0.f;
+      const int64_t gn = n0 + mm;
+      Bs[kk][mm] = (gn < p.N && gk < p.K) ? B[gk * p.b_sk + gn * p.b_sn] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  float* C = p.c + batch * p.sc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + ty * 4 + i;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = n0 + tx * 4 + j;
+      if (n >= p.N) continue;
+      float v = p.alpha * acc[i][j];
+      if (HAS_BIAS)
+        v += p.beta * load_as<float>(p.bias, batch * p.bias_sb + m * p.bias_sm + n * p.bias_sn,
+                                     p.bias_dtype);
+      C[m * p.ldc + n] = v;
+    }
+  }
+}
+
+// ---- host side --------------------------------------------------------------------
+
+// A batched matrix view: element (b, r, c) at data + b*sb + r*s0 + c*s1.
+struct Mat {
+  void* data;
+  int dtype;
+  int64_t batch, rows, cols;
+  int64_t sb, s0, s1;
+};
+
+mi_status_t as_mat(const mi_tensor_t* t, const char* name, Mat* m) {
+  MI_RETURN_IF(validate(t, name));
+  if (t->ndim == 2) {
+    *m = Mat{t->data, t->dtype, 1, t->sizes[0], t->sizes[1], 0, t->strides[0], t->strides[1]};
+  } else if (t->ndim == 3) {
+    *m = Mat{t->data, t->dtype, t->sizes[0], t->sizes[1], t->sizes[2],
+             t->sizes[0] == 1 ? 0 : t->strides[0], t->strides[1], t->strides[2]};
+  } else {
+    MI_FAIL(MI_ERR_INVALID, "%s: expected a 2-D or 3-D tensor, got %d dims", name, t->ndim);
+  }
+  return MI_OK;
+}
+
+mi_tensor_t mat_desc(const Mat& m) {
+  mi_tensor_t t{};
+  t.data = m.data;
+  t.dtype = m.dtype;
+  t.ndim = 3;
+  t.sizes[0] = m.batch;
+  t.sizes[1] = m.rows;
+  t.sizes[2] = m.cols;
+  t.strides[0] = m.sb;
+  t.strides[1] = m.s0;
+  t.strides[2] = m.s1;
+  return t;
+}
+
+// Rows of `m` must be contiguous along the columns, 16-byte aligned, with a
+// leading dim that keeps every row 16-byte aligned; otherwise `m` is copied
+// densely (leading dim rounded up to 16 bytes) into workspace.
+mi_status_t dense_rows(Mat& m, Workspace& ws, hipStream_t stream) {
+  const int es = dtype_size(m.dtype);
+  const int64_t align_el = 16 / es;
+  const bool unit = m.s1 == 1 || m.cols == 1;
+  const bool ok = unit && (m.rows == 1 || (m.s0 % align_el == 0 && m.s0 >= m.cols)) &&
+                  ((uintptr_t)m.data % 16) == 0 && (m.batch == 1 || m.sb % align_el == 0);
+  if (ok) {
+    if (m.rows == 1) m.s0 = (m.cols + align_el - 1) / align_el * align_el;
+    m.s1 = 1;
+    return MI_OK;
+  }
+  const int64_t ld = (m.cols + align_el - 1) / align_el * align_el;
+  MI_RETURN_IF(ws.alloc((size_t)(m.batch * m.rows * ld) * es, stream));
+  Mat d{ws.get(), m.dtype, m.batch, m.rows, m.cols, m.rows * ld, ld, 1};
+  mi_tensor_t dt = mat_desc(d), st = mat_desc(m);
+  MI_RETURN_IF(mi_copy(&dt, &st, (mi_stream_t)stream));
+  m = d;
+  return MI_OK;
+}
+
+Mat transposed(const Mat& m) {
+  return Mat{m.data, m.dtype, m.batch, m.cols, m.rows, m.sb, m.s1, m.s0};
+}
+
+template <typename T, int BM, int BN, int WM, int WN, bool I8, bool HB>
+struct Cfg {
+  static void* fn() { return (void*)gemm_mfma_kernel<T, BM, BN, WM, WN, I8, HB>; }
+  static size_t lds() { return (size_t)2 * (BM + BN) * PITCH * sizeof(uint16_t); }
+  static mi_status_t launch(const GemmArgs& q0, int64_t batch, hipStream_t s, const char* what) {
+    static bool attr = [] {
+      (void)hipFuncSetAttribute(fn(), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds());
+      return true;
+    }();
+    (void)attr;
+    GemmArgs q = q0;
+    q.tiles_m = (int)((q.M + BM - 1) / BM);
+    q.tiles_n = (int)((q.N + BN - 1) / BN);
+    dim3 grid((unsigned)(q.tiles_m * q.tiles_n), (unsigned)batch);
+    hipLaunchKernelGGL((gemm_mfma_kernel<T, BM, BN, WM, WN, I8, HB>), grid, dim3(64 * WM * WN),
+                       lds(), s, q);
+    return check_launch(what);
+  }
+};
+
+// Tile configuration by problem shape: 256 x 256 when there are enough tiles
+// to fill the 256 CUs, narrower N tiles for short-M problems.
+template <typename T, bool I8, bool HB>
+mi_status_t launch_mfma(const GemmArgs& q, int64_t batch, hipStream_t s, const char* what) {
+  const int64_t cus = cu_count();
+  const int64_t big = ((q.M + 255) / 256) * ((q.N + 255) / 256) * batch;
+  if (big >= cus) return Cfg<T, 256, 256, 2, 4, I8, HB>::launch(q, batch, s, what);
+  if (q.M <= 32) return Cfg<T, 32, 64, 1, 2, I8, HB>::launch(q, batch, s, what);
+  const int64_t mid = ((q.M + 127) / 128) * ((q.N + 127) / 128) * batch;
+  if (mid >= cus / 2) return Cfg<T, 128, 128, 2, 2, I8, HB>::launch(q, batch, s, what);
+  return Cfg<T, 128, 64, 2, 2, I8, HB>::launch(q, batch, s, what);
+}
+
+template <typename T>
+mi_status_t dispatch_mfma(const GemmArgs& q, bool int8, bool has_bias, int64_t batch,
+                          hipStream_t s, const char* what) {
+  if (int8) {
+    if (has_bias) return launch_mfma<T, true, true>(q, batch, s, what);
+    return launch_mfma<T, true, false>(q, batch, s, what);
+  }
+  if (has_bias) return launch_mfma<T, false, true>(q, batch, s, what);
+  return launch_mfma<T, false, false>(q, batch, s, what);
+}
+
+struct BiasView {
+  const void* data = nullptr;
+  int dtype = MI_F32;
+  int64_t sb = 0, sm = 0, sn = 0;
+};
+
+mi_status_t bias_view(const mi_tensor_t* bias, int64_t batch, int64_t M, int64_t N,
+                      const char* what, BiasView* bv) {
+  MI_RETURN_IF(validate(bias, "bias"));
+  MI_CHECK_ARG(bias->ndim <= 3, "%s: bias has too many dims", what);
+  int64_t sz[3] = {1, 1, 1}, st[3] = {0, 0, 0};
+  const int off = 3 - bias->ndim;
+  for (int d = 0; d < bias->ndim; ++d) {
+    sz[off + d] = bias->sizes[d];
+    st[off + d] = bias->sizes[d] == 1 ? 0 : bias->strides[d];
+  }
+  MI_CHECK_ARG((sz[0] == 1 || sz[0] == batch) && (sz[1] == 1 || sz[1] == M) &&
+                   (sz[2] == 1 || sz[2] == N),
+               "%s: bias does not broadcast to the output", what);
+  bv->data = bias->data;
+  bv->dtype = bias->dtype;
+  bv->sb = st[0];
+  bv->sm = st[1];
+  bv->sn = st[2];
+  return MI_OK;
+}
+
+// Converts a bias of a dtype the epilogue does not read into a dense fp32
+// copy in workspace (same shape, so the broadcast view is unchanged).
+mi_status_t bias_to_f32(const mi_tensor_t* bias, Workspace& ws, hipStream_t stream,
+                        BiasView* bv) {
+  mi_tensor_t dst = *bias;
+  MI_RETURN_IF(ws.alloc((size_t)numel(*bias) * 4, stream));
+  dst.data = ws.get();
+  dst.dtype = MI_F32;
+  int64_t s = 1;
+  for (int d = dst.ndim - 1; d >= 0; --d) {
+    dst.strides[d] = s;
+    s *= dst.sizes[d];
+  }
+  MI_RETURN_IF(mi_copy(&dst, bias, (mi_stream_t)stream));
+  int64_t st[3] = {0, 0, 0};
+  const int off = 3 - dst.ndim;
+  for (int d = 0; d < dst.ndim; ++d) st[off + d] = dst.sizes[d] == 1 ? 0 : dst.strides[d];
+  bv->data = ws.get();
+  bv->dtype = MI_F32;
+  bv->sb = st[0];
+  bv->sm = st[1];
+  bv->sn = st[2];
+  return MI_OK;
+}
+
+// out[b] = beta * bias[b] + alpha * a[b] @ b[b]; `wt` (when not NULL) is an
+// int8 weight [N, K] with per-N fp32 `scale`, used instead of `b`.
+mi_status_t run_gemm(const mi_tensor_t* out, const mi_tensor_t* a, const mi_tensor_t* b,
+                     const mi_tensor_t* wt, const mi_tensor_t* scale, const mi_tensor_t* bias,
+                     double alpha, double beta, hipStream_t stream, const char* what) {
+  clear_error();
+  Mat A, B, C;
+  const bool int8 = wt != nullptr;
+  MI_RETURN_IF(as_mat(a, "mat1", &A));
+  if (int8) {
+    MI_RETURN_IF(as_mat(wt, "weight", &B));
+    MI_CHECK_ARG(B.batch == 1 && wt->ndim == 2, "%s: weight must be 2-D [N, K]", what);
+    MI_CHECK_ARG(B.dtype == MI_I8, "%s: weight must be int8", what);
+    B = transposed(B);  // [K, N] view of the weight
+  } else {
+    MI_RETURN_IF(as_mat(b, "mat2", &B));
+  }
+  MI_RETURN_IF(as_mat(out, "out", &C));
+  MI_CHECK_ARG(A.dtype == C.dtype && (int8 || B.dtype == A.dtype),
+               "%s: expected operands and out of one dtype, got %s, %s, %s", what,
+               dtype_name(A.dtype), dtype_name(B.dtype), dtype_name(C.dtype));
+  MI_CHECK_ARG(A.dtype == MI_BF16 || A.dtype == MI_F16 || (A.dtype == MI_F32 && !int8),
+               "%s: dtype %s is not supported", what, dtype_name(A.dtype));
+  MI_CHECK_ARG(A.cols == B.rows,
+               "%s: mat1 and mat2 shapes cannot be multiplied (%lldx%lld and %lldx%lld)", what,
+               (long long)A.rows, (long long)A.cols, (long long)B.rows, (long long)B.cols);
+  const int64_t batch = std::max(A.batch, std::max(B.batch, C.batch));
+  MI_CHECK_ARG((A.batch == batch || A.batch == 1) && (B.batch == batch || B.batch == 1) &&
+                   C.batch == batch,
+               "%s: batch sizes differ", what);
+  MI_CHECK_ARG(C.rows == A.rows && C.cols == B.cols,
+               "%s: out has shape %lldx%lld, expected %lldx%lld", what, (long long)C.rows,
+               (long long)C.cols, (long long)A.rows, (long long)B.cols);
+  MI_CHECK_ARG(batch <= 65535, "%s: batch too large", what);
+  if (A.batch == 1) A.sb = 0;
+  if (B.batch == 1) B.sb = 0;
+  A.batch = B.batch = batch;
+  const int64_t M = A.rows, N = B.cols, K = A.cols;
+  if (int8) {
+    MI_RETURN_IF(validate(scale, "scales"));
+    MI_CHECK_ARG(scale->dtype == MI_F32 && numel(*scale) == N && is_contiguous(*scale),
+                 "%s: scales must be a dense fp32 vector of %lld elements", what, (long long)N);
+  }
+  if (M == 0 || N == 0 || batch == 0) return MI_OK;
+  const bool has_bias = bias != nullptr && bias->data != nullptr && beta != 0.0;
+  BiasView bv;
+  Workspace wbias;
+  if (has_bias) {
+    MI_RETURN_IF(bias_view(bias, batch, M, N, what, &bv));
+    if (A.dtype != MI_F32 && bv.dtype != MI_F32 && bv.dtype != A.dtype)
+      MI_RETURN_IF(bias_to_f32(bias, wbias, stream, &bv));
+  }
+  if (K == 0) {
+    mi_tensor_t ct = mat_desc(C);
+    mi_scalar_t z{};
+    z.dtype = MI_F64;
+    z.wrapped = 1;
+    if (!has_bias) return mi_fill(&ct, z, (mi_stream_t)stream);
+    mi_tensor_t bt{};
+    bt.data = (void*)bv.data;
+    bt.dtype = bv.dtype;
+    bt.ndim = 3;
+    bt.sizes[0] = batch;
+    bt.sizes[1] = M;
+    bt.sizes[2] = N;
+    bt.strides[0] = bv.sb;
+    bt.strides[1] = bv.sm;
+    bt.strides[2] = bv.sn;
+    mi_scalar_t bs = z;
+    bs.f = beta;
+    return mi_mul_scalar(&ct, &bt, bs, (mi_stream_t)stream);
+  }
+
+  if (A.dtype == MI_F32) {
+    MI_CHECK_ARG(C.s1 == 1 || N == 1, "%s: out must have unit column stride", what);
+    GemmF32Args q{};
+    q.a = (const float*)A.data;
+    q.b = (const float*)B.data;
+    q.c = (float*)C.data;
+    q.bias = bv.data;
+    q.bias_dtype = bv.dtype;
+    q.bias_sm = bv.sm;
+    q.bias_sn = bv.sn;
+    q.bias_sb = bv.sb;
+    q.M = M;
+    q.N = N;
+    q.K = K;
+    q.a_sm = A.s0;
+    q.a_sk = A.s1;
+    q.b_sk = B.s0;
+    q.b_sn = B.s1;
+    q.ldc = C.s0;
+    q.sa = A.sb;
+    q.sb = B.sb;
+    q.sc = C.sb;
+    q.alpha = (float)alpha;
+    q.beta = (float)beta;
+    dim3 grid(ceil_div_u(N, 64), ceil_div_u(M, 64), (unsigned)batch);
+    if (has_bias) hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(256), 0, stream, q);
+    else hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(256), 0, stream, q);
+    return check_launch(what);
+  }
+
+  // MFMA path: A as [M, K] rows, B as [N, K] rows (B^T with K contiguous)
+  Workspace wa, wb, wc;
+  Mat Bt = transposed(B);
+  MI_RETURN_IF(dense_rows(A, wa, stream));
+  MI_RETURN_IF(dense_rows(Bt, wb, stream));
+  Mat Cw = C;
+  const bool c_ok = (C.s1 == 1 || N == 1) && (C.batch == 1 || C.sb != 0);
+  if (!c_ok) {
+    MI_RETURN_IF(wc.alloc((size_t)(batch * M * N) * 2, stream));
+    Cw = Mat{wc.get(), C.dtype, batch, M, N, M * N, N, 1};
+  }
+  GemmArgs q{};
+  q.a = (const uint16_t*)A.data;
+  q.b = Bt.data;
+  q.c = (uint16_t*)Cw.data;
+  q.bias = bv.data;
+  q.scale = int8 ? (const float*)scale->data : nullptr;
+  q.bias_dtype = bv.dtype;
+  q.bias_sm = bv.sm;
+  q.bias_sn = bv.sn;
+  q.bias_sb = bv.sb;
+  q.M = M;
+  q.N = N;
+  q.K = K;
+  q.lda = A.s0;
+  q.ldb = Bt.s0;
+  q.ldc = Cw.s0;
+  q.sa = A.sb;
+  q.sb = Bt.sb;
+  q.sc = Cw.sb;
+  q.alpha = (float)alpha;
+  q.beta = (float)beta;
+  if (A.dtype == MI_BF16) MI_RETURN_IF(dispatch_mfma<BF16>(q, int8, has_bias, batch, stream, what));
+  else MI_RETURN_IF(dispatch_mfma<F16>(q, int8, has_bias, batch, stream, what));
+  if (!c_ok) {
+    mi_tensor_t dst = mat_desc(C), src = mat_desc(Cw);
+    MI_RETURN_IF(mi_copy(&dst, &src, (mi_stream_t)stream));
+  }
+  return MI_OK;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+mi_status_t mi_addmm(const mi_tensor_t* out, const mi_tensor_t* self, const mi_tensor_t* mat1,
+                     const mi_tensor_t* mat2, double beta, double alpha, mi_stream_t stream) {
+  return run_gemm(out, mat1, mat2, nullptr, nullptr, self, alpha, beta, (hipStream_t)stream,
+                  "addmm");
+}
+
+mi_status_t mi_mm(const mi_tensor_t* out, const mi_tensor_t* self, const mi_tensor_t* mat2,
+                  mi_stream_t stream) {
+  return run_gemm(out, self, mat2, nullptr, nullptr, nullptr, 1.0, 0.0, (hipStream_t)stream, "mm");
+}
+
+mi_status_t mi_bmm(const mi_tensor_t* out, const mi_tensor_t* self, const mi_tensor_t* mat2,
+                   mi_stream_t stream) {
+  clear_error();
+  MI_CHECK_ARG(self && mat2 && out, "bmm: NULL descriptor");
+  MI_CHECK_ARG(self->ndim == 3 && mat2->ndim == 3 && out->ndim == 3, "bmm: expected 3-D tensors");
+  MI_CHECK_ARG(self->sizes[0] == mat2->sizes[0], "bmm: batch sizes differ");
+  return run_gemm(out, self, mat2, nullptr, nullptr, nullptr, 1.0, 0.0, (hipStream_t)stream, "bmm");
+}
+
+mi_status_t mi_baddbmm(const mi_tensor_t* out, const mi_tensor_t* self, const mi_tensor_t* batch1,
+                       const mi_tensor_t* batch2, double beta, double alpha, mi_stream_t stream) {
+  return run_gemm(out, batch1, batch2, nullptr, nullptr, self, alpha, beta, (hipStream_t)stream,
+                  "baddbmm");
+}
+
+mi_status_t mi_int8_linear(const mi_tensor_t* out, const mi_tensor_t* x, const mi_tensor_t* weight,
+                           const mi_tensor_t* scales, const mi_tensor_t* bias, mi_stream_t stream) {
+  clear_error();
+  MI_CHECK_ARG(out && x && weight && scales, "int8_linear: NULL descriptor");
+  MI_CHECK_ARG(x->ndim == 2 && out->ndim == 2, "int8_linear: x and out must be 2-D");
+  return run_gemm(out, x, nullptr, weight, scales, bias, 1.0, 1.0, (hipStream_t)stream,
+                  "int8_linear");
+}
+
+}  // extern "C"

@@ -85,6 +85,11 @@ _SIGNATURES = {
     "mi_rms_norm": ([_T, _T, _T, ctypes.c_double, _S], ctypes.c_int),
     "mi_rope": ([_T, _T, _T, _T, _T, ctypes.c_double, _S], ctypes.c_int),
     "mi_silu_mul": ([_T, _T, _T, _S], ctypes.c_int),
+    "mi_addmm": ([_T, _T, _T, _T, ctypes.c_double, ctypes.c_double, _S], ctypes.c_int),
+    "mi_mm": ([_T, _T, _T, _S], ctypes.c_int),
+    "mi_bmm": ([_T, _T, _T, _S], ctypes.c_int),
+    "mi_baddbmm": ([_T, _T, _T, _T, ctypes.c_double, ctypes.c_double, _S], ctypes.c_int),
+    "mi_int8_linear": ([_T, _T, _T, _T, _T, _S], ctypes.c_int),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -272,4 +277,32 @@ def rope(q_out, k_out, q, k, positions, theta):
 
 def silu_mul(out, gate, up):
     check("mi_silu_mul", lib().mi_silu_mul(desc(out), desc(gate), desc(up), stream_of(out)))
+    return out
+
+
+def addmm(out, bias, a, b, beta=1.0, alpha=1.0):
+    check("mi_addmm", lib().mi_addmm(desc(out), desc(bias), desc(a), desc(b), beta, alpha,
+                                     stream_of(out)))
+    return out
+
+
+def mm(out, a, b):
+    check("mi_mm", lib().mi_mm(desc(out), desc(a), desc(b), stream_of(out)))
+    return out
+
+
+def bmm(out, a, b):
+    check("mi_bmm", lib().mi_bmm(desc(out), desc(a), desc(b), stream_of(out)))
+    return out
+
+
+def baddbmm(out, bias, a, b, beta=1.0, alpha=1.0):
+    check("mi_baddbmm", lib().mi_baddbmm(desc(out), desc(bias), desc(a), desc(b), beta, alpha,
+                                         stream_of(out)))
+    return out
+
+
+def int8_linear(out, x, weight, scales, bias=None):
+    check("mi_int8_linear", lib().mi_int8_linear(desc(out), desc(x), desc(weight), desc(scales),
+                                                 desc(bias), stream_of(out)))
     return out
