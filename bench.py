@@ -265,7 +265,56 @@ def other_ops(torch, _abi, synthetic):
                         lambda s: _abi.silu_mul(s["o"], s["g"], s["u"]), 1082130432))
     del gs, gt, up, c3
     res.extend(gemm_ops(torch, _abi))
+    res.extend(decoder_ops(torch))
     return res
+
+
+def decoder_ops(torch, steps=5):
+    """Config 5: Llama-7B-shaped decoder layer forward, batch 8 x seq 2048,
+    random-init bf16 weights, through the gcu PrivateUse1 ops: eager, then a
+    GCUGraph replay of the same layer; tokens/s and allocator peak/reserved."""
+    import torch_gcu  # noqa: F401
+    from torch_gcu.utils import decoder_layer as dl
+
+    log("bench: config 5 decoder layer")
+    cfg = dl.LayerConfig()
+    B, S = 8, 2048
+    w = {k: v.to("gcu") for k, v in dl.init_weights(cfg).items()}
+    gen = torch.Generator().manual_seed(20261205)
+    ids = torch.randint(0, cfg.vocab, (B, S), generator=gen).to("gcu")
+    pos = dl.positions(B, S, "gcu")
+    flops = dl.flops(cfg, B, S)
+    for _ in range(2):
+        dl.forward(w, ids, cfg, pos)
+    torch.gcu.synchronize()
+    torch.gcu.reset_peak_memory_stats()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dl.forward(w, ids, cfg, pos)
+    torch.gcu.synchronize()
+    eager_s = (time.perf_counter() - t0) / steps
+    peak = torch.gcu.max_memory_allocated()
+    reserved = torch.gcu.memory_reserved()
+    graph = torch.gcu.GCUGraph()
+    with torch.gcu.graph(graph):
+        dl.forward(w, ids, cfg, pos)
+    graph.replay()
+    torch.gcu.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.gcu.synchronize()
+    graph_s = (time.perf_counter() - t0) / steps
+    graph.reset()
+    tokens = B * S
+    out = []
+    for name, sec in [("eager", eager_s), ("gcugraph replay", graph_s)]:
+        tf = flops / sec / 1e12
+        out.append({"op": f"c5.decoder_layer fwd B8xS2048 ({name})", "ms": round(sec * 1e3, 3),
+                    "tok/s": round(tokens / sec, 1), "TFLOP/s": round(tf, 1),
+                    "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "flops": flops,
+                    "alloc_peak_bytes": peak, "alloc_reserved_bytes": reserved})
+    return out
 
 
 def main():

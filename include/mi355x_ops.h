@@ -228,6 +228,20 @@ mi_status_t mi_int8_linear(const mi_tensor_t* out, const mi_tensor_t* x,
                            const mi_tensor_t* weight, const mi_tensor_t* scales,
                            const mi_tensor_t* bias, mi_stream_t stream);
 
+/* ---- attention ------------------------------------------------------------------
+ * Flash-attention forward: out = softmax(scale * q k^T [+ causal mask]) v.
+ * q [B, H, Sq, D], k and v [B, Hk, Sk, D] with H a multiple of Hk (query
+ * heads share k/v heads in groups), D = 64 or 128, bf16 or fp16, head_dim
+ * contiguous and rows 16-byte aligned; out like q.  is_causal masks key j
+ * for query i when j > i.  lse (optional, NULL data for none) receives the
+ * fp32 [B, H, Sq] log-sum-exp of the scaled scores.  Replaces
+ * topsatenScaledDotProductFlashAttention
+ * (torch_gcu/csrc/aten/aot_ops/gcu_attention.cpp:59-70). */
+mi_status_t mi_flash_attention_fwd(const mi_tensor_t* out, const mi_tensor_t* lse,
+                                   const mi_tensor_t* q, const mi_tensor_t* k,
+                                   const mi_tensor_t* v, int32_t is_causal,
+                                   double scale, mi_stream_t stream);
+
 /* ---- fused efficient ops ---------------------------------------------------
  * The reference's efficient_ops entry point pattern
  * (torch_gcu/csrc/efficient_ops/ops.h:14-93, pybind at

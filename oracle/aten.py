@@ -143,6 +143,24 @@ def bmm(a, b):
     return torch.bmm(a.float(), b.float()).to(a.dtype)
 
 
+def sdpa(q, k, v, is_causal=False, scale=None):
+    """Scaled dot-product attention as CPU ATen runs it for [B, H, S, D]
+    inputs: _scaled_dot_product_flash_attention_for_cpu (the CPU kernel
+    F.scaled_dot_product_attention selects; for bf16 it rounds the softmax
+    weights to bf16 before the P V product, as GPU flash kernels do).  k/v
+    heads are repeated to the query heads when fewer.  Returns (out, lse).
+    The reference reaches attention through _scaled_dot_product_flash_attention
+    (torch_gcu/csrc/aten/GCUNativeFunctions.cpp:49-102).  Pinned by the fp32
+    closed form softmax(scale q k^T + mask) v in tests/test_oracle.py."""
+    H, Hk = q.shape[1], k.shape[1]
+    if Hk != H:
+        k = k.repeat_interleave(H // Hk, dim=1)
+        v = v.repeat_interleave(H // Hk, dim=1)
+    out, lse = torch.ops.aten._scaled_dot_product_flash_attention_for_cpu(
+        q, k, v, 0.0, is_causal, scale=scale)
+    return out, lse
+
+
 def int8_linear(x, w, scales, bias=None):
     """int8 weight-only linear, fp32 closed form (x @ W^T) * scales (+ bias)
     with one cast; new efficient op, no reference counterpart.  Pinned by

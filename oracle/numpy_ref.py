@@ -83,3 +83,27 @@ def rope64(x, positions, theta):
 def silu_mul64(g, u):
     g = np.asarray(g, dtype=np.float64)
     return g / (1.0 + np.exp(-g)) * np.asarray(u, dtype=np.float64)
+
+
+def matmul64(a, b):
+    return np.asarray(a, dtype=np.float64) @ np.asarray(b, dtype=np.float64)
+
+
+def attention64(q, k, v, causal, scale=None):
+    """softmax(scale q k^T + mask) v in float64 for [B, H, Sq, D] q and
+    [B, Hk, Sk, D] k/v (query head h reads kv head h * Hk // H); the causal
+    mask is top-left aligned (key j visible to query i when j <= i).
+    Returns (out, lse) with lse the natural-log row log-sum-exp."""
+    q, k, v = (np.asarray(t, dtype=np.float64) for t in (q, k, v))
+    H, Hk = q.shape[1], k.shape[1]
+    idx = np.arange(H) * Hk // H
+    k, v = k[:, idx], v[:, idx]
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    s = np.einsum("bhqd,bhkd->bhqk", q, k) * scale
+    if causal:
+        Sq, Sk = s.shape[-2:]
+        s = np.where(np.arange(Sk)[None, :] > np.arange(Sq)[:, None], -np.inf, s)
+    m = s.max(-1, keepdims=True)
+    e = np.exp(s - m)
+    z = e.sum(-1, keepdims=True)
+    return np.einsum("bhqk,bhkd->bhqd", e / z, v), (m + np.log(z))[..., 0]

@@ -68,3 +68,23 @@ def assert_close(actual: torch.Tensor, expected: torch.Tensor, kind: str, what: 
 def max_rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     a, e = actual.cpu().double(), expected.cpu().double()
     return float(((a - e).abs() / e.abs().clamp_min(1e-30)).max())
+
+
+def rel_l2(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    a, e = actual.cpu().double(), expected.cpu().double()
+    return float((a - e).norm() / e.norm().clamp_min(1e-30))
+
+
+def assert_composed_close(actual: torch.Tensor, cpu: torch.Tensor, truth: torch.Tensor,
+                          what: str = "", factor: float = 1.25) -> None:
+    """Bar for a chain of bf16 ops (a whole decoder layer), where per-op
+    roundings compound and residual sums cancel, so no single elementwise
+    bound of the op bar holds near zero.  `cpu` is CPU ATen's result in the
+    same dtype, `truth` the same chain in fp32.  The device result must be
+    no further from the fp32 truth than CPU ATen is (relative L2, within
+    `factor`), and within 1e-2 relative L2 of CPU ATen itself."""
+    e_dev, e_cpu = rel_l2(actual, truth), rel_l2(cpu, truth)
+    assert e_dev <= factor * e_cpu + 1e-4, (
+        f"{what}: relative L2 error vs fp32 {e_dev:.3g} exceeds {factor} x CPU ATen's {e_cpu:.3g}")
+    d = rel_l2(actual, cpu)
+    assert d <= BF16_RTOL, f"{what}: relative L2 distance to CPU ATen {d:.3g} > {BF16_RTOL}"

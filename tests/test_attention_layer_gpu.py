@@ -1,0 +1,117 @@
+"""Flash-attention forward and the config-5 decoder layer on the GPU.
+
+Attention is compared with CPU ATen's flash attention (oracle.aten.sdpa, which
+like the kernel rounds the softmax weights to bf16 before the P V product);
+the decoder layer on gcu is held to the composed-chain bar against the same
+layer on CPU ATen (bf16) and in fp32, and its GCUGraph replay must equal its
+eager output bit for bit."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import torch_gcu  # noqa: F401
+from oracle import aten
+from oracle.tolerance import assert_close, assert_composed_close, assert_exact
+from torch_gcu import _abi
+from torch_gcu.utils import decoder_layer as dl
+
+pytestmark = pytest.mark.gpu
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rn(shape, seed, dtype=torch.bfloat16):
+    return torch.randn(shape, generator=g(seed)).to(dtype)
+
+
+def ref_attention(q, k, v, causal, scale=None):
+    """CPU ATen flash attention (oracle.aten.sdpa): (out, lse)."""
+    return aten.sdpa(q, k, v, causal, scale)
+
+
+@pytest.mark.parametrize("B,H,Hk,Sq,Sk,D,causal", [
+    (2, 4, 4, 256, 256, 128, True),
+    (1, 2, 2, 200, 200, 64, False),
+    (1, 8, 2, 130, 130, 128, True),
+    (2, 2, 2, 96, 300, 128, False),
+    (1, 1, 1, 1, 77, 128, False),
+    (1, 2, 2, 129, 129, 64, True),
+])
+def test_flash_attention_parity(B, H, Hk, Sq, Sk, D, causal):
+    q, k, v = rn((B, H, Sq, D), 1), rn((B, Hk, Sk, D), 2), rn((B, Hk, Sk, D), 3)
+    ref, ref_lse = ref_attention(q, k, v, causal)
+    out = torch.empty(B, H, Sq, D, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(B, H, Sq, dtype=torch.float32, device="cuda")
+    _abi.flash_attention_fwd(out, lse, q.cuda(), k.cuda(), v.cuda(), causal)
+    assert_close(out, ref, "bf16", f"attention {B},{H},{Hk},{Sq},{Sk},{D},{causal}")
+    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2 * max(1.0, ref_lse.abs().max().item())
+
+
+def test_config5_attention_shape_head_sample():
+    """[8, 32, 2048, 128] causal: all heads computed, 3 heads checked."""
+    B, H, S, D = 8, 32, 2048, 128
+    q, k, v = rn((B, H, S, D), 4), rn((B, H, S, D), 5), rn((B, H, S, D), 6)
+    out = torch.empty(B, H, S, D, dtype=torch.bfloat16, device="cuda")
+    _abi.flash_attention_fwd(out, None, q.cuda(), k.cuda(), v.cuda(), True)
+    o = out.cpu()
+    for b, h in [(0, 0), (3, 17), (7, 31)]:
+        ref, _ = ref_attention(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], True)
+        assert_close(o[b:b + 1, h:h + 1], ref, "bf16", f"head {b},{h}")
+
+
+def test_sdpa_on_gcu_uses_flash_and_matches():
+    q, k, v = rn((2, 4, 160, 128), 7), rn((2, 4, 160, 128), 8), rn((2, 4, 160, 128), 9)
+    torch_gcu._C._set_op_debug_config("op_statistics=true")
+    torch_gcu._C._clear_op_statistics()
+    try:
+        out = F.scaled_dot_product_attention(q.to("gcu"), k.to("gcu"), v.to("gcu"), is_causal=True)
+        stats = torch_gcu._C._op_statistics()
+    finally:
+        torch_gcu._C._set_op_debug_config("")
+    assert stats.get("_scaled_dot_product_fused_attention_overrideable", (0, 0))[0] == 1, stats
+    ref, _ = ref_attention(q, k, v, True)
+    assert_close(out.cpu(), ref, "bf16", "sdpa gcu")
+    # a float32 mask selects the math path (native bmm + softmax)
+    mask = torch.zeros(160, 160)
+    out2 = F.scaled_dot_product_attention(q.float().to("gcu"), k.float().to("gcu"),
+                                          v.float().to("gcu"), attn_mask=mask.to("gcu"))
+    ref2, _ = ref_attention(q.float(), k.float(), v.float(), False)
+    assert_close(out2.cpu(), ref2, "fp32", "sdpa math path")
+
+
+SMALL = dl.LayerConfig(vocab=1000, hidden=256, heads=2, head_dim=128, ffn=512)
+
+
+def test_decoder_layer_gcu_matches_cpu():
+    w = dl.init_weights(SMALL, seed=11)
+    ids = torch.randint(0, SMALL.vocab, (2, 96), generator=g(12))
+    ref = dl.forward(w, ids, SMALL)
+    truth = dl.forward({k: v.float() for k, v in w.items()}, ids, SMALL)
+    wg = {k: v.to("gcu") for k, v in w.items()}
+    out = dl.forward(wg, ids.to("gcu"), SMALL)
+    assert_composed_close(out.cpu(), ref, truth, "decoder layer")
+
+
+def test_decoder_layer_graph_replay_equals_eager():
+    w = {k: v.to("gcu") for k, v in dl.init_weights(SMALL, seed=13).items()}
+    ids = torch.randint(0, SMALL.vocab, (2, 128), generator=g(14)).to("gcu")
+    pos = dl.positions(2, 128, "gcu")
+    eager = dl.forward(w, ids, SMALL, pos)
+    graph = torch.gcu.GCUGraph()
+    torch.gcu.synchronize()
+    with torch.gcu.graph(graph):
+        out = dl.forward(w, ids, SMALL, pos)
+    for k in range(3):
+        graph.replay()
+        torch.gcu.synchronize()
+        assert_exact(out.cpu(), eager.cpu(), f"replay {k}")
+    new_ids = torch.randint(0, SMALL.vocab, (2, 128), generator=g(15))
+    ids.copy_(new_ids.to("gcu"))
+    graph.replay()
+    torch.gcu.synchronize()
+    assert_exact(out.cpu(), dl.forward(w, ids, SMALL, pos).cpu(), "replay with new ids")
+    graph.reset()

@@ -137,6 +137,48 @@ def test_silu_mul_vs_float64():
                           atol=1e-6)
 
 
+# ---- config 4/5: contractions and attention ---------------------------------------
+
+def test_addmm_bmm_vs_float64():
+    a = torch.randn(64, 96, generator=g(20)).bfloat16()
+    b = torch.randn(96, 48, generator=g(21)).bfloat16()
+    bias = torch.randn(48, generator=g(22)).bfloat16()
+    ref = npr.matmul64(a.float().numpy(), b.float().numpy()) * 0.5 + 2.0 * bias.double().numpy()
+    assert_close(aten.addmm(bias, a, b, beta=2.0, alpha=0.5), torch.from_numpy(ref).bfloat16(),
+                 "bf16", "addmm")
+    a3 = torch.randn(3, 32, 40, generator=g(23)).bfloat16()
+    b3 = torch.randn(3, 40, 24, generator=g(24)).bfloat16()
+    ref3 = np.stack([npr.matmul64(a3[i].float().numpy(), b3[i].float().numpy()) for i in range(3)])
+    assert_close(aten.bmm(a3, b3), torch.from_numpy(ref3).bfloat16(), "bf16", "bmm")
+    # row sampling identity: rows of the product are products of rows
+    assert_exact(aten.addmm(None, a[5:9], b), aten.addmm(None, a, b)[5:9], "addmm rows")
+
+
+def test_int8_linear_vs_float64_and_weight_int8pack_mm():
+    x = torch.randn(16, 128, generator=g(25)).bfloat16()
+    w = torch.randint(-128, 128, (64, 128), generator=g(26), dtype=torch.int8)
+    s = (torch.rand(64, generator=g(27)) * 0.01 + 1e-3).bfloat16()
+    got = aten.int8_linear(x, w, s)
+    ref = npr.matmul64(x.float().numpy(), w.float().numpy().T) * s.double().numpy()
+    assert_close(got, torch.from_numpy(ref).bfloat16(), "bf16", "int8_linear")
+    lib = torch.ops.aten._weight_int8pack_mm(x, w, s)
+    assert_close(got, lib, "bf16", "int8_linear vs _weight_int8pack_mm")
+
+
+@pytest.mark.parametrize("H,Hk,Sq,Sk,causal", [(4, 4, 64, 64, True), (4, 2, 64, 80, False),
+                                               (2, 1, 33, 33, True), (2, 2, 1, 40, False)])
+def test_sdpa_vs_float64(H, Hk, Sq, Sk, causal):
+    q = torch.randn(2, H, Sq, 64, generator=g(28)).bfloat16()
+    k = torch.randn(2, Hk, Sk, 64, generator=g(29)).bfloat16()
+    v = torch.randn(2, Hk, Sk, 64, generator=g(30)).bfloat16()
+    out, lse = aten.sdpa(q, k, v, causal)
+    ro, rl = npr.attention64(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal)
+    assert_close(out, torch.from_numpy(ro).bfloat16(), "bf16", "sdpa out")
+    assert (lse.double() - torch.from_numpy(rl)).abs().max().item() < 1e-3
+    if causal:  # query 0 sees key 0 only: out = v[0], lse = scale * q0.k0
+        assert_exact(out[:, :, 0], v[:, torch.arange(H) * Hk // H, 0], "causal row 0")
+
+
 @pytest.mark.parametrize("name", ["rms_norm", "rope", "silu_mul"])
 def test_golden_fixtures(name):
     path = os.path.join(GOLDEN, f"{name}.npz")
@@ -180,3 +222,8 @@ def test_planted_mistakes_are_caught():
     idx = torch.tensor([3, 1, 5])
     want = torch.from_numpy(npr.index_select(table.numpy(), 0, idx.numpy()))
     assert not torch.equal(aten.index_select(table, 1, idx), want)  # transposed gather
+    q = torch.randn(1, 2, 16, 32, generator=g(17))
+    ro, _ = npr.attention64(q.numpy(), q.numpy(), q.numpy(), True)
+    unscaled = torch.softmax((q @ q.transpose(-1, -2)).masked_fill(
+        torch.ones(16, 16, dtype=torch.bool).triu(1), float("-inf")), -1) @ q
+    assert (unscaled.double() - torch.from_numpy(ro)).abs().max() > 1e-2  # dropped 1/sqrt(d)

@@ -95,6 +95,31 @@ at::Tensor silu_mul(const at::Tensor& gate, const at::Tensor& up) {
   return out;
 }
 
+// int8 weight-only linear: y = (x @ weight^T) * scales (+ bias), x [..., K]
+// bf16/fp16, weight int8 [N, K], scales fp32 [N].
+at::Tensor int8_linear(const at::Tensor& x, const at::Tensor& weight, const at::Tensor& scales,
+                       const std::optional<at::Tensor>& bias) {
+  TORCH_CHECK(is_gcu(x) && is_gcu(weight) && is_gcu(scales),
+              "int8_linear: x, weight and scales must be gcu tensors");
+  TORCH_CHECK(weight.dim() == 2 && weight.scalar_type() == at::kChar,
+              "int8_linear: weight must be int8 [N, K]");
+  TORCH_CHECK(x.size(-1) == weight.size(1), "int8_linear: x has ", x.size(-1),
+              " features, weight expects ", weight.size(1));
+  const c10::DeviceGuard g(x.device());
+  const at::Tensor x2 = x.reshape({-1, x.size(-1)});
+  const at::Tensor w = weight.is_contiguous() ? weight : weight.contiguous();
+  const at::Tensor sc = scales.to(at::kFloat).contiguous();
+  at::Tensor out = at::empty({x2.size(0), w.size(0)}, x.options());
+  const mi_tensor_t o = desc(out), xd = desc(x2), wd = desc(w), sd = desc(sc);
+  mi_tensor_t bd{};
+  if (bias.has_value() && bias->defined()) bd = desc(*bias);
+  check_mi(mi_int8_linear(&o, &xd, &wd, &sd, &bd, mi_stream(out)), "int8_linear");
+  after_op();
+  std::vector<int64_t> shape = x.sizes().vec();
+  shape.back() = w.size(0);
+  return out.view(shape);
+}
+
 // Advanced index with int32 indices (torch_gcu/csrc/efficient_ops/ops.cpp:221-342):
 // one index tensor selecting along dim 0 is an index_select; other patterns
 // run through aten::index after the indices are widened.
@@ -129,6 +154,7 @@ TORCH_LIBRARY(torch_gcu, m) {
   m.def("rope_(Tensor(a!) q, Tensor(b!)? k, Tensor positions, float theta=10000.0) -> ()");
   m.def("silu_mul(Tensor gate, Tensor up) -> Tensor");
   m.def("int32_indices_index(Tensor self, Tensor?[] indices) -> Tensor");
+  m.def("int8_linear(Tensor x, Tensor weight, Tensor scales, Tensor? bias=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(torch_gcu, PrivateUse1, m) {
@@ -137,4 +163,5 @@ TORCH_LIBRARY_IMPL(torch_gcu, PrivateUse1, m) {
   m.impl("rope_", TORCH_FN(torch_gcu::efficient::rope_));
   m.impl("silu_mul", TORCH_FN(torch_gcu::efficient::silu_mul));
   m.impl("int32_indices_index", TORCH_FN(torch_gcu::efficient::int32_indices_index));
+  m.impl("int8_linear", TORCH_FN(torch_gcu::efficient::int8_linear));
 }

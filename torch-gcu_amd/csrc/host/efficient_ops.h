@@ -18,6 +18,8 @@ void rope_(at::Tensor& q, const std::optional<at::Tensor>& k, const at::Tensor& 
 at::Tensor silu_mul(const at::Tensor& gate, const at::Tensor& up);
 at::Tensor int32_indices_index(const at::Tensor& self,
                                const c10::List<std::optional<at::Tensor>>& indices);
+at::Tensor int8_linear(const at::Tensor& x, const at::Tensor& weight, const at::Tensor& scales,
+                       const std::optional<at::Tensor>& bias);
 
 }  // namespace efficient
 }  // namespace torch_gcu

@@ -90,6 +90,8 @@ _SIGNATURES = {
     "mi_bmm": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_baddbmm": ([_T, _T, _T, _T, ctypes.c_double, ctypes.c_double, _S], ctypes.c_int),
     "mi_int8_linear": ([_T, _T, _T, _T, _T, _S], ctypes.c_int),
+    "mi_flash_attention_fwd": ([_T, _T, _T, _T, _T, ctypes.c_int32, ctypes.c_double, _S],
+                               ctypes.c_int),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -305,4 +307,13 @@ def baddbmm(out, bias, a, b, beta=1.0, alpha=1.0):
 def int8_linear(out, x, weight, scales, bias=None):
     check("mi_int8_linear", lib().mi_int8_linear(desc(out), desc(x), desc(weight), desc(scales),
                                                  desc(bias), stream_of(out)))
+    return out
+
+
+def flash_attention_fwd(out, lse, q, k, v, is_causal=True, scale=None):
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    check("mi_flash_attention_fwd",
+          lib().mi_flash_attention_fwd(desc(out), desc(lse), desc(q), desc(k), desc(v),
+                                       int(is_causal), float(scale), stream_of(out)))
     return out

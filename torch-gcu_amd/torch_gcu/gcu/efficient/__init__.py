@@ -36,6 +36,13 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return torch.ops.torch_gcu.silu_mul(gate, up)
 
 
+def int8_linear(x: torch.Tensor, weight: torch.Tensor, scales: torch.Tensor,
+                bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """(x @ weight^T) * scales (+ bias): int8 [N, K] weight, fp32 [N] scales,
+    widened exactly to bf16/fp16 and multiplied on MFMA with fp32 accumulation."""
+    return torch.ops.torch_gcu.int8_linear(x, weight, scales, bias)
+
+
 def gcu_index(self: torch.Tensor, indices: Sequence[Optional[torch.Tensor]]) -> torch.Tensor:
     """self[indices] with int32 index tensors (no int64 upcast on device)."""
     return torch.ops.torch_gcu.int32_indices_index(self, list(indices))
