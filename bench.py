@@ -32,6 +32,7 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "torch-gcu_amd"))
 
 HBM_PEAK_GBS = 8000.0
+CAL_COPY_BYTES = 512 * 2**20
 METRIC = "HBM GB/s (elementwise/norm), MFMA TFLOPS (addmm/int8), decoder-layer tok/s"
 
 
@@ -98,6 +99,11 @@ def run_config2(torch, _abi, synthetic, steps, warmup):
         "mean": torch.empty(sets[0]["m"].shape[1], dtype=torch.float32, device="cuda"),
     }
     timers = {k: EventTimer(torch) for k in outs}
+    # one plain 512 MiB device copy (untimed): under rocprofv3 --pmc its
+    # FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes
+    cal = torch.empty(CAL_COPY_BYTES // 2, dtype=torch.int16, device="cuda")
+    _abi.copy_(torch.empty_like(cal), cal)
+    del cal
 
     def step(i, timed):
         s = sets[i % 2]
@@ -265,8 +271,26 @@ def other_ops(torch, _abi, synthetic):
                         lambda s: _abi.silu_mul(s["o"], s["g"], s["u"]), 1082130432))
     del gs, gt, up, c3
     res.extend(gemm_ops(torch, _abi))
+    res.extend(attention_ops(torch, _abi))
     res.extend(decoder_ops(torch))
     return res
+
+
+def attention_ops(torch, _abi):
+    """Config 5's attention alone: causal SDPA forward, q/k/v bf16
+    [8, 32, 2048, 128], through the flash kernel."""
+    log("bench: config 5 attention")
+    gen = torch.Generator().manual_seed(20261206)
+    B, H, S, D = 8, 32, 2048, 128
+    sets = []
+    for _ in range(2):
+        q, k, v = (torch.randn(B, H, S, D, generator=gen).bfloat16().cuda() for _ in range(3))
+        sets.append({"q": q, "k": k, "v": v})
+    out = torch.empty(B, H, S, D, dtype=torch.bfloat16, device="cuda")
+    flops = 4 * B * H * D * (S * (S + 1) // 2)
+    return [bench_op(torch, "c5.sdpa causal bf16 [8,32,2048,128]", sets,
+                     lambda s: _abi.flash_attention_fwd(out, None, s["q"], s["k"], s["v"], True),
+                     4 * B * H * S * D * 2, iters=10, flops=flops, bound="mfma")]
 
 
 def decoder_ops(torch, steps=5):

@@ -47,7 +47,10 @@ std::tuple<at::Tensor, at::Tensor> run_flash(const at::Tensor& q, const at::Tens
                                              std::optional<double> scale) {
   const c10::DeviceGuard g(q.device());
   const at::Tensor qa = rows_aligned(q), ka = rows_aligned(k), va = rows_aligned(v);
-  at::Tensor out = at::empty(q.sizes(), q.options());
+  // [B, S, H, D] storage viewed as [B, H, S, D]: the usual next step,
+  // out.transpose(1, 2).reshape(B, S, H * D), is then a view, not a copy
+  at::Tensor out =
+      at::empty({q.size(0), q.size(2), q.size(1), q.size(3)}, q.options()).transpose(1, 2);
   at::Tensor lse = at::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(at::kFloat));
   const double sc = scale.has_value() ? *scale : 1.0 / std::sqrt((double)q.size(3));
   const mi_tensor_t o = desc(out), l = desc(lse), qd = desc(qa), kd = desc(ka), vd = desc(va);

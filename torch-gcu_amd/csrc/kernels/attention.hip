@@ -6,19 +6,28 @@
 // (key j is visible to query i when j <= i), as torch's is_causal.
 //
 // A 256-lane block owns 128 query rows (32 per wave) of one (b, h) and walks
-// the keys in tiles of 64:
-//   1. the tile's K rows go to LDS as [key][d] and its V rows as [d][key]
-//      (transposed on the way in, so both MFMA operands are read as 16-byte
-//      runs);
-//   2. S = Q K^T with Q held in registers as MFMA A operands for the whole
-//      block (D/16 fragments per lane), 2 x (D/16) v_mfma_f32_32x32x16;
-//   3. online softmax in fp32 in the log2 domain: each lane holds 16 rows of
-//      one key column, row maxima and sums are reduced across the 32 lanes of
-//      its half-wave with xor shuffles, the running O rows are rescaled;
-//   4. P is rounded to the input type and passed through a per-wave LDS tile
-//      to become the A operand of O += P V (4 x (D/32) MFMAs).
-// Key tiles entirely above the causal diagonal are never visited, and the
-// query tiles are issued longest-first so the causal triangle balances.
+// the keys in tiles of 64, with two LDS stages so the global loads of tile
+// i+1 overlap the MFMAs of tile i (one barrier per tile):
+//   1. K rows go to LDS as [key][d]; V rows as [d][key], transposed on the
+//      way in four keys at a time (one 8-byte LDS store per 4 keys x 1 d);
+//   2. each wave computes the transposed scores S^T = K Q^T (32 keys x its 32
+//      queries per MFMA tile, v_mfma_f32_32x32x16): Q stays in registers as
+//      the B operand for the whole block, so lane l owns query l % 32 and
+//      holds 32 of the tile's 64 keys for it (the other 32 are in lane
+//      l ^ 32);
+//   3. the online softmax is therefore per lane, in fp32, in the log2
+//      domain: the row max needs one exchange between the two half-waves,
+//      the running sum none until the end, and the rescale factor is a
+//      per-lane scalar;
+//   4. P, rounded to the input type, is already laid out as the B operand of
+//      O^T += V^T P^T (keys are fed to the MFMA's k dimension in a permuted
+//      order that matches the S^T accumulator layout, and V^T is read in the
+//      same order), so P never goes through LDS.
+// Key tiles above a wave's causal diagonal are skipped.  Blocks are ordered
+// head-major with the longest query tiles first, and renumbered so each of
+// the 8 XCDs (which receive workgroups round robin) walks a contiguous run of
+// heads: a head's K/V is then read into one XCD's L2 while its query tiles
+// run there.
 #include <cmath>
 
 #include "iter.h"
@@ -28,25 +37,28 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <typename T>
 struct AttnOp;
 template <>
 struct AttnOp<BF16> {
   typedef bf16x8 vec;
+  typedef __bf16 elem;
   static __device__ __forceinline__ f32x16 mma(vec a, vec b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint16_t cvt(float v) { return f32_to_bf16(v); }
 };
 template <>
 struct AttnOp<F16> {
   typedef f16x8 vec;
+  typedef _Float16 elem;
   static __device__ __forceinline__ f32x16 mma(vec a, vec b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint16_t cvt(float v) { return f32_to_f16(v); }
 };
 
 struct AttnArgs {
@@ -64,143 +76,229 @@ struct AttnArgs {
   float scale_log2;  // softmax scale * log2(e)
   int causal;
   int q_tiles;
+  int n_blocks;      // q_tiles * H * B
+  int xcd_remap;     // n_blocks % 8 == 0: renumber blocks per XCD
 };
 
 constexpr int QT = 128;  // query rows per block
 constexpr int KT = 64;   // keys per tile
 constexpr int NT = 256;
 
+template <int D>
+struct FlashCfg {
+  static constexpr int KP = D + 8;                // K pitch ([key][d]), 16 B pad
+  static constexpr int VP = KT + 4;               // V^T pitch ([d][key]), 8 B pad
+  static constexpr int KS = KT * KP;              // elements of one K stage
+  static constexpr int STAGE = KS + D * VP;       // K + V^T
+  static constexpr int KCH = KT * D / 8 / NT;     // 16-byte K chunks per lane
+  static constexpr int VGR = (KT / 4) * (D / 8);  // (4 keys x 8 d) V groups
+  static size_t lds() { return (size_t)2 * STAGE * sizeof(uint16_t); }
+};
+
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
+  return (a & 0xffffu) | (b << 16);
+}
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
+  return (a >> 16) | (b & 0xffff0000u);
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   typedef typename AttnOp<T>::vec vec;
-  constexpr int KP = D + 8;   // K tile pitch ([key][d])
-  constexpr int VP = KT + 8;  // V^T tile pitch ([d][key])
-  constexpr int PP = KT + 8;  // P tile pitch ([row][key])
-  constexpr int DF = D / 16;  // k-steps of S = Q K^T
-  constexpr int DT = D / 32;  // 32-column output tiles of O
-  __shared__ __align__(16) uint16_t Ks[KT * KP];
-  __shared__ __align__(16) uint16_t Vt[D * VP];
-  __shared__ __align__(16) uint16_t Ps[4][32 * PP];
+  typedef FlashCfg<D> C;
+  constexpr int DF = D / 16;  // k-steps of S^T = K Q^T
+  constexpr int DT = D / 32;  // 32-row d tiles of O^T
+  extern __shared__ __align__(16) uint16_t smem[];
 
-  const int qt = p.q_tiles - 1 - (int)blockIdx.x;  // longest rows first
-  const int64_t h = blockIdx.y, b = blockIdx.z;
+  // block -> (b, h, query tile); head-major, longest query tile first
+  int bid = (int)blockIdx.x;
+  if (p.xcd_remap) bid = (bid & 7) * (p.n_blocks >> 3) + (bid >> 3);
+  const int qt = p.q_tiles - 1 - bid % p.q_tiles;
+  const int bh = bid / p.q_tiles;
+  const int64_t h = bh % p.H, b = bh / p.H;
   const int64_t hk = h * p.Hk / p.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, col = lane & 31;
   const int64_t q0 = (int64_t)qt * QT;
   const int64_t wq0 = q0 + wave * 32;  // this wave's first query row
+  const int64_t qrow = wq0 + col;      // the query this lane owns
 
   const uint16_t* Q = p.q + b * p.q_sb + h * p.q_sh;
   const uint16_t* K = p.k + b * p.k_sb + hk * p.k_sh;
   const uint16_t* V = p.v + b * p.v_sb + hk * p.v_sh;
 
-  // Q fragments: lane holds Q[wq0 + col][16 t + 8 half .. +8], rows clamped
+  // B operand of S^T: lane supplies Q[qrow][16 t + 8 half + i], rows clamped
   vec qf[DF];
   {
-    const int64_t r = min(wq0 + col, p.Sq - 1);
+    const int64_t r = min(qrow, p.Sq - 1);
 #pragma unroll
     for (int t = 0; t < DF; ++t) qf[t] = *(const vec*)(Q + r * p.q_ss + 16 * t + 8 * half);
   }
 
+  // ---- K / V staging: global -> registers -> LDS ----
+  u32x4 kr[C::KCH];
+  u32x4 vr0, vr1, vr2, vr3;
+  const bool v_lane = C::VGR >= NT || (int)threadIdx.x < C::VGR;
+  const int vkg = threadIdx.x & 15, vdc = (threadIdx.x >> 4) * 8;
+  auto load_kv = [&](int64_t kv0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
+      const int64_t gk = min(kv0 + key, p.Sk - 1);
+      kr[i] = *(const u32x4*)(K + gk * p.k_ss + dc);
+    }
+    if (v_lane) {
+      const int64_t g0 = kv0 + 4 * vkg, last = p.Sk - 1;
+      vr0 = *(const u32x4*)(V + min(g0, last) * p.v_ss + vdc);
+      vr1 = *(const u32x4*)(V + min(g0 + 1, last) * p.v_ss + vdc);
+      vr2 = *(const u32x4*)(V + min(g0 + 2, last) * p.v_ss + vdc);
+      vr3 = *(const u32x4*)(V + min(g0 + 3, last) * p.v_ss + vdc);
+    }
+  };
+  auto store_kv = [&](int stage) __attribute__((always_inline)) {
+    uint16_t* ks = smem + stage * C::STAGE;
+    uint16_t* vt = ks + C::KS;
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
+      *(u32x4*)(ks + key * C::KP + dc) = kr[i];
+    }
+    if (v_lane) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = e >> 1;
+        const uint32_t a0 = vr0[j], a1 = vr1[j], a2 = vr2[j], a3 = vr3[j];
+        u32x2 w;
+        w[0] = (e & 1) ? hi_pair(a0, a1) : lo_pair(a0, a1);
+        w[1] = (e & 1) ? hi_pair(a2, a3) : lo_pair(a2, a3);
+        *(u32x2*)(vt + (vdc + e) * C::VP + 4 * vkg) = w;
+      }
+    }
+  };
+
   f32x16 o[DT];
 #pragma unroll
   for (int d = 0; d < DT; ++d) o[d] = f32x16{};
-  float m_run[16], l_run[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    m_run[r] = -INFINITY;
-    l_run[r] = 0.f;
-  }
+  float m_run = -INFINITY, l_run = 0.f;
 
   const int64_t kv_end = p.causal ? min(p.Sk, q0 + QT) : p.Sk;
-  for (int64_t kv0 = 0; kv0 < kv_end; kv0 += KT) {
-    // ---- stage K as [key][d] and V as [d][key] ----
+  const int n_tiles = (int)((kv_end + KT - 1) / KT);
+  load_kv(0);
+  store_kv(0);
+  __syncthreads();
+  for (int it = 0; it < n_tiles; ++it) {
+    const int64_t kv0 = (int64_t)it * KT;
+    const bool more = it + 1 < n_tiles;
+    if (more) load_kv(kv0 + KT);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t* ks = smem + (it & 1) * C::STAGE;
+    const uint16_t* vt = ks + C::KS;
+    if (!p.causal || kv0 <= wq0 + 31) {
+      // ---- S^T = K Q^T: two 32-key tiles x this wave's 32 queries ----
+      f32x16 s[2];
 #pragma unroll
-    for (int i = 0; i < KT * D / 8 / NT; ++i) {
-      const int v = threadIdx.x + i * NT;
-      const int key = v / (D / 8), dc = (v % (D / 8)) * 8;
-      const int64_t gk = min(kv0 + key, p.Sk - 1);
-      *(uint4*)(Ks + key * KP + dc) = *(const uint4*)(K + gk * p.k_ss + dc);
-      union {
-        uint4 u;
-        uint16_t h[8];
-      } vv;
-      vv.u = *(const uint4*)(V + gk * p.v_ss + dc);
+      for (int st = 0; st < 2; ++st) {
+        s[st] = f32x16{};
+        const uint16_t* kb = ks + (st * 32 + col) * C::KP + 8 * half;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(dc + e) * VP + key] = vv.h[e];
-    }
-    __syncthreads();
-
-    // ---- S = Q K^T for this wave's 32 rows x 64 keys ----
-    f32x16 s[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      s[nt] = f32x16{};
-      const uint16_t* kb = Ks + (nt * 32 + col) * KP + 8 * half;
-#pragma unroll
-      for (int t = 0; t < DF; ++t) s[nt] = AttnOp<T>::mma(qf[t], *(const vec*)(kb + 16 * t), s[nt]);
-    }
-
-    // ---- masking, online softmax (log2 domain) ----
-    const bool need_mask = (kv0 + KT > p.Sk) || (p.causal && kv0 + KT - 1 > wq0);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t row = wq0 + 8 * (r >> 2) + 4 * half + (r & 3);
-      float x0 = s[0][r] * p.scale_log2, x1 = s[1][r] * p.scale_log2;
-      if (need_mask) {
-        const int64_t k0 = kv0 + col, k1 = kv0 + 32 + col;
-        if (k0 >= p.Sk || (p.causal && k0 > row)) x0 = -INFINITY;
-        if (k1 >= p.Sk || (p.causal && k1 > row)) x1 = -INFINITY;
+        for (int t = 0; t < DF; ++t) s[st] = AttnOp<T>::mma(*(const vec*)(kb + 16 * t), qf[t], s[st]);
       }
-      float mx = fmaxf(x0, x1);
+      // ---- mask, online softmax in the log2 domain ----
+      // accumulator r of tile st holds key kv0 + 32 st + 8 (r / 4) + 4 half + r % 4
+      const bool need_mask = (kv0 + KT > p.Sk) || (p.causal && kv0 + KT - 1 > wq0);
+      float mx = -INFINITY;
 #pragma unroll
-      for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      const float m_new = fmaxf(m_run[r], mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // fully masked so far
-      const float p0 = __builtin_amdgcn_exp2f(x0 - m_use);
-      const float p1 = __builtin_amdgcn_exp2f(x1 - m_use);
-      float rs = p0 + p1;
+      for (int st = 0; st < 2; ++st) {
 #pragma unroll
-      for (int off = 16; off > 0; off >>= 1) rs += __shfl_xor(rs, off, 64);
-      const float corr = __builtin_amdgcn_exp2f(m_run[r] - m_use);
-      l_run[r] = l_run[r] * corr + rs;
-      m_run[r] = m_new;
+        for (int r = 0; r < 16; ++r) {
+          float x = s[st][r] * p.scale_log2;
+          if (need_mask) {
+            const int64_t key = kv0 + 32 * st + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (key >= p.Sk || (p.causal && key > qrow)) x = -INFINITY;
+          }
+          s[st][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // nothing visible yet
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+      m_run = m_new;
+      // P as the B operand of O^T += V^T P^T: k-step t (16 keys) takes
+      // accumulators 8 (t % 2) .. 8 (t % 2) + 7 of tile t / 2
+      vec pk[KT / 16];
+      float rs = 0.f;
 #pragma unroll
-      for (int d = 0; d < DT; ++d) o[d][r] *= corr;
-      const int rl = 8 * (r >> 2) + 4 * half + (r & 3);
-      Ps[wave][rl * PP + col] = AttnOp<T>::cvt(p0);
-      Ps[wave][rl * PP + 32 + col] = AttnOp<T>::cvt(p1);
-    }
-    __syncthreads();
-
-    // ---- O += P V ----
+      for (int t = 0; t < KT / 16; ++t) {
+        f32x8 pf;
 #pragma unroll
-    for (int t = 0; t < KT / 16; ++t) {
-      const vec pa = *(const vec*)(&Ps[wave][col * PP + 16 * t + 8 * half]);
+        for (int i = 0; i < 8; ++i) {
+          pf[i] = __builtin_amdgcn_exp2f(s[t >> 1][8 * (t & 1) + i] - m_use);
+          rs += pf[i];
+        }
+        pk[t] = __builtin_convertvector(pf, vec);
+      }
+      l_run = l_run * corr + rs;
+      if (__ballot(corr != 1.0f)) {
 #pragma unroll
-      for (int d = 0; d < DT; ++d) {
-        const vec vb = *(const vec*)(Vt + (d * 32 + col) * VP + 16 * t + 8 * half);
-        o[d] = AttnOp<T>::mma(pa, vb, o[d]);
+        for (int d = 0; d < DT; ++d) o[d] *= corr;
+      }
+      // ---- O^T += V^T P^T: the lane reads V^T[d][key] for the same keys:
+      // 16 t + 4 half + 0..3 and 16 t + 8 + 4 half + 0..3 ----
+#pragma unroll
+      for (int t = 0; t < KT / 16; ++t) {
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          const uint16_t* vb = vt + (d * 32 + col) * C::VP + 16 * t + 4 * half;
+          const u32x2 a0 = *(const u32x2*)vb, a1 = *(const u32x2*)(vb + 8);
+          const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
+          o[d] = AttnOp<T>::mma(__builtin_bit_cast(vec, a), pk[t], o[d]);
+        }
       }
     }
+    if (more) store_kv((it + 1) & 1);
     __syncthreads();
   }
 
-  // ---- normalise and store ----
-  uint16_t* O = p.o + b * p.o_sb + h * p.o_sh;
+  // ---- normalise and store: accumulator r of d tile dt is
+  // O[qrow][32 dt + 8 (r / 4) + 4 half + r % 4] ----
+  const float l = l_run + __shfl_xor(l_run, 32, 64);
+  if (qrow < p.Sq) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    uint16_t* O = p.o + b * p.o_sb + h * p.o_sh + qrow * p.o_ss;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t row = wq0 + 8 * (r >> 2) + 4 * half + (r & 3);
-    if (row >= p.Sq) continue;
-    const float inv = l_run[r] > 0.f ? 1.0f / l_run[r] : 0.f;
+    for (int d = 0; d < DT; ++d) {
 #pragma unroll
-    for (int d = 0; d < DT; ++d) O[row * p.o_ss + d * 32 + col] = AttnOp<T>::cvt(o[d][r] * inv);
-    if (col == 0 && p.lse) {
-      const float lse = l_run[r] > 0.f ? (m_run[r] + __builtin_amdgcn_logf(l_run[r])) * 0.6931471805599453f
-                                        : INFINITY;
-      p.lse[b * p.lse_sb + h * p.lse_sh + row] = lse;
+      for (int g = 0; g < 4; ++g) {
+        typedef typename AttnOp<T>::elem E;
+        typedef E e4 __attribute__((ext_vector_type(4)));
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        f4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = o[d][4 * g + i] * inv;
+        *(e4*)(O + d * 32 + 8 * g + 4 * half) = __builtin_convertvector(v, e4);
+      }
     }
+    if (half == 0 && p.lse)
+      p.lse[b * p.lse_sb + h * p.lse_sh + qrow] =
+          l > 0.f ? (m_run + __builtin_amdgcn_logf(l)) * 0.6931471805599453f : INFINITY;
   }
+}
+
+template <typename T, int D>
+mi_status_t launch_flash(const AttnArgs& a, hipStream_t s) {
+  static bool attr = [] {
+    (void)hipFuncSetAttribute((const void*)flash_fwd_kernel<T, D>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)FlashCfg<D>::lds());
+    return true;
+  }();
+  (void)attr;
+  hipLaunchKernelGGL((flash_fwd_kernel<T, D>), dim3((unsigned)a.n_blocks), dim3(NT),
+                     FlashCfg<D>::lds(), s, a);
+  return check_launch("flash_attention_fwd");
 }
 
 mi_status_t check4(const mi_tensor_t* t, const char* name) {
@@ -278,15 +376,12 @@ extern "C" mi_status_t mi_flash_attention_fwd(const mi_tensor_t* out, const mi_t
   a.scale_log2 = (float)(scale * 1.4426950408889634);
   a.causal = is_causal ? 1 : 0;
   a.q_tiles = (int)((Sq + QT - 1) / QT);
-  MI_CHECK_ARG(H <= 65535 && B <= 65535, "attention: too many heads or batches");
-  dim3 grid((unsigned)a.q_tiles, (unsigned)H, (unsigned)B);
+  const int64_t nb = (int64_t)a.q_tiles * H * B;
+  MI_CHECK_ARG(nb <= 0x7fffffff, "attention: too many query tiles");
+  a.n_blocks = (int)nb;
+  a.xcd_remap = (nb % 8 == 0) ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
-  if (q->dtype == MI_BF16) {
-    if (D == 128) hipLaunchKernelGGL((flash_fwd_kernel<BF16, 128>), grid, dim3(NT), 0, s, a);
-    else hipLaunchKernelGGL((flash_fwd_kernel<BF16, 64>), grid, dim3(NT), 0, s, a);
-  } else {
-    if (D == 128) hipLaunchKernelGGL((flash_fwd_kernel<F16, 128>), grid, dim3(NT), 0, s, a);
-    else hipLaunchKernelGGL((flash_fwd_kernel<F16, 64>), grid, dim3(NT), 0, s, a);
-  }
-  return check_launch("flash_attention_fwd");
+  if (q->dtype == MI_BF16)
+    return D == 128 ? launch_flash<BF16, 128>(a, s) : launch_flash<BF16, 64>(a, s);
+  return D == 128 ? launch_flash<F16, 128>(a, s) : launch_flash<F16, 64>(a, s);
 }
