@@ -325,6 +325,35 @@ def test_reduce_long_rows_and_noncontiguous():
     assert_exact(out, ref, "transposed amax")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64, torch.int64,
+                                   torch.int32, torch.uint8])
+@pytest.mark.parametrize("shape,dims", [((3000, 257), (0,)), ((2, 1500, 1024), (1,)),
+                                        ((1024, 4099), (0,)), ((700, 8, 3), (0,))])
+def test_column_reduce_split_pass(dtype, shape, dims):
+    """Column reductions long enough to be split over blocks and finished by
+    the second pass over partials, with aligned (vector) and odd widths."""
+    x = rand(shape, dtype, 29)
+    ref = aten.sum_(x, list(dims))
+    out = empty_like_ref(ref)
+    _abi.sum_(out, dev(x), dims)
+    if dtype.is_floating_point:
+        assert_close(out, ref, "bf16" if dtype == torch.bfloat16 else "fp32", "split sum")
+    else:
+        assert_exact(out, ref, "split sum")
+    if dtype.is_floating_point:
+        x.view(-1)[777] = float("nan")
+    ref = aten.amax(x, list(dims))
+    out = empty_like_ref(ref)
+    _abi.amax(out, dev(x), dims)
+    assert_exact(out, ref, "split amax")
+    if dtype.is_floating_point:
+        x = rand(shape, dtype, 30)
+        ref = aten.mean(x, list(dims))
+        out = empty_like_ref(ref)
+        _abi.mean(out, dev(x), dims)
+        assert_close(out, ref, "bf16" if dtype == torch.bfloat16 else "fp32", "split mean")
+
+
 def test_amax_nan_and_empty_sum():
     x = torch.randn(4, 100)
     x[2, 17] = float("nan")
@@ -361,6 +390,45 @@ def test_softmax_parity(log, case):
     assert_close(out, ref, kind, f"softmax {case}")
 
 
+# row widths that select each register-resident block shape (256 x 1 ..
+# 1024 x 16 vectors) and the two-read fallback just past it
+@pytest.mark.parametrize("width,dtype", [(2048, torch.bfloat16), (4096, torch.bfloat16),
+                                         (8192, torch.bfloat16), (16384, torch.bfloat16),
+                                         (65536, torch.bfloat16), (131072, torch.bfloat16),
+                                         (131080, torch.bfloat16), (60000, torch.float32),
+                                         (65540, torch.float32)])
+def test_softmax_row_shapes(width, dtype):
+    x = rand((9, width), dtype, 27) * 3
+    for log in (True, False):
+        ref = (aten.log_softmax if log else aten.softmax)(x, -1)
+        out = empty_like_ref(ref)
+        (_abi.log_softmax if log else _abi.softmax)(out, dev(x), -1)
+        kind = "bf16" if dtype == torch.bfloat16 else "fp32"
+        assert_close(out, ref, kind, f"softmax log={log} width={width}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_softmax_nan_inf_rows(dtype):
+    """A NaN anywhere in a row makes the whole row NaN (ATen's max propagates
+    it); +inf makes the row NaN; an all -inf row is NaN; -inf elements give
+    probability 0 (log -inf)."""
+    x = rand((6, 32000), dtype, 28) * 4
+    x[0, 17] = float("nan")
+    x[1, 31999] = float("inf")
+    x[2, :] = float("-inf")
+    x[3, ::3] = float("-inf")
+    x[4, 0] = float("nan")
+    x[4, 1] = float("inf")
+    for log in (True, False):
+        ref = (aten.log_softmax if log else aten.softmax)(x, -1)
+        out = empty_like_ref(ref)
+        (_abi.log_softmax if log else _abi.softmax)(out, dev(x), -1)
+        o = out.cpu()
+        assert torch.equal(torch.isnan(o), torch.isnan(ref)), f"NaN pattern log={log}"
+        assert_close(out, ref, "bf16" if dtype == torch.bfloat16 else "fp32",
+                     f"softmax special log={log}")
+
+
 # ---- fused efficient ops ----------------------------------------------------------
 
 def test_config3_rms_norm_rope_silu_mul_reduced_tokens():
@@ -393,6 +461,30 @@ def test_config3_full_size():
     out = torch.empty(c["gate"].shape, dtype=torch.bfloat16, device=DEV)
     _abi.silu_mul(out, dev(c["gate"]), dev(c["up"]))
     assert_close(out, aten.silu_mul(c["gate"], c["up"]), "bf16", "silu_mul full")
+
+
+@pytest.mark.parametrize("tokens,hq,hk,d,dtype,with_k", [
+    (37, 32, 32, 128, torch.bfloat16, True),    # ragged last block of 16 tokens
+    (16, 5, 3, 64, torch.float16, True),
+    (23, 4, 0, 32, torch.float32, False),        # q only
+    (3, 2, 1, 4096, torch.bfloat16, True),       # one token per block (LDS-bound)
+    (129, 1, 1, 16, torch.float32, True),
+])
+def test_rope_shapes(tokens, hq, hk, d, dtype, with_k):
+    q = rand((tokens, hq, d), dtype, 34)
+    pos = torch.randint(0, 8192, (tokens,), generator=g(35))
+    qo = torch.empty_like(dev(q))
+    if with_k:
+        k = rand((tokens, hk, d), dtype, 36)
+        ko = torch.empty_like(dev(k))
+        _abi.rope(qo, ko, dev(q), dev(k), dev(pos), 10000.0)
+        # the bf16 bar for every dtype: at positions near 8192 one ulp of the
+        # fp32 angle (from powf / sincosf differing by an ulp between the
+        # device and CPU libm) moves cos/sin by ~5e-4
+        assert_close(ko, aten.rope(k, pos, 10000.0), "bf16", "rope k")
+    else:
+        _abi.rope(qo, None, dev(q), None, dev(pos), 10000.0)
+    assert_close(qo, aten.rope(q, pos, 10000.0), "bf16", "rope q")
 
 
 def test_fused_edge_cases():

@@ -98,9 +98,10 @@ __global__ __launch_bounds__(kBlock) void binary_2d_kernel(
       }
       rowv[u] = r;
       colv[u] = c;
-      if (a.mode == M_FULL) va[u].u = ((const uint4*)a.p)[v];
+      // full operands are streamed (read once); a broadcast row stays cached
+      if (a.mode == M_FULL) va[u].u = ld_stream((const uint4*)a.p + v);
       else if (a.mode == M_ROW) va[u].u = ((const uint4*)a.p)[c];
-      if (b.mode == M_FULL) vb[u].u = ((const uint4*)b.p)[v];
+      if (b.mode == M_FULL) vb[u].u = ld_stream((const uint4*)b.p + v);
       else if (b.mode == M_ROW) vb[u].u = ((const uint4*)b.p)[c];
     }
   }
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(kBlock) void binary_2d_kernel(
         const Acc y = (b.mode == M_FULL || b.mode == M_ROW) ? TypeOf<Tag>::load(vb[u].s[e]) : cb;
         o.s[e] = TypeOf<Tag>::store(apply<OP, Acc>(x, y, alpha));
       }
-      ((uint4*)out)[v] = o.u;
+      st_stream((uint4*)out + v, o.u);
     }
   }
 }

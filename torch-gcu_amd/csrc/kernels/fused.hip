@@ -4,14 +4,15 @@
 //   rms_norm  reads x once and writes y once: one wave per row holds the row
 //             in registers (4096 bf16 = 8 x 16-byte vectors per lane), so the
 //             sum of squares and the scaling share a single HBM read;
-//   rope      one lane per (token, 8-pair slice) computes its 8 cos/sin pairs
-//             once and applies them to every head of q and of k, so the
-//             transcendental cost is divided by 2 x 32 heads;
+//   rope      a block computes the cos/sin tables of its 16 tokens once into
+//             LDS (one sincosf per token and pair, shared by all 2 x 32
+//             heads), then streams the tokens' q and k rows contiguously;
 //   silu_mul  streams gate and up with four 16-byte vectors per operand in
 //             flight per lane; silu uses the hardware exp2 and reciprocal.
 // Arithmetic is fp32 with one rounding to the output type, which is what
 // torch.rms_norm's CPU kernel does for bf16 (upcast, x * rsqrt(mean(x^2) +
 // eps) * w, one cast) and what the fp32 closed forms of RoPE and SiLU-mul do.
+#include <algorithm>
 #include <cmath>
 
 #include "iter.h"
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(256) void rms_norm_wave_kernel(
   for (int k = 0; k < VPL; ++k) {
     const int64_t i = lane + (int64_t)k * 64;
     if (i < nv) {
-      v[k] = px[i];
+      v[k] = ld_stream(px + i);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float f = FT<Tag>::load(v[k].s[e]);
@@ -87,7 +88,7 @@ __global__ __launch_bounds__(256) void rms_norm_wave_kernel(
         if (HAS_W) y = y * FT<Tag>::load(wv.s[e]);
         o.s[e] = FT<Tag>::store(y);
       }
-      po[i] = o;
+      st_stream(po + i, o);
     }
   }
 }
@@ -193,51 +194,79 @@ struct RopeTensor {
   int64_t out_tok_stride, out_head_stride;
 };
 
-// Lane (token t, slice j) owns pairs i in [j*P, (j+1)*P), P = 16 B / esize.
+// A block owns `tpb` consecutive tokens.  Its lanes first compute the
+// tokens' fp32 cos/sin tables (tpb x half each) into LDS, one sincosf per
+// (token, pair) as the fp32 closed form does, then stream the tokens' q and
+// k rows: a job is one (token, head, slice of P pairs) and reads the two
+// 16-byte halves x1 = x[j*P ..], x2 = x[half + j*P ..].  Jobs run head-major
+// within a token, so a wave's loads cover 8 heads x 256 B of one token row
+// contiguously, and each lane keeps eight jobs' loads in flight.
+constexpr int kRopeUnroll = 8;
+
 template <typename Tag, typename PosT>
 __global__ __launch_bounds__(256) void rope_kernel(RopeTensor q, RopeTensor k, const PosT* pos,
-                                                   int64_t pos_stride, int64_t tokens,
-                                                   int64_t half, float theta_f,
-                                                   float dim_f) {
+                                                   int64_t pos_stride, int64_t tokens, int half,
+                                                   int tpb, float theta_f, float dim_f) {
   typedef typename FT<Tag>::storage St;
   constexpr int P = 16 / sizeof(St);
   union V {
     uint4 u;
     St s[P];
   };
-  const int64_t slices = half / P;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= tokens * slices) return;
-  const int64_t t = gid / slices;
-  const int64_t j = gid - t * slices;
-  const float p = (float)pos[t * pos_stride];
-  float c[P], s[P];
-#pragma unroll
-  for (int e = 0; e < P; ++e) {
-    const int64_t i = j * P + e;
+  extern __shared__ float rope_cs[];
+  const int64_t t0 = (int64_t)blockIdx.x * tpb;
+  const int nt = (int)min((int64_t)tpb, tokens - t0);
+  float* cs_c = rope_cs;
+  float* cs_s = rope_cs + tpb * half;
+  for (int idx = threadIdx.x; idx < nt * half; idx += 256) {
+    const int tt = idx / half, i = idx - tt * half;
+    const float p = (float)pos[(t0 + tt) * pos_stride];
     // inv_freq = 1 / theta^(2i/d), as in the fp32 closed form
-    const float expo = (float)(2 * i) / dim_f;
-    const float inv_freq = 1.0f / powf(theta_f, expo);
-    sincosf(p * inv_freq, &s[e], &c[e]);
+    const float inv_freq = 1.0f / powf(theta_f, (float)(2 * i) / dim_f);
+    sincosf(p * inv_freq, &cs_s[idx], &cs_c[idx]);
   }
-#pragma unroll 1
-  for (int w = 0; w < 2; ++w) {
-    const RopeTensor& r = w == 0 ? q : k;
-    if (r.in == nullptr) continue;
-    const St* in_t = (const St*)r.in + t * r.in_tok_stride + j * P;
-    St* out_t = (St*)r.out + t * r.out_tok_stride + j * P;
-    for (int64_t h = 0; h < r.heads; ++h) {
-      const V a = *(const V*)(in_t + h * r.in_head_stride);
-      const V b = *(const V*)(in_t + h * r.in_head_stride + half);
-      V oa, ob;
+  __syncthreads();
+  const int slices = half / P;
+  const int jq = q.in ? (int)q.heads * slices : 0;
+  const int jpt = jq + (k.in ? (int)k.heads * slices : 0);
+  const int total = nt * jpt;
+  for (int b0 = threadIdx.x; b0 < total; b0 += 256 * kRopeUnroll) {
+    V xa[kRopeUnroll], xb[kRopeUnroll];
+    St* op[kRopeUnroll];
+    int ci[kRopeUnroll];
 #pragma unroll
-      for (int e = 0; e < P; ++e) {
-        const float x1 = FT<Tag>::load(a.s[e]), x2 = FT<Tag>::load(b.s[e]);
-        oa.s[e] = FT<Tag>::store(x1 * c[e] - x2 * s[e]);
-        ob.s[e] = FT<Tag>::store(x2 * c[e] + x1 * s[e]);
+    for (int u = 0; u < kRopeUnroll; ++u) {
+      const int job = b0 + u * 256;
+      op[u] = nullptr;
+      if (job < total) {
+        const int tt = job / jpt;
+        int r = job - tt * jpt;
+        const bool isk = r >= jq;
+        if (isk) r -= jq;
+        const RopeTensor& rt = isk ? k : q;
+        const int h = r / slices, j = r - h * slices;
+        const int64_t t = t0 + tt;
+        const St* in = (const St*)rt.in + t * rt.in_tok_stride + h * rt.in_head_stride + j * P;
+        op[u] = (St*)rt.out + t * rt.out_tok_stride + h * rt.out_head_stride + j * P;
+        ci[u] = tt * half + j * P;
+        xa[u] = ld_stream((const V*)in);
+        xb[u] = ld_stream((const V*)(in + half));
       }
-      *(V*)(out_t + h * r.out_head_stride) = oa;
-      *(V*)(out_t + h * r.out_head_stride + half) = ob;
+    }
+#pragma unroll
+    for (int u = 0; u < kRopeUnroll; ++u) {
+      if (op[u] != nullptr) {
+        V oa, ob;
+#pragma unroll
+        for (int e = 0; e < P; ++e) {
+          const float c = cs_c[ci[u] + e], sn = cs_s[ci[u] + e];
+          const float x1 = FT<Tag>::load(xa[u].s[e]), x2 = FT<Tag>::load(xb[u].s[e]);
+          oa.s[e] = FT<Tag>::store(x1 * c - x2 * sn);
+          ob.s[e] = FT<Tag>::store(x2 * c + x1 * sn);
+        }
+        st_stream((V*)op[u], oa);
+        st_stream((V*)(op[u] + half), ob);
+      }
     }
   }
 }
@@ -290,8 +319,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(typename FT<Tag>::storage
   for (int k = 0; k < U; ++k) {
     const int64_t i = base + k * 256;
     if (i < nvec) {
-      vg[k] = ((const V*)g)[i];
-      vu[k] = ((const V*)u)[i];
+      vg[k] = ld_stream((const V*)g + i);
+      vu[k] = ld_stream((const V*)u + i);
     }
   }
 #pragma unroll
@@ -305,7 +334,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(typename FT<Tag>::storage
         const float sig = __builtin_amdgcn_rcpf(1.0f + fast_exp(-x));
         o.s[e] = FT<Tag>::store(x * sig * FT<Tag>::load(vu[k].s[e]));
       }
-      ((V*)out)[i] = o;
+      st_stream((V*)out + i, o);
     }
   }
   // tail elements
@@ -418,18 +447,25 @@ mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out, const mi
     MI_CHECK_ARG(k->dtype == q->dtype, "rope: q and k dtypes differ");
   if (tokens == 0) return MI_OK;
   const int64_t half = D / 2;
-  const int64_t work = tokens * (half / P);
-  const unsigned grid = ceil_div_u(work, 256);
+  MI_CHECK_ARG(half <= 8192, "rope: head_dim %lld too large", (long long)D);
+  MI_CHECK_ARG((rq.heads + rk.heads) * (half / P) * 16 < (int64_t)1 << 31,
+               "rope: too many heads");
+  // tokens per block: 16, fewer when the cos/sin tables would pass 64 KiB of LDS
+  const int tpb = (int)std::max<int64_t>(1, std::min<int64_t>(16, 8192 / half));
+  const size_t lds = (size_t)2 * tpb * half * sizeof(float);
+  const unsigned grid = ceil_div_u(tokens, tpb);
   const float l2t = (float)theta;
   const float inv_dim = (float)D;
   const int64_t ps = positions->strides[0];
 #define MI_ROPE_LAUNCH(TAG)                                                                   \
   if (positions->dtype == MI_I64)                                                           \
-    hipLaunchKernelGGL((rope_kernel<TAG, int64_t>), dim3(grid), dim3(256), 0, stream, rq, rk, \
-                       (const int64_t*)positions->data, ps, tokens, half, l2t, inv_dim);     \
+    hipLaunchKernelGGL((rope_kernel<TAG, int64_t>), dim3(grid), dim3(256), lds, stream, rq,  \
+                       rk, (const int64_t*)positions->data, ps, tokens, (int)half, tpb, l2t, \
+                       inv_dim);                                                            \
   else                                                                                      \
-    hipLaunchKernelGGL((rope_kernel<TAG, int32_t>), dim3(grid), dim3(256), 0, stream, rq, rk, \
-                       (const int32_t*)positions->data, ps, tokens, half, l2t, inv_dim);
+    hipLaunchKernelGGL((rope_kernel<TAG, int32_t>), dim3(grid), dim3(256), lds, stream, rq,  \
+                       rk, (const int32_t*)positions->data, ps, tokens, (int)half, tpb, l2t, \
+                       inv_dim);
   switch (q->dtype) {
     case MI_BF16: MI_ROPE_LAUNCH(BF16) break;
     case MI_F16: MI_ROPE_LAUNCH(F16) break;

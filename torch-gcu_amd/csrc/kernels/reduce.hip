@@ -4,15 +4,15 @@
 // which must form one dense block; otherwise a permuted dense copy is made
 // in workspace first):
 //   - inner == 1 ("row" reduction, e.g. config 2's bf16 [8192, 32000] over
-//     the last dim): one 256-lane block per row, 16-byte vector loads, four
-//     in flight per lane, wave64 shuffle reduction then an LDS combine of the
-//     four waves.  Long rows with few of them are split over several blocks
-//     and finished by a second pass over the partials.
+//     the last dim): one 512-lane block per row, 16-byte non-temporal loads,
+//     eight in flight per lane, wave64 shuffle reduction then a combine of
+//     the eight wave results.  Long rows with few of them are split over
+//     several blocks and finished by a second pass over the partials.
 //   - inner > 1 ("column" reduction, e.g. fp32 [16384, 4096] over dim 0):
-//     lanes own 16-byte column vectors so each wave reads 1 KiB contiguous
-//     per row; the rows are split into chunks over blocks (partials in
-//     workspace, then a second pass), which keeps more than 1000 blocks in
-//     flight for a 4096-wide output.
+//     lanes own 16-byte column vectors side by side, so a 256-lane block
+//     reads 4 KiB contiguous per row; the rows are split into chunks over
+//     blocks (partials in workspace, then a second pass), about 4 blocks per
+//     CU for a 4096-wide output.
 // Floating inputs accumulate in float (double for f64), integers in int64.
 #include <algorithm>
 #include <cmath>
@@ -104,10 +104,14 @@ __device__ __forceinline__ void red_store(const RedOut& o, int op, int64_t idx, 
   store_as<A>(o.data, idx, o.dtype, v);
 }
 
-constexpr int kRowBlock = 256;
+constexpr int kRowBlock = 512;
+constexpr int kRowUnroll = 8;
 
 // rows x [R] -> rows x splits partials (or final when splits == 1).
-// Block (row, split) reduces elements [split*chunk, min(R, (split+1)*chunk)).
+// Block (row, split) reduces elements [split*chunk, min(R, (split+1)*chunk)):
+// 512 lanes, eight 16-byte non-temporal loads in flight per lane (a config-2
+// row of 64,000 B is one batch), a wave64 shuffle reduction, then the
+// per-wave results in a fixed order.
 template <typename Tag>
 __global__ __launch_bounds__(kRowBlock) void row_reduce_kernel(
     const typename RT<Tag>::storage* __restrict__ in, int64_t R, int64_t row_stride,
@@ -115,7 +119,7 @@ __global__ __launch_bounds__(kRowBlock) void row_reduce_kernel(
   typedef typename RT<Tag>::storage St;
   typedef typename RT<Tag>::acc A;
   constexpr int VEC = 16 / sizeof(St) > 0 ? 16 / sizeof(St) : 1;
-  __shared__ A red[16];
+  __shared__ A red[kRowBlock / 64];
   const int64_t row = blockIdx.x;
   const int64_t split = blockIdx.y;
   const int64_t beg = split * chunk;
@@ -131,21 +135,22 @@ __global__ __launch_bounds__(kRowBlock) void row_reduce_kernel(
     };
     const int64_t nv = (end - beg) / VEC;
     const V* pv = (const V*)(p + beg);
-    int64_t v = threadIdx.x;
-    for (; v + 3 * kRowBlock < nv; v += 4 * kRowBlock) {
-      V x0 = pv[v], x1 = pv[v + kRowBlock], x2 = pv[v + 2 * kRowBlock], x3 = pv[v + 3 * kRowBlock];
+    for (int64_t v0 = threadIdx.x; v0 < nv; v0 += (int64_t)kRowBlock * kRowUnroll) {
+      V x[kRowUnroll];
+      bool ok[kRowUnroll];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        acc = red_combine(op, acc, RT<Tag>::load(x0.s[e]));
-        acc = red_combine(op, acc, RT<Tag>::load(x1.s[e]));
-        acc = red_combine(op, acc, RT<Tag>::load(x2.s[e]));
-        acc = red_combine(op, acc, RT<Tag>::load(x3.s[e]));
+      for (int u = 0; u < kRowUnroll; ++u) {
+        const int64_t v = v0 + (int64_t)u * kRowBlock;
+        ok[u] = v < nv;
+        if (ok[u]) x[u] = ld_stream(pv + v);
       }
-    }
-    for (; v < nv; v += kRowBlock) {
-      V x0 = pv[v];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc = red_combine(op, acc, RT<Tag>::load(x0.s[e]));
+      for (int u = 0; u < kRowUnroll; ++u) {
+        if (ok[u]) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc = red_combine(op, acc, RT<Tag>::load(x[u].s[e]));
+        }
+      }
     }
     i = beg + nv * VEC;
   }
@@ -179,59 +184,90 @@ __global__ __launch_bounds__(256) void row_reduce_wave_kernel(
   if (lane == 0) red_store(out, op, row, acc);
 }
 
-// [outer, R, inner] column reduction over R; block (64 x 4) lanes own one
-// column (VEC columns when vectorised) and a quarter of the chunk's rows.
+constexpr int kColBlock = 256;
+constexpr int kColUnroll = 8;
+
+// [outer, R, inner] column reduction over R, first pass: 256 lanes side by
+// side along a row (a lane owns VEC adjacent columns, so a block reads
+// 256 * VEC contiguous elements of each row), each walking the rows of its
+// split with eight loads in flight.  Output layout [outer, splits, inner]
+// (Acc partials, or the final value when there is one split).
 template <typename Tag, int VEC>
-__global__ __launch_bounds__(256) void col_reduce_kernel(
+__global__ __launch_bounds__(kColBlock) void col_reduce_kernel(
     const typename RT<Tag>::storage* __restrict__ in, int64_t R, int64_t inner,
     int64_t chunk, int op, RedOut out) {
   typedef typename RT<Tag>::storage St;
   typedef typename RT<Tag>::acc A;
-  __shared__ A part[4][64 * VEC];
   const int64_t ncv = inner / VEC;  // column vectors
-  const int64_t ncb = (ncv + 63) / 64;
+  const int64_t ncb = (ncv + kColBlock - 1) / kColBlock;
   const int64_t o = blockIdx.x / ncb;
-  const int64_t cv = (blockIdx.x - o * ncb) * 64 + threadIdx.x;
+  const int64_t cv = (blockIdx.x - o * ncb) * kColBlock + threadIdx.x;
+  if (cv >= ncv) return;
   const int64_t split = blockIdx.y;
   const int64_t beg = split * chunk;
   const int64_t end = beg + chunk < R ? beg + chunk : R;
   A acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = red_ident<A>(op);
-  if (cv < ncv) {
-    const St* base = in + (o * R) * inner + cv * VEC;
-    union V {
-      St s[VEC];
-    };
-    int64_t r = beg + threadIdx.y;
-    for (; r + 12 < end; r += 16) {
-      V x0 = *(const V*)(base + r * inner), x1 = *(const V*)(base + (r + 4) * inner);
-      V x2 = *(const V*)(base + (r + 8) * inner), x3 = *(const V*)(base + (r + 12) * inner);
+  union alignas(VEC * sizeof(St)) V {  // the host checked this alignment
+    St s[VEC];
+  };
+  const V* base = (const V*)(in + (o * R) * inner) + cv;
+  int64_t r = beg;
+  for (; r + kColUnroll <= end; r += kColUnroll) {
+    V x[kColUnroll];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        acc[e] = red_combine(op, acc[e], RT<Tag>::load(x0.s[e]));
-        acc[e] = red_combine(op, acc[e], RT<Tag>::load(x1.s[e]));
-        acc[e] = red_combine(op, acc[e], RT<Tag>::load(x2.s[e]));
-        acc[e] = red_combine(op, acc[e], RT<Tag>::load(x3.s[e]));
-      }
+    for (int u = 0; u < kColUnroll; ++u) {
+      if constexpr (sizeof(V) == 16) x[u] = ld_stream(base + (r + u) * ncv);
+      else x[u] = base[(r + u) * ncv];
     }
-    for (; r < end; r += 4) {
-      V x0 = *(const V*)(base + r * inner);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = red_combine(op, acc[e], RT<Tag>::load(x0.s[e]));
-    }
+    for (int u = 0; u < kColUnroll; ++u)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = red_combine(op, acc[e], RT<Tag>::load(x[u].s[e]));
+  }
+  for (; r < end; ++r) {
+    const V x = base[r * ncv];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = red_combine(op, acc[e], RT<Tag>::load(x.s[e]));
   }
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) part[threadIdx.y][threadIdx.x * VEC + e] = acc[e];
-  __syncthreads();
-  if (threadIdx.y == 0 && cv < ncv) {
+  for (int e = 0; e < VEC; ++e)
+    red_store(out, op, (o * gridDim.y + split) * inner + cv * VEC + e, acc[e]);
+}
+
+// Second pass over Acc partials [outer, S, inner]: a block is 16 columns x
+// 16 lanes down the S partials; the 16 lane results are combined in a fixed
+// order through LDS, so the result does not depend on scheduling.
+template <typename A>
+__global__ __launch_bounds__(256) void col_finish_kernel(const A* __restrict__ part, int64_t outer,
+                                                         int64_t S, int64_t inner, int op,
+                                                         RedOut out) {
+  __shared__ A red[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t c = (int64_t)blockIdx.x * 16 + tx;  // flattened (outer, inner) column
+  const bool live = c < outer * inner;
+  A acc = red_ident<A>(op);
+  if (live) {
+    const int64_t o = c / inner, i = c - o * inner;
+    const A* p = part + o * S * inner + i;
+    int64_t s = ty;
+    for (; s + 112 < S; s += 128) {
+      A x[8];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      A v = part[0][threadIdx.x * VEC + e];
-      for (int y = 1; y < 4; ++y) v = red_combine(op, v, part[y][threadIdx.x * VEC + e]);
-      // output layout [outer, splits, inner]
-      red_store(out, op, (o * gridDim.y + split) * inner + cv * VEC + e, v);
+      for (int u = 0; u < 8; ++u) x[u] = p[(s + 16 * u) * inner];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = red_combine(op, acc, x[u]);
     }
+    for (; s < S; s += 16) acc = red_combine(op, acc, p[s * inner]);
+  }
+  red[ty][tx] = acc;
+  __syncthreads();
+  if (ty == 0 && live) {
+    A r = red[0][tx];
+#pragma unroll
+    for (int y = 1; y < 16; ++y) r = red_combine(op, r, red[y][tx]);
+    red_store(out, op, c, r);
   }
 }
 
@@ -292,52 +328,53 @@ mi_status_t launch_row(const void* in, int64_t outer, int64_t R, int op, RedOut 
 }
 
 template <typename Tag, int VEC>
-mi_status_t launch_col_v(const void* in, int64_t outer, int64_t R, int64_t inner, int64_t splits,
-                         int op, RedOut o, hipStream_t stream) {
+mi_status_t launch_col_v(const void* in, int64_t outer, int64_t R, int64_t inner, int64_t chunk,
+                         int64_t splits, int op, RedOut o, hipStream_t stream) {
   const int64_t ncv = inner / VEC;
-  const int64_t chunk = (R + splits - 1) / splits;
-  const int64_t s = (R + chunk - 1) / chunk;
-  dim3 grid((unsigned)(ceil_div_u(ncv, 64) * outer), (unsigned)s, 1);
-  hipLaunchKernelGGL((col_reduce_kernel<Tag, VEC>), grid, dim3(64, 4), 0, stream,
+  dim3 grid((unsigned)(ceil_div_u(ncv, kColBlock) * outer), (unsigned)splits, 1);
+  hipLaunchKernelGGL((col_reduce_kernel<Tag, VEC>), grid, dim3(kColBlock), 0, stream,
                      (const typename RT<Tag>::storage*)in, R, inner, chunk, op, o);
   return check_launch("col_reduce");
 }
 
 template <typename Tag>
-mi_status_t launch_col_any(const void* in, int64_t outer, int64_t R, int64_t inner,
+mi_status_t launch_col_any(const void* in, int64_t outer, int64_t R, int64_t inner, int64_t chunk,
                            int64_t splits, int op, RedOut o, hipStream_t stream) {
   typedef typename RT<Tag>::storage St;
   constexpr int V = 16 / sizeof(St) >= 4 ? 4 : 16 / sizeof(St);
   if (inner % V == 0 && ((uintptr_t)in % (V * sizeof(St))) == 0)
-    return launch_col_v<Tag, V>(in, outer, R, inner, splits, op, o, stream);
-  return launch_col_v<Tag, 1>(in, outer, R, inner, splits, op, o, stream);
+    return launch_col_v<Tag, V>(in, outer, R, inner, chunk, splits, op, o, stream);
+  return launch_col_v<Tag, 1>(in, outer, R, inner, chunk, splits, op, o, stream);
 }
 
+// Splits R so that about 4 blocks per CU are in flight (config 2's fp32
+// [16384, 4096] mean(0): 4 column blocks x 256 splits of 64 rows), then
+// combines the partials in a second pass.
 template <typename Tag>
 mi_status_t launch_col(const void* in, int64_t outer, int64_t R, int64_t inner, int op,
                        RedOut final_out, hipStream_t stream) {
   typedef typename RT<Tag>::acc A;
+  typedef typename RT<Tag>::storage St;
+  constexpr int V = 16 / sizeof(St) >= 4 ? 4 : 16 / sizeof(St);
   const int64_t cus = cu_count();
-  const int64_t col_blocks = outer * ((inner + 255) / 256);
+  const int64_t col_blocks = outer * ((inner / V + kColBlock - 1) / kColBlock);
   int64_t splits = 1;
-  if (col_blocks < 4 * cus && R >= 64) {
+  if (col_blocks < 4 * cus && R >= 2 * kColUnroll) {
     splits = (4 * cus + col_blocks - 1) / col_blocks;
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, R / 32));
   }
-  if (splits > 65535) splits = 65535;
-  if (splits == 1) return launch_col_any<Tag>(in, outer, R, inner, 1, op, final_out, stream);
+  splits = std::min<int64_t>(splits, 1024);
   const int64_t chunk = (R + splits - 1) / splits;
   splits = (R + chunk - 1) / chunk;
+  if (splits == 1) return launch_col_any<Tag>(in, outer, R, inner, chunk, 1, op, final_out, stream);
   Workspace ws;
   MI_RETURN_IF(ws.alloc((size_t)(outer * splits * inner) * sizeof(A), stream));
   RedOut part{ws.get(), -1, 1.0};
   const int pop = op == R_MEAN ? R_SUM : op;
-  MI_RETURN_IF(launch_col_any<Tag>(in, outer, R, inner, splits, pop, part, stream));
-  typedef typename std::conditional<
-      std::is_same<A, float>::value, float,
-      typename std::conditional<std::is_same<A, double>::value, double, int64_t>::type>::type
-      ATag;
-  return launch_col_any<ATag>(ws.get(), outer, splits, inner, 1, op, final_out, stream);
+  MI_RETURN_IF(launch_col_any<Tag>(in, outer, R, inner, chunk, splits, pop, part, stream));
+  hipLaunchKernelGGL((col_finish_kernel<A>), dim3(ceil_div_u(outer * inner, 16)), dim3(256), 0,
+                     stream, (const A*)ws.get(), outer, splits, inner, op, final_out);
+  return check_launch("col_reduce finish");
 }
 
 template <typename Tag>

@@ -1,8 +1,8 @@
 // softmax / log_softmax along one dim, computed in float.
 //
 // Rows along a dense last dim (config 2: bf16 [8192, 32000], 64,000 B per
-// row) are read from HBM once: a 256-lane block holds its row in registers
-// (up to 32 x 16-byte vectors per lane), takes the row max and the sum of
+// row) are read from HBM once: a block of up to 1024 lanes holds its row in
+// registers (up to 16 x 16-byte vectors per lane), takes the row max and the sum of
 // exp(x - max) with wave64 shuffles plus an LDS combine, then writes
 //   log_softmax: x - max - log(sum)      softmax: exp(x - max) * (1 / sum)
 // which is the same sequence of float operations ATen's CPU kernel uses
@@ -67,16 +67,44 @@ __device__ __forceinline__ float block_sum_f(float v, float* red) {
   return r;
 }
 
-// Register-resident row: VPT 16-byte vectors per lane.
-template <typename InTag, typename OutTag, int VPT, bool LOG>
-__global__ __launch_bounds__(kBlock) void softmax_reg_kernel(
+// Register-resident row: NTH lanes, VPT 16-byte vectors per lane.  The row
+// max uses fmaxf, which skips NaN: a NaN element still makes exp(x - max)
+// and therefore the row sum NaN, so every output of that row is NaN, as in
+// ATen (whose max propagates the NaN).  Loads and stores are non-temporal:
+// each byte is touched once.
+template <int NTH>
+__device__ __forceinline__ float block_fmax(float v, float* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < NTH / 64; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+template <int NTH>
+__device__ __forceinline__ float block_fsum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  v = wave_sum(v);
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < NTH / 64; ++w) r += red[w];
+  return r;
+}
+
+template <typename InTag, typename OutTag, int NTH, int VPT, bool LOG>
+__global__ __launch_bounds__(NTH) void softmax_reg_kernel(
     typename ST<OutTag>::storage* __restrict__ out,
     const typename ST<InTag>::storage* __restrict__ in, int64_t D, int64_t in_row_stride,
     int64_t out_row_stride) {
   typedef typename ST<InTag>::storage Si;
   typedef typename ST<OutTag>::storage So;
   constexpr int VEC = 16 / sizeof(Si);
-  __shared__ float red[16];
+  __shared__ float red[2][NTH / 64];
   union Vi {
     uint4 u;
     Si s[VEC];
@@ -88,56 +116,58 @@ __global__ __launch_bounds__(kBlock) void softmax_reg_kernel(
   };
   const int64_t row = blockIdx.x;
   const Vi* pin = (const Vi*)(in + row * in_row_stride);
-  const int64_t nv = D / VEC;
+  const int nv = (int)(D / VEC);
   Vi x[VPT];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int v = threadIdx.x + k * NTH;
+    if (v < nv) x[k] = ld_stream(pin + v);
+  }
   float m = -INFINITY;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    const int64_t v = threadIdx.x + (int64_t)k * kBlock;
-    if (v < nv) {
-      x[k] = pin[v];
+    if ((int)threadIdx.x + k * NTH < nv) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) m = nan_max(m, ST<InTag>::load(x[k].s[e]));
+      for (int e = 0; e < VEC; ++e) m = fmaxf(m, ST<InTag>::load(x[k].s[e]));
     }
   }
-  m = block_max_f(m, red);
+  m = block_fmax<NTH>(m, red[0]);
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    const int64_t v = threadIdx.x + (int64_t)k * kBlock;
-    if (v < nv) {
+    if ((int)threadIdx.x + k * NTH < nv) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) s += kexp<InTag>(ST<InTag>::load(x[k].s[e]) - m);
     }
   }
-  s = block_sum_f(s, red);
+  s = block_fsum<NTH>(s, red[1]);
   So* po = out + row * out_row_stride;
   if constexpr (LOG) {
     const float lse = logf(s);
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-      const int64_t v = threadIdx.x + (int64_t)k * kBlock;
+      const int v = threadIdx.x + k * NTH;
       if (v < nv) {
         Vo o;
 #pragma unroll
         for (int e = 0; e < VEC; ++e)
           o.s[e] = ST<OutTag>::store((ST<InTag>::load(x[k].s[e]) - m) - lse);
 #pragma unroll
-        for (int w = 0; w < kWords; ++w) ((uint4*)(po + v * VEC))[w] = o.u[w];
+        for (int w = 0; w < kWords; ++w) st_stream((uint4*)(po + (int64_t)v * VEC) + w, o.u[w]);
       }
     }
   } else {
     const float inv = 1.0f / s;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-      const int64_t v = threadIdx.x + (int64_t)k * kBlock;
+      const int v = threadIdx.x + k * NTH;
       if (v < nv) {
         Vo o;
 #pragma unroll
         for (int e = 0; e < VEC; ++e)
           o.s[e] = ST<OutTag>::store(kexp<InTag>(ST<InTag>::load(x[k].s[e]) - m) * inv);
 #pragma unroll
-        for (int w = 0; w < kWords; ++w) ((uint4*)(po + v * VEC))[w] = o.u[w];
+        for (int w = 0; w < kWords; ++w) st_stream((uint4*)(po + (int64_t)v * VEC) + w, o.u[w]);
       }
     }
   }
@@ -224,20 +254,27 @@ mi_status_t launch_t(const mi_tensor_t* out, const mi_tensor_t* self, int dim,
     const bool aligned = ((uintptr_t)self->data % 16 == 0) &&
                          ((uintptr_t)out->data % 16 == 0) && (D % VEC == 0);
     const int64_t nv = D / VEC;
-    auto run_reg = [&](auto vpt_c) -> mi_status_t {
+    auto run_reg = [&](auto nth_c, auto vpt_c) -> mi_status_t {
+      constexpr int NTH = decltype(nth_c)::value;
       constexpr int VPT = decltype(vpt_c)::value;
-      hipLaunchKernelGGL((softmax_reg_kernel<InTag, OutTag, VPT, LOG>), dim3((unsigned)outer),
-                         dim3(kBlock), 0, stream, (typename ST<OutTag>::storage*)out->data,
-                         (const Si*)self->data, D, D, D);
+      hipLaunchKernelGGL((softmax_reg_kernel<InTag, OutTag, NTH, VPT, LOG>),
+                         dim3((unsigned)outer), dim3(NTH), 0, stream,
+                         (typename ST<OutTag>::storage*)out->data, (const Si*)self->data, D, D,
+                         D);
       return check_launch("softmax_reg");
     };
-    if (aligned && nv <= (int64_t)kBlock * 32 && outer <= 0x7fffffff) {
-      if (nv <= kBlock * 1) return run_reg(std::integral_constant<int, 1>());
-      if (nv <= kBlock * 2) return run_reg(std::integral_constant<int, 2>());
-      if (nv <= kBlock * 4) return run_reg(std::integral_constant<int, 4>());
-      if (nv <= kBlock * 8) return run_reg(std::integral_constant<int, 8>());
-      if (nv <= kBlock * 16) return run_reg(std::integral_constant<int, 16>());
-      return run_reg(std::integral_constant<int, 32>());
+    typedef std::integral_constant<int, 1> V1;
+    typedef std::integral_constant<int, 1024> N1024;
+    // rows of up to 256 K vectors: 1024 lanes hold up to 16 vectors each
+    // (64 VGPRs of row data); short rows take one vector per lane
+    if (aligned && nv <= 1024 * 16 && outer <= 0x7fffffff) {
+      if (nv <= 256) return run_reg(std::integral_constant<int, 256>(), V1());
+      if (nv <= 512) return run_reg(std::integral_constant<int, 512>(), V1());
+      if (nv <= 1024) return run_reg(N1024(), V1());
+      if (nv <= 2048) return run_reg(N1024(), std::integral_constant<int, 2>());
+      if (nv <= 4096) return run_reg(N1024(), std::integral_constant<int, 4>());
+      if (nv <= 8192) return run_reg(N1024(), std::integral_constant<int, 8>());
+      return run_reg(N1024(), std::integral_constant<int, 16>());
     }
     hipLaunchKernelGGL((softmax_row_kernel<InTag, OutTag, LOG>), dim3((unsigned)outer),
                        dim3(kBlock), 0, stream, (typename ST<OutTag>::storage*)out->data,
