@@ -138,3 +138,59 @@ def test_int8_linear_edges_and_bias():
     out = torch.empty(33, 300, dtype=torch.bfloat16, device="cuda")
     _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda(), bias.cuda())
     assert_close(out, aten.int8_linear(x, w, scales, bias), "bf16", "int8 ragged + bias")
+
+
+# ---- the 256 x 256 direct-to-LDS kernel (K % 64 == 0, >= 256 tiles) ------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(4100, 4200, 128), (4096, 4096, 64), (8192, 2049, 192)])
+def test_dl_kernel_ragged_tiles(dtype, M, N, K):
+    a = rn((M, K), 50, dtype, 1.0)
+    w = rn((N, K), 51, dtype, 1.0)  # F.linear weight, K contiguous
+    ref = aten.addmm(None, a, w.t(), beta=0.0)
+    out = torch.empty(M, N, dtype=dtype, device="cuda")
+    _abi.mm(out, a.cuda(), w.cuda().t())
+    assert_close(out, ref, "bf16", f"dl mm {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("bias_shape", ["row", "full", "col", "f32row"])
+def test_dl_kernel_bias_alpha_beta(bias_shape):
+    M, N, K = 4160, 4096, 256
+    a, w = rn((M, K), 52, std=1.0), rn((N, K), 53, std=1.0)
+    bias = {"row": rn((N,), 54, std=1.0), "full": rn((M, N), 54, std=1.0),
+            "col": rn((M, 1), 54, std=1.0),
+            "f32row": torch.randn(N, generator=g(54))}[bias_shape]
+    for alpha, beta in [(1.0, 1.0), (0.5, 2.0)]:
+        ref = aten.addmm(bias, a, w.t(), beta=beta, alpha=alpha)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        _abi.addmm(out, bias.cuda(), a.cuda(), w.cuda().t(), beta=beta, alpha=alpha)
+        assert_close(out, ref, "bf16", f"dl addmm {bias_shape} a={alpha} b={beta}")
+
+
+def test_dl_kernel_batched_strided_and_odd_ldc():
+    # bmm with enough batches to select the large-tile kernel
+    B, M, N, K = 64, 512, 512, 128
+    a, bt = rn((B, M, K), 55, std=1.0), rn((B, N, K), 56, std=1.0)
+    out = torch.empty(B, M, N, dtype=torch.bfloat16, device="cuda")
+    _abi.bmm(out, a.cuda(), bt.cuda().transpose(1, 2))
+    assert_close(out, aten.bmm(a, bt.transpose(1, 2).contiguous()), "bf16", "dl bmm")
+    # A rows inside a wider buffer (lda > K), output rows with an odd stride
+    M, N, K = 4096, 4096, 192
+    wide = rn((M, K + 64), 57, std=1.0)
+    a = wide[:, 32:32 + K]
+    w = rn((N, K), 58, std=1.0)
+    big = torch.zeros(M, N + 3, dtype=torch.bfloat16, device="cuda")
+    out = big[:, :N]
+    _abi.mm(out, wide.cuda()[:, 32:32 + K], w.cuda().t())
+    assert_close(out, aten.addmm(None, a, w.t(), beta=0.0), "bf16", "dl strided A, odd ldc")
+    assert (big[:, N:].cpu() == 0).all()
+
+
+def test_row_major_b_transpose_path():
+    """B as a row-major [K, N] matrix (config 4's layout) goes through the
+    tiled transpose into a K-contiguous copy, then the large-tile kernel."""
+    M, N, K = 4096, 4160, 320
+    a, b, bias = rn((M, K), 59, std=1.0), rn((K, N), 60, std=1.0), rn((N,), 61, std=1.0)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _abi.addmm(out, bias.cuda(), a.cuda(), b.cuda())
+    assert_close(out, aten.addmm(bias, a, b), "bf16", "row-major B")

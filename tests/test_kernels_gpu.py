@@ -513,3 +513,14 @@ def test_fused_edge_cases():
     out = torch.empty(3, 1001, dtype=torch.bfloat16, device=DEV)
     _abi.silu_mul(out, dev(gt), dev(up))
     assert_close(out, aten.silu_mul(gt, up), "bf16", "silu_mul ragged")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.int16])
+@pytest.mark.parametrize("shape", [(1000, 777), (64, 64), (3, 130, 70)])
+def test_transpose_copy(dtype, shape):
+    """copy_ of a transposed view (the tiled-transpose path) is bit-exact."""
+    x = rand(shape, dtype, 40)
+    view = x.transpose(-1, -2)
+    out = torch.empty(view.shape, dtype=dtype, device=DEV)
+    _abi.copy_(out, _strided_on_device(view))
+    assert_exact(out, view.contiguous(), f"transpose copy {shape}")

@@ -198,6 +198,35 @@ __global__ __launch_bounds__(kBlock) void copy_general_kernel(char* out, int dt_
 }
 
 // Same-dtype strided copy moving raw elements of size sizeof(T).
+// out[b][r][c] = src[b][r + c * src_ld] for a dense out ([R, C] per batch,
+// row stride out_ld): a transpose.  64 x 64 tiles go through LDS so that the
+// reads run along src's unit-stride dim and the writes along out's.
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(T* __restrict__ out, const T* __restrict__ src,
+                                                        int64_t R, int64_t C, int64_t out_ld,
+                                                        int64_t src_ld, int64_t out_bs,
+                                                        int64_t src_bs) {
+  __shared__ T tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const T* s = src + b * src_bs;
+  T* o = out + b * out_bs;
+  // read: lanes along r (src unit stride), rows of the tile along c
+#pragma unroll 4
+  for (int k = ty; k < 64; k += 4) {
+    const int64_t r = r0 + tx, c = c0 + k;
+    if (r < R && c < C) tile[k][tx] = s[r + c * src_ld];
+  }
+  __syncthreads();
+  // write: lanes along c (out unit stride)
+#pragma unroll 4
+  for (int k = ty; k < 64; k += 4) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    if (r < R && c < C) o[r * out_ld + c] = tile[tx][k];
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void copy_raw_kernel(T* out, const T* src,
                                                           OffsetCalc<2> oc, int64_t n) {
@@ -596,6 +625,28 @@ mi_status_t mi_copy(const mi_tensor_t* out, const mi_tensor_t* src, mi_stream_t 
         MI_FAIL(MI_ERR_LAUNCH, "copy: hipMemcpyAsync failed: %s",
                 hipGetErrorString(hipGetLastError()));
       return MI_OK;
+    }
+    // a transpose (out dense, src unit-stride along out's second-innermost
+    // dim): tiled through LDS instead of the strided element copy
+    const int nd = it.ndim;
+    if ((nd == 2 || nd == 3) && it.strides[0][nd - 1] == 1 && it.strides[1][nd - 2] == 1 &&
+        it.strides[1][nd - 1] != 1 && (esz == 2 || esz == 4) &&
+        (nd == 2 || it.sizes[0] <= 65535)) {
+      const int64_t R = it.sizes[nd - 2], C = it.sizes[nd - 1];
+      const int64_t batch = nd == 3 ? it.sizes[0] : 1;
+      const int64_t obs = nd == 3 ? it.strides[0][0] : 0, sbs = nd == 3 ? it.strides[1][0] : 0;
+      dim3 grid(ceil_div_u(C, 64), ceil_div_u(R, 64), (unsigned)batch);
+      if (grid.y <= 65535) {
+        if (esz == 2)
+          hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(256), 0, stream,
+                             (uint16_t*)it.data[0], (const uint16_t*)it.data[1], R, C,
+                             it.strides[0][nd - 2], it.strides[1][nd - 1], obs, sbs);
+        else
+          hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, dim3(256), 0, stream,
+                             (uint32_t*)it.data[0], (const uint32_t*)it.data[1], R, C,
+                             it.strides[0][nd - 2], it.strides[1][nd - 1], obs, sbs);
+        return check_launch("transpose");
+      }
     }
     OffsetCalc<2> oc = make_offset_calc<2>(it);
     const unsigned g = grid_for(it.numel);

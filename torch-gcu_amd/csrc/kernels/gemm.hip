@@ -331,6 +331,244 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_mfma_kernel(GemmArgs p) 
   }
 }
 
+// ---- 16-bit operands, K % 64 == 0: direct-to-LDS pipeline --------------------------
+//
+// 256 x 256 output tile per 512-lane block (8 waves as 4 along M x 2 along N,
+// each wave 64 x 128 = 2 x 4 MFMA tiles, so two waves share a SIMD and one
+// issues MFMAs while the other waits).  K steps of 64 flow through a ring of
+// two LDS stages that global_load_lds_dwordx4 fills straight from global
+// memory (no VGPR staging, no ds_write): the end of step k refills the stage
+// it just finished with step k + 2.  Rows are 128 B (8 chunks of 16 B) and
+// chunk c of row r is stored at chunk c ^ (r & 7) ^ ((r >> 3) & 1), which
+// keeps the 16-byte fragment reads of 16 consecutive rows on distinct banks
+// (whether the LDS is banked 32 or 64 wide).  Each substep's fragment reads
+// for the next substep, and at the step boundary the refill loads, are
+// interleaved with the MFMAs.  The epilogue applies alpha / beta * bias,
+// rounds once, stages each wave's 64 x 128 tile through LDS and stores whole
+// 256-byte row segments.
+namespace dl {
+constexpr int BK = 64, STAGES = 2, WM = 4, WN = 2, FM = 2, FN = 4;
+constexpr int NW = WM * WN, NT = 64 * NW;
+constexpr int BM = WM * FM * 32, BN = WN * FN * 32;  // 256 x 256
+constexpr int CH = BK / 8;                             // 16-byte chunks per row
+constexpr int RPK = 512 / BK;                          // rows per 1 KiB wave load
+constexpr int NQA = BM / RPK / NW, NQB = BN / RPK / NW;
+constexpr int LPS = NQA + NQB;                         // wave loads per step
+constexpr int TA = BM * BK, TB = BN * BK;
+constexpr int KS = BK / 16;
+constexpr int TM = FM * 32, TN = FN * 32, EP = TN + 8;  // epilogue tile, LDS pitch
+constexpr size_t LDS_BYTES =
+    (size_t)STAGES * (TA + TB) * 2 > (size_t)NW * TM * EP * 2 ? (size_t)STAGES * (TA + TB) * 2
+                                                                : (size_t)NW * TM * EP * 2;
+constexpr int GROUP_M = 4;
+}  // namespace dl
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  // s_waitcnt: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] at [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ int dl_swz(int r, int c) { return c ^ ((r & 7) ^ ((r >> 3) & 1)); }
+
+template <typename T, bool HAS_BIAS>
+__global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
+  constexpr int BK = dl::BK, STAGES = dl::STAGES, WN = dl::WN, FM = dl::FM, FN = dl::FN;
+  constexpr int BM = dl::BM, BN = dl::BN, CH = dl::CH, RPK = dl::RPK, NQA = dl::NQA,
+                NQB = dl::NQB, LPS = dl::LPS, TA = dl::TA, TB = dl::TB, KS = dl::KS,
+                TM = dl::TM, TN = dl::TN, EP = dl::EP, GROUP_M = dl::GROUP_M;
+  typedef typename MfmaOp<T>::vec vec;
+  extern __shared__ __align__(16) uint16_t smem[];
+  // XCD-aware tile order (round-robin dispatch over 8 XCDs), then groups of
+  // GROUP_M row panels so the tiles an XCD runs together share A and B panels
+  int tm, tn;
+  {
+    const int total = p.tiles_m * p.tiles_n;
+    int id = blockIdx.x;
+    if (total % 8 == 0) {
+      const int per = total / 8;
+      id = (id % 8) * per + id / 8;
+    }
+    const int group = id / (GROUP_M * p.tiles_n);
+    const int first_m = group * GROUP_M;
+    const int gsize = min(p.tiles_m - first_m, GROUP_M);
+    const int in_group = id - group * GROUP_M * p.tiles_n;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+  }
+  const int64_t batch = blockIdx.y;
+  const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const uint16_t* A = p.a + batch * p.sa;
+  const uint16_t* B = (const uint16_t*)p.b + batch * p.sb;
+
+  // per-lane byte offsets (the host checked they fit 32 bits); rows past the
+  // matrix are clamped to its last row and only feed outputs never stored
+  uint32_t ao[NQA], bo[NQB];
+#pragma unroll
+  for (int q = 0; q < NQA; ++q) {
+    const int row = (wave * NQA + q) * RPK + lane / CH;
+    ao[q] = (uint32_t)(((int64_t)min(m0 + row, M - 1) * p.lda + dl_swz(row, lane % CH) * 8) * 2);
+  }
+#pragma unroll
+  for (int q = 0; q < NQB; ++q) {
+    const int row = (wave * NQB + q) * RPK + lane / CH;
+    bo[q] = (uint32_t)(((int64_t)min(n0 + row, N - 1) * p.ldb + dl_swz(row, lane % CH) * 8) * 2);
+  }
+  auto issue = [&](int st, int k0) __attribute__((always_inline)) {
+    uint16_t* as = smem + st * (TA + TB);
+    uint16_t* bs = as + TA;
+    const char* Ab = (const char*)(A + k0);
+    const char* Bb = (const char*)(B + k0);
+#pragma unroll
+    for (int q = 0; q < NQA; ++q)
+      __builtin_amdgcn_global_load_lds((const void*)(Ab + ao[q]),
+                                       (lds_void_t*)(as + (wave * NQA + q) * 512), 16, 0, 0);
+#pragma unroll
+    for (int q = 0; q < NQB; ++q)
+      __builtin_amdgcn_global_load_lds((const void*)(Bb + bo[q]),
+                                       (lds_void_t*)(bs + (wave * NQB + q) * 512), 16, 0, 0);
+  };
+  // fragment read offsets: lane supplies row l % 32, k chunk 2 s + l / 32
+  int roff[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) roff[s] = (lane & 31) * BK + dl_swz(lane & 31, 2 * s + (lane >> 5)) * 8;
+
+  // acc[j][i] = D^T tile (n rows j, m cols i): B fragments are the MFMA's A
+  // operand, so a lane ends up owning one output row m and 4 runs of 4 n
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int i = 0; i < FM; ++i) acc[j][i] = f32x16{};
+  vec af[2][FM], bfr[2][FN];
+  auto read_frags = [&](int st, int s, int buf) __attribute__((always_inline)) {
+    const uint16_t* as = smem + st * (TA + TB) + wm * TM * BK + roff[s];
+    const uint16_t* bs = smem + st * (TA + TB) + TA + wn * TN * BK + roff[s];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[buf][i] = *(const vec*)(as + i * 32 * BK);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * 32 * BK);
+  };
+  auto mfmas = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) acc[j][i] = MfmaOp<T>::mma(bfr[buf][j], af[buf][i], acc[j][i]);
+  };
+  constexpr int NMF = FM * FN, NDS = FM + FN;
+  // one K step over stage st.  ISSUE: refill stage st with step kt + STAGES;
+  // NEXT: step kt + 1 exists and its first fragments are read here.
+  auto step = [&](int st, int kt, bool ISSUE, bool NEXT) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int buf = s & 1;
+      if (s + 1 < KS) {
+        read_frags(st, s + 1, buf ^ 1);
+        mfmas(buf);
+#pragma unroll
+        for (int k = 0; k < NDS; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, NMF - NDS, 0);
+      } else {
+        if (NEXT) {
+          // step kt + 1 has landed once at most the newer steps' loads are
+          // outstanding; the barrier also tells every wave that all waves
+          // are done reading stage st
+          if (ISSUE) wait_vmcnt<(STAGES - 2) * LPS>();
+          else wait_vmcnt<0>();
+          __syncthreads();
+          if (ISSUE) issue(st, (kt + STAGES) * BK);
+          read_frags(st + 1 == STAGES ? 0 : st + 1, 0, buf ^ 1);
+        }
+        mfmas(buf);
+#pragma unroll
+        for (int k = 0; k < NMF; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (ISSUE && k < LPS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+          if (NEXT && k < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  const int KT = K / BK;
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+    if (s < KT) issue(s, s * BK);
+  if (STAGES <= KT) wait_vmcnt<(STAGES - 1) * LPS>();
+  else wait_vmcnt<0>();
+  __syncthreads();
+  read_frags(0, 0, 0);
+  int st = 0, kt = 0;
+  for (; kt < KT - STAGES; ++kt) {
+    step(st, kt, true, true);
+    st = st + 1 == STAGES ? 0 : st + 1;
+  }
+  for (; kt < KT; ++kt) {
+    step(st, kt, false, kt + 1 < KT);
+    st = st + 1 == STAGES ? 0 : st + 1;
+  }
+
+  // epilogue: out = alpha * acc + beta * bias, one rounding, staged per wave
+  __syncthreads();
+  uint16_t* es = smem + wave * TM * EP;
+  const float alpha = p.alpha, beta = p.beta;
+  const bool bias_f32 = p.bias_dtype == MI_F32;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int ml = i * 32 + (lane & 31);
+    const int64_t m = m0 + wm * TM + ml;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
+        u16x4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = alpha * acc[j][i][4 * g + e];
+          if (HAS_BIAS) {
+            const int64_t n = min<int64_t>(n0 + wn * TN + nl + e, p.N - 1);
+            const int64_t bo_ = batch * p.bias_sb + min<int64_t>(m, p.M - 1) * p.bias_sm + n * p.bias_sn;
+            x += beta * (bias_f32 ? ((const float*)p.bias)[bo_]
+                                  : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo_]));
+          }
+          v[e] = MfmaOp<T>::store(x);
+        }
+        *(u16x4_t*)(es + ml * EP + nl) = v;
+      }
+  }
+  uint16_t* Cb = p.c + batch * p.sc;
+  const int64_t rbase = m0 + wm * TM, cbase = n0 + wn * TN;
+  constexpr int LPR = TN / 8, RPI = 64 / LPR;  // lanes per row, rows per pass
+  const bool vec_ok = (p.ldc % 8) == 0 && (((uintptr_t)Cb) & 15) == 0;
+#pragma unroll 4
+  for (int it = 0; it < TM / RPI; ++it) {
+    const int r = it * RPI + lane / LPR, c = (lane % LPR) * 8;
+    const uint4 v = *(const uint4*)(es + r * EP + c);
+    const int64_t m = rbase + r, n = cbase + c;
+    if (m < p.M) {
+      if (vec_ok && n + 7 < p.N) {
+        *(uint4*)(Cb + m * p.ldc + n) = v;
+      } else {
+        const uint16_t* pv = (const uint16_t*)&v;
+        for (int e = 0; e < 8; ++e)
+          if (n + e < p.N) Cb[m * p.ldc + n + e] = pv[e];
+      }
+    }
+  }
+}
+
 // ---- fp32: VALU tiled kernel (64 x 64 tile, 4 x 4 outputs per lane) ----------------
 
 struct GemmF32Args {
@@ -483,10 +721,41 @@ struct Cfg {
 
 // Tile configuration by problem shape: 256 x 256 when there are enough tiles
 // to fill the 256 CUs, narrower N tiles for short-M problems.
+// The direct-to-LDS kernel needs K % 64 == 0, 16-byte aligned rows and
+// per-batch byte offsets that fit 32 bits (lane offsets are 32-bit).
+bool dl_eligible(const GemmArgs& q) {
+  if (q.K % dl::BK != 0 || q.K == 0) return false;
+  if (q.lda % 8 != 0 || q.ldb % 8 != 0) return false;
+  if ((((uintptr_t)q.a) | ((uintptr_t)q.b)) & 15) return false;
+  if ((q.sa % 8) != 0 || (q.sb % 8) != 0) return false;
+  if (q.M > 0x7fffffff || q.N > 0x7fffffff || q.K > 0x7fffffff) return false;
+  const int64_t amax = (q.M - 1) * q.lda * 2 + q.K * 2, bmax = (q.N - 1) * q.ldb * 2 + q.K * 2;
+  return amax < ((int64_t)1 << 32) && bmax < ((int64_t)1 << 32);
+}
+
+template <typename T, bool HB>
+mi_status_t launch_dl(const GemmArgs& q0, int64_t batch, hipStream_t s, const char* what) {
+  static bool attr = [] {
+    (void)hipFuncSetAttribute((const void*)gemm_dl_kernel<T, HB>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)dl::LDS_BYTES);
+    return true;
+  }();
+  (void)attr;
+  GemmArgs q = q0;
+  q.tiles_m = (int)((q.M + dl::BM - 1) / dl::BM);
+  q.tiles_n = (int)((q.N + dl::BN - 1) / dl::BN);
+  dim3 grid((unsigned)(q.tiles_m * q.tiles_n), (unsigned)batch);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, HB>), grid, dim3(dl::NT), dl::LDS_BYTES, s, q);
+  return check_launch(what);
+}
+
 template <typename T, bool I8, bool HB>
 mi_status_t launch_mfma(const GemmArgs& q, int64_t batch, hipStream_t s, const char* what) {
   const int64_t cus = cu_count();
   const int64_t big = ((q.M + 255) / 256) * ((q.N + 255) / 256) * batch;
+  if constexpr (!I8) {
+    if (big >= cus && dl_eligible(q)) return launch_dl<T, HB>(q, batch, s, what);
+  }
   if (big >= cus) return Cfg<T, 256, 256, 2, 4, I8, HB>::launch(q, batch, s, what);
   if (q.M <= 32) return Cfg<T, 32, 64, 1, 2, I8, HB>::launch(q, batch, s, what);
   const int64_t mid = ((q.M + 127) / 128) * ((q.N + 127) / 128) * batch;
