@@ -173,22 +173,35 @@ def cpu_baseline(torch, synthetic, seconds):
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
+def hold_device(torch, ms=20.0):
+    """Keeps the stream busy for about `ms` with a spin kernel, so the launches
+    enqueued right after it reach the device back to back: the timed region
+    then measures device time, not the host's per-call launch cost."""
+    torch.cuda._sleep(int(ms * 2.4e6))  # the spin counts shader clocks (~2.4 GHz)
+
+
 def bench_op(torch, name, sets, fn, alg_bytes, iters=30, flops=None, bound="hbm"):
-    """Per-launch time of fn over rotating input sets (HIP events)."""
+    """Per-launch device time of fn over rotating input sets (HIP events on
+    the stream the ops run on; the launches are queued behind a spin kernel,
+    and `host_bound` reports whether the device caught up with the host)."""
     for s in sets[:2]:
         fn(s)
     torch.cuda.synchronize()
     st = torch.cuda.Event(enable_timing=True)
     en = torch.cuda.Event(enable_timing=True)
+    hold_device(torch)
     st.record()
     for i in range(iters):
         fn(sets[i % len(sets)])
     en.record()
+    host_bound = st.query()  # the device reached the start before all launches were queued
     torch.cuda.synchronize()
     ms = st.elapsed_time(en) / iters
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     r = {"op": name, "ms": round(ms, 4), "GB/s": round(gbs, 1),
          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes": alg_bytes}
+    if host_bound:
+        r["host_bound"] = True
     if flops is not None:
         tf = flops / (ms * 1e-3) / 1e12
         r.update({"TFLOP/s": round(tf, 1), "frac_mfma_bf16": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),

@@ -194,3 +194,29 @@ def test_row_major_b_transpose_path():
     out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
     _abi.addmm(out, bias.cuda(), a.cuda(), b.cuda())
     assert_close(out, aten.addmm(bias, a, b), "bf16", "row-major B")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (16, 11008, 4096), (33, 520, 1024),
+                                   (64, 4096, 640), (7, 17, 128), (5, 40, 192)])
+@pytest.mark.parametrize("bias", [None, "bf16", "f32"])
+def test_int8_linear_skinny(M, N, K, bias):
+    """M <= 64 and K % 128 == 0 take the weight-streaming kernel (16 W rows
+    per block, K split over four waves, partial tiles added in a fixed
+    order); K = 192 exercises the general kernel's int8 path."""
+    x, w, scales = int8_inputs(M, N=N, K=K, seed=70 + M)
+    b = None
+    if bias == "bf16":
+        b = torch.randn(N, generator=g(71)).to(torch.bfloat16)
+    elif bias == "f32":
+        b = torch.randn(N, generator=g(72))
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda(), None if b is None else b.cuda())
+    assert_close(out, aten.int8_linear(x, w, scales, b), "bf16", f"skinny M={M} N={N} K={K} {bias}")
+
+
+def test_int8_linear_skinny_f16():
+    x, w, scales = int8_inputs(24, N=777, K=512, seed=80)
+    x = x.to(torch.float16)
+    out = torch.empty(24, 777, dtype=torch.float16, device="cuda")
+    _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda())
+    assert_close(out, aten.int8_linear(x, w, scales), "bf16", "skinny f16")

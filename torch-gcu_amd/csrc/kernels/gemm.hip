@@ -569,6 +569,171 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
   }
 }
 
+// ---- int8 weight-only linear for few rows (M <= 64): HBM-bound on W -------------------
+//
+// A 256-lane block owns 16 output columns (16 rows of W [N, K]); its 4 waves
+// split K into interleaved 128-wide chunks, so per step the block reads 512
+// contiguous bytes of each of its 16 W rows and every 128-byte line is read
+// whole by one wave.  In a chunk, lane (r = l % 16, g = l / 16) streams
+// W[n0 + r][128 c + 32 g .. + 32] with two non-temporal 16-byte loads (up to
+// four chunks, with their x fragments, in flight), widens the 32 int8 to
+// bf16 (exact) and feeds four v_mfma_f32_16x16x32 with the matching 32 k of
+// each x row
+// (x is [M, K] and stays in cache).  The k order inside a chunk is the same
+// for both operands, so the sum is the plain dot product.  The four partial
+// 16 x 16 tiles are added in a fixed order through LDS; the epilogue applies
+// the per-column scale and bias and rounds once.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int int4v_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mfma16;
+template <>
+struct Mfma16<BF16> {
+  typedef bf16x8 vec;
+  static __device__ __forceinline__ f32x4_t mma(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ vec widen(int4v_t w, int half) {
+    vec v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int byte = 8 * half + e;
+      v[e] = (__bf16)(float)(int8_t)(w[byte >> 2] >> (8 * (byte & 3)));
+    }
+    return v;
+  }
+};
+template <>
+struct Mfma16<F16> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ f32x4_t mma(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ vec widen(int4v_t w, int half) {
+    vec v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int byte = 8 * half + e;
+      v[e] = (_Float16)(float)(int8_t)(w[byte >> 2] >> (8 * (byte & 3)));
+    }
+    return v;
+  }
+};
+
+constexpr int kSkN = 2;    // 16-row n-tiles per block (32 W rows)
+constexpr int kSkW = 8;    // waves per block, splitting K
+
+template <typename T, int MT, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * kSkW) void int8_skinny_kernel(GemmArgs p) {
+  typedef typename Mfma16<T>::vec vec;
+  __shared__ float red[kSkW][kSkN][16][17];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16 * kSkN;
+  // lane (r, g) owns bytes [32 g, 32 g + 32) of each 128-byte chunk of the W
+  // rows n0 + 16 t + r, so one wave reads whole 128-byte lines
+  const int8_t* wrow[kSkN];
+#pragma unroll
+  for (int t = 0; t < kSkN; ++t)
+    wrow[t] = (const int8_t*)p.b + min<int64_t>(n0 + 16 * t + r, p.N - 1) * p.ldb + 32 * g;
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xrow[mt] = p.a + min<int64_t>(mt * 16 + r, p.M - 1) * p.lda + 32 * g;
+  f32x4_t acc[MT][kSkN];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < kSkN; ++t) acc[mt][t] = f32x4_t{};
+  // one 128-wide chunk of W (kSkN tiles) and x in registers, double-buffered:
+  // the loads of chunk c + kSkW are in flight while chunk c is widened and
+  // multiplied
+  struct Chunk {
+    int4v_t w[kSkN][2];
+    vec x[MT][4];
+  };
+  auto load = [&](Chunk& ch, int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < kSkN; ++t) {
+      const int8_t* wp = wrow[t] + 128 * c;
+      ch.w[t][0] = __builtin_bit_cast(int4v_t, ld_stream((const uint4*)wp));
+      ch.w[t][1] = __builtin_bit_cast(int4v_t, ld_stream((const uint4*)(wp + 16)));
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) ch.x[mt][h] = *(const vec*)(xrow[mt] + 128 * c + 8 * h);
+  };
+  // consecutive MFMAs go to different accumulators (n-tiles inner)
+  auto compute = [&](const Chunk& ch) __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int t = 0; t < kSkN; ++t) {
+        const vec wk = Mfma16<T>::widen(ch.w[t][h >> 1], h & 1);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][t] = Mfma16<T>::mma(ch.x[mt][h], wk, acc[mt][t]);
+      }
+  };
+  const int KC = (int)(p.K / 128);  // chunks; wave w takes chunks w, w + kSkW, ...
+  // two named buffers (a runtime-indexed pair would live in scratch memory)
+  Chunk b0, b1;
+  if (wave < KC) load(b0, wave);
+  for (int c = wave; c < KC; c += 2 * kSkW) {
+    if (c + kSkW < KC) load(b1, c + kSkW);
+    compute(b0);
+    if (c + kSkW < KC) {
+      if (c + 2 * kSkW < KC) load(b0, c + 2 * kSkW);
+      compute(b1);
+    }
+  }
+  // D[m = 4 (l / 16) + i][n = l % 16] of each 16 x 16 (m-tile, n-tile); the
+  // m-tiles are reduced one at a time through LDS
+  const int tn = threadIdx.x & 15, tm = (threadIdx.x >> 4) & 15, tt = threadIdx.x >> 8;
+  const bool bias_f32 = p.bias_dtype == MI_F32;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    if (mt > 0) __syncthreads();
+#pragma unroll
+    for (int t = 0; t < kSkN; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][t][4 * g + i][r] = acc[mt][t][i];
+    __syncthreads();
+    const int64_t m = mt * 16 + tm;
+    if (m >= p.M) continue;
+    // 512 lanes: lane -> (n-tile tt (+2, ...), row m, column n)
+#pragma unroll
+    for (int t = tt; t < kSkN; t += 2) {
+      const int64_t n = n0 + 16 * t + tn;
+      if (n >= p.N) continue;
+      float sum = red[0][t][tm][tn];
+#pragma unroll
+      for (int w = 1; w < kSkW; ++w) sum += red[w][t][tm][tn];
+      float v = p.alpha * p.scale[n] * sum;
+      if (HAS_BIAS) {
+        const int64_t bo = m * p.bias_sm + n * p.bias_sn;
+        v += p.beta * (bias_f32 ? ((const float*)p.bias)[bo]
+                                : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo]));
+      }
+      p.c[m * p.ldc + n] = MfmaOp<T>::store(v);
+    }
+  }
+}
+
+template <typename T, bool HB>
+mi_status_t launch_skinny(const GemmArgs& q, hipStream_t s) {
+  const dim3 grid(ceil_div_u(q.N, 16 * kSkN)), block(64 * kSkW);
+  const int mt = (int)((q.M + 15) / 16);
+  switch (mt) {
+    case 1: hipLaunchKernelGGL((int8_skinny_kernel<T, 1, HB>), grid, block, 0, s, q); break;
+    case 2: hipLaunchKernelGGL((int8_skinny_kernel<T, 2, HB>), grid, block, 0, s, q); break;
+    case 3: hipLaunchKernelGGL((int8_skinny_kernel<T, 3, HB>), grid, block, 0, s, q); break;
+    default: hipLaunchKernelGGL((int8_skinny_kernel<T, 4, HB>), grid, block, 0, s, q); break;
+  }
+  return check_launch("int8_linear skinny");
+}
+
 // ---- fp32: VALU tiled kernel (64 x 64 tile, 4 x 4 outputs per lane) ----------------
 
 struct GemmF32Args {
@@ -961,8 +1126,22 @@ mi_status_t run_gemm(const mi_tensor_t* out, const mi_tensor_t* a, const mi_tens
   q.sc = Cw.sb;
   q.alpha = (float)alpha;
   q.beta = (float)beta;
-  if (A.dtype == MI_BF16) MI_RETURN_IF(dispatch_mfma<BF16>(q, int8, has_bias, batch, stream, what));
-  else MI_RETURN_IF(dispatch_mfma<F16>(q, int8, has_bias, batch, stream, what));
+  // int8 weight with few rows of x: the weight stream dominates
+  const bool skinny = int8 && batch == 1 && M <= 64 && K % 128 == 0 && (q.lda % 8) == 0 &&
+                      (q.ldb % 16) == 0 && ((((uintptr_t)q.a) | ((uintptr_t)q.b)) & 15) == 0 &&
+                      (N == 1 || Cw.s1 == 1);
+  if (skinny) {
+    mi_status_t st;
+    if (A.dtype == MI_BF16)
+      st = has_bias ? launch_skinny<BF16, true>(q, stream) : launch_skinny<BF16, false>(q, stream);
+    else
+      st = has_bias ? launch_skinny<F16, true>(q, stream) : launch_skinny<F16, false>(q, stream);
+    MI_RETURN_IF(st);
+  } else if (A.dtype == MI_BF16) {
+    MI_RETURN_IF(dispatch_mfma<BF16>(q, int8, has_bias, batch, stream, what));
+  } else {
+    MI_RETURN_IF(dispatch_mfma<F16>(q, int8, has_bias, batch, stream, what));
+  }
   if (!c_ok) {
     mi_tensor_t dst = mat_desc(C), src = mat_desc(Cw);
     MI_RETURN_IF(mi_copy(&dst, &src, (mi_stream_t)stream));
