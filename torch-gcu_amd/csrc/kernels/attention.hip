@@ -136,24 +136,30 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   }
 
   // ---- K / V staging: global -> registers -> LDS ----
+  // Per-lane element offsets are 32-bit (the host checked Sk * stride fits);
+  // a tile adds kv0 * stride, and only the last tile clamps its rows.
   u32x4 kr[C::KCH];
   u32x4 vr0, vr1, vr2, vr3;
   const bool v_lane = C::VGR >= NT || (int)threadIdx.x < C::VGR;
   const int vkg = threadIdx.x & 15, vdc = (threadIdx.x >> 4) * 8;
-  auto load_kv = [&](int64_t kv0) __attribute__((always_inline)) {
+  const int k_ss = (int)p.k_ss, v_ss = (int)p.v_ss, Sk = (int)p.Sk;
+  auto load_kv = [&](int kv0) __attribute__((always_inline)) {
+    const bool full = kv0 + KT <= Sk;
 #pragma unroll
     for (int i = 0; i < C::KCH; ++i) {
       const int c = threadIdx.x + i * NT;
       const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
-      const int64_t gk = min(kv0 + key, p.Sk - 1);
-      kr[i] = *(const u32x4*)(K + gk * p.k_ss + dc);
+      const int gk = full ? kv0 + key : min(kv0 + key, Sk - 1);
+      kr[i] = *(const u32x4*)(K + gk * k_ss + dc);
     }
     if (v_lane) {
-      const int64_t g0 = kv0 + 4 * vkg, last = p.Sk - 1;
-      vr0 = *(const u32x4*)(V + min(g0, last) * p.v_ss + vdc);
-      vr1 = *(const u32x4*)(V + min(g0 + 1, last) * p.v_ss + vdc);
-      vr2 = *(const u32x4*)(V + min(g0 + 2, last) * p.v_ss + vdc);
-      vr3 = *(const u32x4*)(V + min(g0 + 3, last) * p.v_ss + vdc);
+      const int g0 = kv0 + 4 * vkg;
+      const int r0 = full ? g0 : min(g0, Sk - 1), r1 = full ? g0 + 1 : min(g0 + 1, Sk - 1);
+      const int r2 = full ? g0 + 2 : min(g0 + 2, Sk - 1), r3 = full ? g0 + 3 : min(g0 + 3, Sk - 1);
+      vr0 = *(const u32x4*)(V + r0 * v_ss + vdc);
+      vr1 = *(const u32x4*)(V + r1 * v_ss + vdc);
+      vr2 = *(const u32x4*)(V + r2 * v_ss + vdc);
+      vr3 = *(const u32x4*)(V + r3 * v_ss + vdc);
     }
   };
   auto store_kv = [&](int stage) __attribute__((always_inline)) {
@@ -183,44 +189,66 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   for (int d = 0; d < DT; ++d) o[d] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const int64_t kv_end = p.causal ? min(p.Sk, q0 + QT) : p.Sk;
-  const int n_tiles = (int)((kv_end + KT - 1) / KT);
+  const int kv_end = (int)(p.causal ? min(p.Sk, q0 + QT) : p.Sk);
+  const int n_tiles = (kv_end + KT - 1) / KT;
+  const int wq = (int)wq0, qr = (int)qrow;
   load_kv(0);
   store_kv(0);
+  // the Q fragments and the first tile have landed: inside the loop the only
+  // outstanding global loads are the next tile's K / V
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int it = 0; it < n_tiles; ++it) {
-    const int64_t kv0 = (int64_t)it * KT;
+    const int kv0 = it * KT;
     const bool more = it + 1 < n_tiles;
     if (more) load_kv(kv0 + KT);
     __builtin_amdgcn_sched_barrier(0);
     const uint16_t* ks = smem + (it & 1) * C::STAGE;
     const uint16_t* vt = ks + C::KS;
-    if (!p.causal || kv0 <= wq0 + 31) {
-      // ---- S^T = K Q^T: two 32-key tiles x this wave's 32 queries ----
-      f32x16 s[2];
+    if (!p.causal || kv0 <= wq + 31) {
+      // ---- S^T = K Q^T: two 32-key tiles x this wave's 32 queries, the two
+      // accumulator chains interleaved ----
+      f32x16 s[2] = {f32x16{}, f32x16{}};
+      const uint16_t* kb0 = ks + col * C::KP + 8 * half;
+      const uint16_t* kb1 = kb0 + 32 * C::KP;
+      // K fragments double-buffered one k-step ahead of their MFMAs
+      vec kf[2][2];
+      kf[0][0] = *(const vec*)kb0;
+      kf[0][1] = *(const vec*)kb1;
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        s[st] = f32x16{};
-        const uint16_t* kb = ks + (st * 32 + col) * C::KP + 8 * half;
-#pragma unroll
-        for (int t = 0; t < DF; ++t) s[st] = AttnOp<T>::mma(*(const vec*)(kb + 16 * t), qf[t], s[st]);
+      for (int t = 0; t < DF; ++t) {
+        if (t + 1 < DF) {
+          kf[(t + 1) & 1][0] = *(const vec*)(kb0 + 16 * (t + 1));
+          kf[(t + 1) & 1][1] = *(const vec*)(kb1 + 16 * (t + 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        s[0] = AttnOp<T>::mma(kf[t & 1][0], qf[t], s[0]);
+        s[1] = AttnOp<T>::mma(kf[t & 1][1], qf[t], s[1]);
+        __builtin_amdgcn_sched_barrier(0);
       }
       // ---- mask, online softmax in the log2 domain ----
       // accumulator r of tile st holds key kv0 + 32 st + 8 (r / 4) + 4 half + r % 4
-      const bool need_mask = (kv0 + KT > p.Sk) || (p.causal && kv0 + KT - 1 > wq0);
       float mx = -INFINITY;
+      if ((kv0 + KT > Sk) || (p.causal && kv0 + KT - 1 > wq)) {
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
+        for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[st][r] * p.scale_log2;
-          if (need_mask) {
-            const int64_t key = kv0 + 32 * st + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (key >= p.Sk || (p.causal && key > qrow)) x = -INFINITY;
+          for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + 32 * st + 8 * (r >> 2) + 4 * half + (r & 3);
+            const bool dead = key >= Sk || (p.causal && key > qr);
+            const float x = dead ? -INFINITY : s[st][r] * p.scale_log2;
+            s[st][r] = x;
+            mx = fmaxf(mx, x);
           }
-          s[st][r] = x;
-          mx = fmaxf(mx, x);
-        }
+      } else {
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float x = s[st][r] * p.scale_log2;
+            s[st][r] = x;
+            mx = fmaxf(mx, x);
+          }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float m_new = fmaxf(m_run, mx);
@@ -247,16 +275,26 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
         for (int d = 0; d < DT; ++d) o[d] *= corr;
       }
       // ---- O^T += V^T P^T: the lane reads V^T[d][key] for the same keys:
-      // 16 t + 4 half + 0..3 and 16 t + 8 + 4 half + 0..3 ----
-#pragma unroll
-      for (int t = 0; t < KT / 16; ++t) {
+      // 16 t + 4 half + 0..3 and 16 t + 8 + 4 half + 0..3; a k-step's DT
+      // fragments are read before its MFMAs ----
+      vec vf[2][DT];
+      auto read_v = [&](int t, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
           const uint16_t* vb = vt + (d * 32 + col) * C::VP + 16 * t + 4 * half;
           const u32x2 a0 = *(const u32x2*)vb, a1 = *(const u32x2*)(vb + 8);
           const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
-          o[d] = AttnOp<T>::mma(__builtin_bit_cast(vec, a), pk[t], o[d]);
+          vf[buf][d] = __builtin_bit_cast(vec, a);
         }
+      };
+      read_v(0, 0);
+#pragma unroll
+      for (int t = 0; t < KT / 16; ++t) {
+        if (t + 1 < KT / 16) read_v(t + 1, (t + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[d] = AttnOp<T>::mma(vf[t & 1][d], pk[t], o[d]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (more) store_kv((it + 1) & 1);
@@ -373,6 +411,9 @@ extern "C" mi_status_t mi_flash_attention_fwd(const mi_tensor_t* out, const mi_t
   a.o_sb = out->strides[0];
   a.o_sh = out->strides[1];
   a.o_ss = out->strides[2];
+  MI_CHECK_ARG(Sk * k->strides[2] + D < 0x7fffffffLL && Sk * v->strides[2] + D < 0x7fffffffLL &&
+                   Sq + QT < 0x7fffffffLL,
+               "attention: a (batch, head) of k or v spans more than 2^31 elements");
   a.scale_log2 = (float)(scale * 1.4426950408889634);
   a.causal = is_causal ? 1 : 0;
   a.q_tiles = (int)((Sq + QT - 1) / QT);
