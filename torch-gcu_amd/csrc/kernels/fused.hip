@@ -194,10 +194,10 @@ struct RopeTensor {
   int64_t out_tok_stride, out_head_stride;
 };
 
-// A block owns `tpb` consecutive tokens.  Its lanes first compute the
-// tokens' fp32 cos/sin tables (tpb x half each) into LDS, one sincosf per
-// (token, pair) as the fp32 closed form does, then stream the tokens' q and
-// k rows: a job is one (token, head, slice of P pairs) and reads the two
+// A block owns `tpb` consecutive tokens.  Its lanes issue their first q/k
+// loads, compute the tokens' fp32 cos/sin tables (tpb x half each) into LDS
+// meanwhile, one sincosf per (token, pair) as the fp32 closed form does, then
+// stream the tokens' q and k rows: a job is one (token, head, slice of P pairs) and reads the two
 // 16-byte halves x1 = x[j*P ..], x2 = x[half + j*P ..].  Jobs run head-major
 // within a token, so a wave's loads cover 8 heads x 256 B of one token row
 // contiguously, and each lane keeps eight jobs' loads in flight.
@@ -218,22 +218,16 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeTensor q, RopeTensor k, c
   const int nt = (int)min((int64_t)tpb, tokens - t0);
   float* cs_c = rope_cs;
   float* cs_s = rope_cs + tpb * half;
-  for (int idx = threadIdx.x; idx < nt * half; idx += 256) {
-    const int tt = idx / half, i = idx - tt * half;
-    const float p = (float)pos[(t0 + tt) * pos_stride];
-    // inv_freq = 1 / theta^(2i/d), as in the fp32 closed form
-    const float inv_freq = 1.0f / powf(theta_f, (float)(2 * i) / dim_f);
-    sincosf(p * inv_freq, &cs_s[idx], &cs_c[idx]);
-  }
-  __syncthreads();
   const int slices = half / P;
   const int jq = q.in ? (int)q.heads * slices : 0;
   const int jpt = jq + (k.in ? (int)k.heads * slices : 0);
   const int total = nt * jpt;
-  for (int b0 = threadIdx.x; b0 < total; b0 += 256 * kRopeUnroll) {
-    V xa[kRopeUnroll], xb[kRopeUnroll];
-    St* op[kRopeUnroll];
-    int ci[kRopeUnroll];
+
+  V xa[kRopeUnroll], xb[kRopeUnroll];
+  St* op[kRopeUnroll];
+  int ci[kRopeUnroll];
+  // job -> (token, tensor, head, slice); issues the job's two 16-byte loads
+  auto fetch = [&](int b0) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kRopeUnroll; ++u) {
       const int job = b0 + u * 256;
@@ -253,6 +247,21 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeTensor q, RopeTensor k, c
         xb[u] = ld_stream((const V*)(in + half));
       }
     }
+  };
+  // the first batch of loads is in flight while the cos/sin tables are built
+  fetch(threadIdx.x);
+  float* inv_freq = rope_cs + 2 * tpb * half;
+  for (int i = threadIdx.x; i < half; i += 256)
+    inv_freq[i] = 1.0f / powf(theta_f, (float)(2 * i) / dim_f);  // 1 / theta^(2i/d), fp32
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < nt * half; idx += 256) {
+    const int tt = idx / half, i = idx - tt * half;
+    const float p = (float)pos[(t0 + tt) * pos_stride];
+    sincosf(p * inv_freq[i], &cs_s[idx], &cs_c[idx]);
+  }
+  __syncthreads();
+  for (int b0 = threadIdx.x; b0 < total; b0 += 256 * kRopeUnroll) {
+    if (b0 != (int)threadIdx.x) fetch(b0);
 #pragma unroll
     for (int u = 0; u < kRopeUnroll; ++u) {
       if (op[u] != nullptr) {
@@ -447,12 +456,13 @@ mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out, const mi
     MI_CHECK_ARG(k->dtype == q->dtype, "rope: q and k dtypes differ");
   if (tokens == 0) return MI_OK;
   const int64_t half = D / 2;
-  MI_CHECK_ARG(half <= 8192, "rope: head_dim %lld too large", (long long)D);
+  MI_CHECK_ARG(half <= 4096, "rope: head_dim %lld too large (at most 8192)", (long long)D);
   MI_CHECK_ARG((rq.heads + rk.heads) * (half / P) * 16 < (int64_t)1 << 31,
                "rope: too many heads");
-  // tokens per block: 16, fewer when the cos/sin tables would pass 64 KiB of LDS
-  const int tpb = (int)std::max<int64_t>(1, std::min<int64_t>(16, 8192 / half));
-  const size_t lds = (size_t)2 * tpb * half * sizeof(float);
+  // tokens per block: 16, fewer when the cos/sin tables (2 * tpb * half fp32)
+  // plus inv_freq (half fp32) would pass 64 KiB of LDS
+  const int tpb = (int)std::max<int64_t>(1, std::min<int64_t>(16, (16384 / half - 1) / 2));
+  const size_t lds = (size_t)(2 * tpb + 1) * half * sizeof(float);  // cos, sin, inv_freq
   const unsigned grid = ceil_div_u(tokens, tpb);
   const float l2t = (float)theta;
   const float inv_dim = (float)D;
