@@ -220,3 +220,21 @@ def test_int8_linear_skinny_f16():
     out = torch.empty(24, 777, dtype=torch.float16, device="cuda")
     _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda())
     assert_close(out, aten.int8_linear(x, w, scales), "bf16", "skinny f16")
+
+
+@pytest.mark.parametrize("dtype,bias", [(torch.bfloat16, None), (torch.bfloat16, "bf16"),
+                                        (torch.float16, "f32")])
+def test_int8_linear_large_tile_path(dtype, bias):
+    """M > 64 with >= 256 tiles of 256 x 256: int8 W rows DMA'd into LDS and
+    widened to 16-bit at fragment read, per-column scale in the epilogue."""
+    M, N, K = 4096, 4100, 192
+    x, w, scales = int8_inputs(M, N=N, K=K, seed=90)
+    x = x.to(dtype)
+    b = None
+    if bias == "bf16":
+        b = torch.randn(N, generator=g(91)).to(torch.bfloat16)
+    elif bias == "f32":
+        b = torch.randn(N, generator=g(92))
+    out = torch.empty(M, N, dtype=dtype, device="cuda")
+    _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda(), None if b is None else b.cuda())
+    assert_close(out, aten.int8_linear(x, w, scales, b), "bf16", f"int8 large tile {dtype} {bias}")

@@ -361,6 +361,8 @@ constexpr size_t LDS_BYTES =
     (size_t)STAGES * (TA + TB) * 2 > (size_t)NW * TM * EP * 2 ? (size_t)STAGES * (TA + TB) * 2
                                                                 : (size_t)NW * TM * EP * 2;
 constexpr int GROUP_M = 4;
+// int8 B: 64-byte rows (4 chunks of 16 B), 16 rows per 1 KiB wave load
+constexpr int CH8 = 4, RPK8 = 16, NQB8 = BN / RPK8 / NW, TB8 = BN * BK / 2;  // TB8 in 16-bit units
 }  // namespace dl
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -373,13 +375,35 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 __device__ __forceinline__ int dl_swz(int r, int c) { return c ^ ((r & 7) ^ ((r >> 3) & 1)); }
+// 64-byte rows: chunk c of row r at c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1), conflict-free for
+// 16-byte reads of 16 consecutive rows under 32- or 64-bank LDS
+__device__ __forceinline__ int dl_swz64(int r, int c) { return c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1)); }
 
-template <typename T, bool HAS_BIAS>
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// 8 int8 (two words) -> 8 x bf16 / f16, exact
+template <typename T>
+__device__ __forceinline__ typename MfmaOp<T>::vec widen8(u32x2_t w) {
+  typename MfmaOp<T>::vec v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float f = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
+    if constexpr (std::is_same<T, BF16>::value) v[e] = (__bf16)f;
+    else v[e] = (_Float16)f;
+  }
+  return v;
+}
+
+template <typename T, bool HAS_BIAS, bool B_INT8>
 __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
   constexpr int BK = dl::BK, STAGES = dl::STAGES, WN = dl::WN, FM = dl::FM, FN = dl::FN;
   constexpr int BM = dl::BM, BN = dl::BN, CH = dl::CH, RPK = dl::RPK, NQA = dl::NQA,
-                NQB = dl::NQB, LPS = dl::LPS, TA = dl::TA, TB = dl::TB, KS = dl::KS,
-                TM = dl::TM, TN = dl::TN, EP = dl::EP, GROUP_M = dl::GROUP_M;
+                TA = dl::TA, KS = dl::KS, TM = dl::TM, TN = dl::TN, EP = dl::EP,
+                GROUP_M = dl::GROUP_M;
+  // the B tile: 16-bit rows of 128 B, or int8 rows of 64 B (widened at fragment read)
+  constexpr int NQB = B_INT8 ? dl::NQB8 : dl::NQB;
+  constexpr int TB = B_INT8 ? dl::TB8 : dl::TB;
+  constexpr int LPS = NQA + NQB;
   typedef typename MfmaOp<T>::vec vec;
   extern __shared__ __align__(16) uint16_t smem[];
   // XCD-aware tile order (round-robin dispatch over 8 XCDs), then groups of
@@ -406,7 +430,7 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const uint16_t* A = p.a + batch * p.sa;
-  const uint16_t* B = (const uint16_t*)p.b + batch * p.sb;
+  const char* Bbase = (const char*)p.b + batch * p.sb * (B_INT8 ? 1 : 2);
 
   // per-lane byte offsets (the host checked they fit 32 bits); rows past the
   // matrix are clamped to its last row and only feed outputs never stored
@@ -418,14 +442,19 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
   }
 #pragma unroll
   for (int q = 0; q < NQB; ++q) {
-    const int row = (wave * NQB + q) * RPK + lane / CH;
-    bo[q] = (uint32_t)(((int64_t)min(n0 + row, N - 1) * p.ldb + dl_swz(row, lane % CH) * 8) * 2);
+    if constexpr (B_INT8) {
+      const int row = (wave * NQB + q) * dl::RPK8 + lane / dl::CH8;
+      bo[q] = (uint32_t)((int64_t)min(n0 + row, N - 1) * p.ldb + dl_swz64(row, lane % dl::CH8) * 16);
+    } else {
+      const int row = (wave * NQB + q) * RPK + lane / CH;
+      bo[q] = (uint32_t)(((int64_t)min(n0 + row, N - 1) * p.ldb + dl_swz(row, lane % CH) * 8) * 2);
+    }
   }
   auto issue = [&](int st, int k0) __attribute__((always_inline)) {
     uint16_t* as = smem + st * (TA + TB);
     uint16_t* bs = as + TA;
     const char* Ab = (const char*)(A + k0);
-    const char* Bb = (const char*)(B + k0);
+    const char* Bb = Bbase + (int64_t)k0 * (B_INT8 ? 1 : 2);
 #pragma unroll
     for (int q = 0; q < NQA; ++q)
       __builtin_amdgcn_global_load_lds((const void*)(Ab + ao[q]),
@@ -436,9 +465,14 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
                                        (lds_void_t*)(bs + (wave * NQB + q) * 512), 16, 0, 0);
   };
   // fragment read offsets: lane supplies row l % 32, k chunk 2 s + l / 32
-  int roff[KS];
+  int roff[KS], roffb[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) roff[s] = (lane & 31) * BK + dl_swz(lane & 31, 2 * s + (lane >> 5)) * 8;
+  for (int s = 0; s < KS; ++s) {
+    roff[s] = (lane & 31) * BK + dl_swz(lane & 31, 2 * s + (lane >> 5)) * 8;
+    // int8 B: byte offset of k 16 s + 8 (lane / 32) .. + 8 in 64-byte rows
+    roffb[s] = (lane & 31) * BK + dl_swz64(lane & 31, s) * 16 + 8 * (lane >> 5);
+  }
+  (void)roffb;
 
   // acc[j][i] = D^T tile (n rows j, m cols i): B fragments are the MFMA's A
   // operand, so a lane ends up owning one output row m and 4 runs of 4 n
@@ -450,11 +484,17 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
   vec af[2][FM], bfr[2][FN];
   auto read_frags = [&](int st, int s, int buf) __attribute__((always_inline)) {
     const uint16_t* as = smem + st * (TA + TB) + wm * TM * BK + roff[s];
-    const uint16_t* bs = smem + st * (TA + TB) + TA + wn * TN * BK + roff[s];
 #pragma unroll
     for (int i = 0; i < FM; ++i) af[buf][i] = *(const vec*)(as + i * 32 * BK);
+    if constexpr (B_INT8) {
+      const char* bs = (const char*)(smem + st * (TA + TB) + TA) + wn * TN * BK + roffb[s];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * 32 * BK);
+      for (int j = 0; j < FN; ++j) bfr[buf][j] = widen8<T>(*(const u32x2_t*)(bs + j * 32 * BK));
+    } else {
+      const uint16_t* bs = smem + st * (TA + TB) + TA + wn * TN * BK + roff[s];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * 32 * BK);
+    }
   };
   auto mfmas = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -537,6 +577,7 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float x = alpha * acc[j][i][4 * g + e];
+          if (B_INT8) x *= p.scale[min<int64_t>(n0 + wn * TN + nl + e, p.N - 1)];
           if (HAS_BIAS) {
             const int64_t n = min<int64_t>(n0 + wn * TN + nl + e, p.N - 1);
             const int64_t bo_ = batch * p.bias_sb + min<int64_t>(m, p.M - 1) * p.bias_sm + n * p.bias_sn;
@@ -888,20 +929,22 @@ struct Cfg {
 // to fill the 256 CUs, narrower N tiles for short-M problems.
 // The direct-to-LDS kernel needs K % 64 == 0, 16-byte aligned rows and
 // per-batch byte offsets that fit 32 bits (lane offsets are 32-bit).
-bool dl_eligible(const GemmArgs& q) {
+bool dl_eligible(const GemmArgs& q, bool int8) {
+  const int bes = int8 ? 1 : 2;  // bytes per B element
   if (q.K % dl::BK != 0 || q.K == 0) return false;
-  if (q.lda % 8 != 0 || q.ldb % 8 != 0) return false;
+  if (q.lda % 8 != 0 || (q.ldb * bes) % 16 != 0) return false;
   if ((((uintptr_t)q.a) | ((uintptr_t)q.b)) & 15) return false;
-  if ((q.sa % 8) != 0 || (q.sb % 8) != 0) return false;
+  if ((q.sa % 8) != 0 || (q.sb * bes) % 16 != 0) return false;
   if (q.M > 0x7fffffff || q.N > 0x7fffffff || q.K > 0x7fffffff) return false;
-  const int64_t amax = (q.M - 1) * q.lda * 2 + q.K * 2, bmax = (q.N - 1) * q.ldb * 2 + q.K * 2;
+  const int64_t amax = (q.M - 1) * q.lda * 2 + q.K * 2,
+                bmax = ((q.N - 1) * q.ldb + q.K) * bes;
   return amax < ((int64_t)1 << 32) && bmax < ((int64_t)1 << 32);
 }
 
-template <typename T, bool HB>
+template <typename T, bool HB, bool I8>
 mi_status_t launch_dl(const GemmArgs& q0, int64_t batch, hipStream_t s, const char* what) {
   static bool attr = [] {
-    (void)hipFuncSetAttribute((const void*)gemm_dl_kernel<T, HB>,
+    (void)hipFuncSetAttribute((const void*)gemm_dl_kernel<T, HB, I8>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)dl::LDS_BYTES);
     return true;
   }();
@@ -910,7 +953,7 @@ mi_status_t launch_dl(const GemmArgs& q0, int64_t batch, hipStream_t s, const ch
   q.tiles_m = (int)((q.M + dl::BM - 1) / dl::BM);
   q.tiles_n = (int)((q.N + dl::BN - 1) / dl::BN);
   dim3 grid((unsigned)(q.tiles_m * q.tiles_n), (unsigned)batch);
-  hipLaunchKernelGGL((gemm_dl_kernel<T, HB>), grid, dim3(dl::NT), dl::LDS_BYTES, s, q);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, HB, I8>), grid, dim3(dl::NT), dl::LDS_BYTES, s, q);
   return check_launch(what);
 }
 
@@ -918,9 +961,7 @@ template <typename T, bool I8, bool HB>
 mi_status_t launch_mfma(const GemmArgs& q, int64_t batch, hipStream_t s, const char* what) {
   const int64_t cus = cu_count();
   const int64_t big = ((q.M + 255) / 256) * ((q.N + 255) / 256) * batch;
-  if constexpr (!I8) {
-    if (big >= cus && dl_eligible(q)) return launch_dl<T, HB>(q, batch, s, what);
-  }
+  if (big >= cus && dl_eligible(q, I8)) return launch_dl<T, HB, I8>(q, batch, s, what);
   if (big >= cus) return Cfg<T, 256, 256, 2, 4, I8, HB>::launch(q, batch, s, what);
   if (q.M <= 32) return Cfg<T, 32, 64, 1, 2, I8, HB>::launch(q, batch, s, what);
   const int64_t mid = ((q.M + 127) / 128) * ((q.N + 127) / 128) * batch;
