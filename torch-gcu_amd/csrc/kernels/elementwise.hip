@@ -19,7 +19,7 @@ namespace mi {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 8;
 
 enum OpKind { OP_ADD = 0, OP_MUL = 1, OP_DIV = 2 };
 enum Mode { M_FULL = 0, M_ROW = 1, M_COL = 2, M_SCALAR = 3 };

@@ -194,21 +194,25 @@ struct RopeTensor {
   int64_t out_tok_stride, out_head_stride;
 };
 
-// A block owns `tpb` consecutive tokens.  Its lanes issue their first q/k
-// loads, compute the tokens' fp32 cos/sin tables (tpb x half each) into LDS
-// meanwhile, one sincosf per (token, pair) as the fp32 closed form does, then
-// stream the tokens' q and k rows: a job is one (token, head, slice of P pairs) and reads the two
-// 16-byte halves x1 = x[j*P ..], x2 = x[half + j*P ..].  Jobs run head-major
-// within a token, so a wave's loads cover 8 heads x 256 B of one token row
-// contiguously, and each lane keeps eight jobs' loads in flight.
-constexpr int kRopeUnroll = 8;
+// A block owns `tpb` consecutive tokens.  A job is one (tensor, head, slice
+// of P pairs) of a token and reads the two 16-byte halves x1 = x[j*P ..],
+// x2 = x[half + j*P ..]; the jobs of a token are numbered head-major (q heads
+// first), so a wave's loads cover 8 heads x 256 B of one token row
+// contiguously.  Lane l takes jobs l, l + 256, ... (NJ of them) of every
+// token, so their (tensor, head, slice) decode is done once per block and a
+// token step is a stride addition.  The lanes issue their first loads, then
+// build the tokens' fp32 cos/sin tables in LDS (one sincosf per token and
+// pair, as the fp32 closed form does, with inv_freq computed once per
+// block), then stream the tokens with eight jobs in flight per lane.
+constexpr int kRopeInflight = 8;
 
-template <typename Tag, typename PosT>
+template <typename Tag, typename PosT, int NJ>
 __global__ __launch_bounds__(256) void rope_kernel(RopeTensor q, RopeTensor k, const PosT* pos,
                                                    int64_t pos_stride, int64_t tokens, int half,
                                                    int tpb, float theta_f, float dim_f) {
   typedef typename FT<Tag>::storage St;
   constexpr int P = 16 / sizeof(St);
+  constexpr int TB = kRopeInflight / NJ > 0 ? kRopeInflight / NJ : 1;  // tokens per batch
   union V {
     uint4 u;
     St s[P];
@@ -218,39 +222,49 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeTensor q, RopeTensor k, c
   const int nt = (int)min((int64_t)tpb, tokens - t0);
   float* cs_c = rope_cs;
   float* cs_s = rope_cs + tpb * half;
+  float* inv_freq = rope_cs + 2 * tpb * half;
   const int slices = half / P;
   const int jq = q.in ? (int)q.heads * slices : 0;
   const int jpt = jq + (k.in ? (int)k.heads * slices : 0);
-  const int total = nt * jpt;
 
-  V xa[kRopeUnroll], xb[kRopeUnroll];
-  St* op[kRopeUnroll];
-  int ci[kRopeUnroll];
-  // job -> (token, tensor, head, slice); issues the job's two 16-byte loads
-  auto fetch = [&](int b0) __attribute__((always_inline)) {
+  // the lane's job slots, decoded once
+  const St* in0[NJ];
+  St* out0[NJ];
+  int64_t ist[NJ], ost[NJ];
+  int cso[NJ];
+  bool live[NJ];
 #pragma unroll
-    for (int u = 0; u < kRopeUnroll; ++u) {
-      const int job = b0 + u * 256;
-      op[u] = nullptr;
-      if (job < total) {
-        const int tt = job / jpt;
-        int r = job - tt * jpt;
-        const bool isk = r >= jq;
-        if (isk) r -= jq;
-        const RopeTensor& rt = isk ? k : q;
-        const int h = r / slices, j = r - h * slices;
-        const int64_t t = t0 + tt;
-        const St* in = (const St*)rt.in + t * rt.in_tok_stride + h * rt.in_head_stride + j * P;
-        op[u] = (St*)rt.out + t * rt.out_tok_stride + h * rt.out_head_stride + j * P;
-        ci[u] = tt * half + j * P;
-        xa[u] = ld_stream((const V*)in);
-        xb[u] = ld_stream((const V*)(in + half));
+  for (int m = 0; m < NJ; ++m) {
+    const int j = threadIdx.x + 256 * m;
+    live[m] = j < jpt;
+    int r = live[m] ? j : 0;
+    const bool isk = r >= jq;
+    if (isk) r -= jq;
+    const RopeTensor& rt = isk ? k : q;
+    const int h = r / slices, sl = r - h * slices;
+    in0[m] = (const St*)rt.in + t0 * rt.in_tok_stride + h * rt.in_head_stride + sl * P;
+    out0[m] = (St*)rt.out + t0 * rt.out_tok_stride + h * rt.out_head_stride + sl * P;
+    ist[m] = rt.in_tok_stride;
+    ost[m] = rt.out_tok_stride;
+    cso[m] = sl * P;
+  }
+  V xa[TB][NJ], xb[TB][NJ];
+  auto fetch = [&](int tt0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < TB; ++u) {
+      const int tt = tt0 + u;
+#pragma unroll
+      for (int m = 0; m < NJ; ++m) {
+        if (tt < nt && live[m]) {
+          const St* in = in0[m] + tt * ist[m];
+          xa[u][m] = ld_stream((const V*)in);
+          xb[u][m] = ld_stream((const V*)(in + half));
+        }
       }
     }
   };
   // the first batch of loads is in flight while the cos/sin tables are built
-  fetch(threadIdx.x);
-  float* inv_freq = rope_cs + 2 * tpb * half;
+  fetch(0);
   for (int i = threadIdx.x; i < half; i += 256)
     inv_freq[i] = 1.0f / powf(theta_f, (float)(2 * i) / dim_f);  // 1 / theta^(2i/d), fp32
   __syncthreads();
@@ -260,21 +274,27 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeTensor q, RopeTensor k, c
     sincosf(p * inv_freq[i], &cs_s[idx], &cs_c[idx]);
   }
   __syncthreads();
-  for (int b0 = threadIdx.x; b0 < total; b0 += 256 * kRopeUnroll) {
-    if (b0 != (int)threadIdx.x) fetch(b0);
+  for (int tt0 = 0; tt0 < nt; tt0 += TB) {
+    if (tt0 > 0) fetch(tt0);
 #pragma unroll
-    for (int u = 0; u < kRopeUnroll; ++u) {
-      if (op[u] != nullptr) {
-        V oa, ob;
+    for (int u = 0; u < TB; ++u) {
+      const int tt = tt0 + u;
 #pragma unroll
-        for (int e = 0; e < P; ++e) {
-          const float c = cs_c[ci[u] + e], sn = cs_s[ci[u] + e];
-          const float x1 = FT<Tag>::load(xa[u].s[e]), x2 = FT<Tag>::load(xb[u].s[e]);
-          oa.s[e] = FT<Tag>::store(x1 * c - x2 * sn);
-          ob.s[e] = FT<Tag>::store(x2 * c + x1 * sn);
+      for (int m = 0; m < NJ; ++m) {
+        if (tt < nt && live[m]) {
+          const int ci = tt * half + cso[m];
+          V oa, ob;
+#pragma unroll
+          for (int e = 0; e < P; ++e) {
+            const float c = cs_c[ci + e], sn = cs_s[ci + e];
+            const float x1 = FT<Tag>::load(xa[u][m].s[e]), x2 = FT<Tag>::load(xb[u][m].s[e]);
+            oa.s[e] = FT<Tag>::store(x1 * c - x2 * sn);
+            ob.s[e] = FT<Tag>::store(x2 * c + x1 * sn);
+          }
+          St* o = out0[m] + tt * ost[m];
+          st_stream((V*)o, oa);
+          st_stream((V*)(o + half), ob);
         }
-        st_stream((V*)op[u], oa);
-        st_stream((V*)(op[u] + half), ob);
       }
     }
   }
@@ -457,8 +477,11 @@ mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out, const mi
   if (tokens == 0) return MI_OK;
   const int64_t half = D / 2;
   MI_CHECK_ARG(half <= 4096, "rope: head_dim %lld too large (at most 8192)", (long long)D);
-  MI_CHECK_ARG((rq.heads + rk.heads) * (half / P) * 16 < (int64_t)1 << 31,
-               "rope: too many heads");
+  // jobs of one token (heads x slices of q and k), spread over 256 lanes
+  const int64_t jpt = (rq.heads + rk.heads) * (half / P);
+  MI_CHECK_ARG(jpt <= 256 * 8, "rope: %lld (head, slice) jobs per token exceed 2048",
+               (long long)jpt);
+  const int nj = (int)((jpt + 255) / 256);
   // tokens per block: 16, fewer when the cos/sin tables (2 * tpb * half fp32)
   // plus inv_freq (half fp32) would pass 64 KiB of LDS
   const int tpb = (int)std::max<int64_t>(1, std::min<int64_t>(16, (16384 / half - 1) / 2));
@@ -467,21 +490,27 @@ mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out, const mi
   const float l2t = (float)theta;
   const float inv_dim = (float)D;
   const int64_t ps = positions->strides[0];
-#define MI_ROPE_LAUNCH(TAG)                                                                   \
-  if (positions->dtype == MI_I64)                                                           \
-    hipLaunchKernelGGL((rope_kernel<TAG, int64_t>), dim3(grid), dim3(256), lds, stream, rq,  \
-                       rk, (const int64_t*)positions->data, ps, tokens, (int)half, tpb, l2t, \
-                       inv_dim);                                                            \
-  else                                                                                      \
-    hipLaunchKernelGGL((rope_kernel<TAG, int32_t>), dim3(grid), dim3(256), lds, stream, rq,  \
-                       rk, (const int32_t*)positions->data, ps, tokens, (int)half, tpb, l2t, \
+#define MI_ROPE_LAUNCH2(TAG, NJ)                                                              \
+  if (positions->dtype == MI_I64)                                                             \
+    hipLaunchKernelGGL((rope_kernel<TAG, int64_t, NJ>), dim3(grid), dim3(256), lds, stream, rq, \
+                       rk, (const int64_t*)positions->data, ps, tokens, (int)half, tpb, l2t,   \
+                       inv_dim);                                                              \
+  else                                                                                        \
+    hipLaunchKernelGGL((rope_kernel<TAG, int32_t, NJ>), dim3(grid), dim3(256), lds, stream, rq, \
+                       rk, (const int32_t*)positions->data, ps, tokens, (int)half, tpb, l2t,   \
                        inv_dim);
+#define MI_ROPE_LAUNCH(TAG)                   \
+  if (nj == 1) { MI_ROPE_LAUNCH2(TAG, 1) }    \
+  else if (nj == 2) { MI_ROPE_LAUNCH2(TAG, 2) } \
+  else if (nj <= 4) { MI_ROPE_LAUNCH2(TAG, 4) } \
+  else { MI_ROPE_LAUNCH2(TAG, 8) }
   switch (q->dtype) {
     case MI_BF16: MI_ROPE_LAUNCH(BF16) break;
     case MI_F16: MI_ROPE_LAUNCH(F16) break;
     default: MI_ROPE_LAUNCH(float) break;
   }
 #undef MI_ROPE_LAUNCH
+#undef MI_ROPE_LAUNCH2
   return check_launch("rope");
 }
 
