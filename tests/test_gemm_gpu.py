@@ -197,12 +197,15 @@ def test_row_major_b_transpose_path():
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (16, 11008, 4096), (33, 520, 1024),
-                                   (64, 4096, 640), (7, 17, 128), (5, 40, 192)])
+                                   (64, 4096, 640), (7, 17, 128), (5, 40, 192),
+                                   (48, 1000, 2048), (2, 33, 3072), (64, 96, 5120)])
 @pytest.mark.parametrize("bias", [None, "bf16", "f32"])
 def test_int8_linear_skinny(M, N, K, bias):
-    """M <= 64 and K % 128 == 0 take the weight-streaming kernel (16 W rows
-    per block, K split over four waves, partial tiles added in a fixed
-    order); K = 192 exercises the general kernel's int8 path."""
+    """M <= 64: K % 1024 == 0 takes the LDS-staged weight stream (32 W rows
+    per block in 1 KiB slabs, an odd slab count included, ragged N), other
+    K % 128 == 0 the register weight stream (K split over eight waves);
+    partial tiles are added in a fixed order.  K = 192 exercises the general
+    kernel's int8 path."""
     x, w, scales = int8_inputs(M, N=N, K=K, seed=70 + M)
     b = None
     if bias == "bf16":
@@ -214,12 +217,13 @@ def test_int8_linear_skinny(M, N, K, bias):
     assert_close(out, aten.int8_linear(x, w, scales, b), "bf16", f"skinny M={M} N={N} K={K} {bias}")
 
 
-def test_int8_linear_skinny_f16():
-    x, w, scales = int8_inputs(24, N=777, K=512, seed=80)
+@pytest.mark.parametrize("K", [512, 2048])
+def test_int8_linear_skinny_f16(K):
+    x, w, scales = int8_inputs(24, N=777, K=K, seed=80)
     x = x.to(torch.float16)
     out = torch.empty(24, 777, dtype=torch.float16, device="cuda")
     _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda())
-    assert_close(out, aten.int8_linear(x, w, scales), "bf16", "skinny f16")
+    assert_close(out, aten.int8_linear(x, w, scales), "bf16", f"skinny f16 K={K}")
 
 
 @pytest.mark.parametrize("dtype,bias", [(torch.bfloat16, None), (torch.bfloat16, "bf16"),

@@ -4,9 +4,10 @@
 //   rms_norm  reads x once and writes y once: one wave per row holds the row
 //             in registers (4096 bf16 = 8 x 16-byte vectors per lane), so the
 //             sum of squares and the scaling share a single HBM read;
-//   rope      a block computes the cos/sin tables of its 16 tokens once into
+//   rope      a block computes the cos/sin tables of its few tokens once into
 //             LDS (one sincosf per token and pair, shared by all 2 x 32
-//             heads), then streams the tokens' q and k rows contiguously;
+//             heads) while the tokens' q and k rows load, then rotates and
+//             stores them;
 //   silu_mul  streams gate and up with four 16-byte vectors per operand in
 //             flight per lane; silu uses the hardware exp2 and reciprocal.
 // Arithmetic is fp32 with one rounding to the output type, which is what
@@ -482,9 +483,13 @@ mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out, const mi
   MI_CHECK_ARG(jpt <= 256 * 8, "rope: %lld (head, slice) jobs per token exceed 2048",
                (long long)jpt);
   const int nj = (int)((jpt + 255) / 256);
-  // tokens per block: 16, fewer when the cos/sin tables (2 * tpb * half fp32)
-  // plus inv_freq (half fp32) would pass 64 KiB of LDS
-  const int tpb = (int)std::max<int64_t>(1, std::min<int64_t>(16, (16384 / half - 1) / 2));
+  // tokens per block: one batch of loads (kRopeInflight / NJ tokens), so a
+  // block loads, rotates, stores and exits and the next block's loads overlap
+  // its stores; fewer when the cos/sin tables (2 * tpb * half fp32) plus
+  // inv_freq (half fp32) would pass 64 KiB of LDS
+  const int nj_t = nj == 1 ? 1 : nj == 2 ? 2 : nj <= 4 ? 4 : 8;
+  const int tpb = (int)std::max<int64_t>(
+      1, std::min<int64_t>(std::max(1, kRopeInflight / nj_t), (16384 / half - 1) / 2));
   const size_t lds = (size_t)(2 * tpb + 1) * half * sizeof(float);  // cos, sin, inv_freq
   const unsigned grid = ceil_div_u(tokens, tpb);
   const float l2t = (float)theta;

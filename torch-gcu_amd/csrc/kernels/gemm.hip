@@ -612,16 +612,15 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
 
 // ---- int8 weight-only linear for few rows (M <= 64): HBM-bound on W -------------------
 //
-// A 256-lane block owns 16 output columns (16 rows of W [N, K]); its 4 waves
-// split K into interleaved 128-wide chunks, so per step the block reads 512
-// contiguous bytes of each of its 16 W rows and every 128-byte line is read
-// whole by one wave.  In a chunk, lane (r = l % 16, g = l / 16) streams
-// W[n0 + r][128 c + 32 g .. + 32] with two non-temporal 16-byte loads (up to
-// four chunks, with their x fragments, in flight), widens the 32 int8 to
-// bf16 (exact) and feeds four v_mfma_f32_16x16x32 with the matching 32 k of
-// each x row
-// (x is [M, K] and stays in cache).  The k order inside a chunk is the same
-// for both operands, so the sum is the plain dot product.  The four partial
+// A 512-lane block owns 32 output columns (two 16-row tiles of W [N, K]);
+// its 8 waves split K into interleaved 128-wide chunks, so per step the block
+// reads 1 KiB contiguous bytes of each of its W rows and every 128-byte line
+// is read whole by one wave.  In a chunk, lane (r = l % 16, g = l / 16)
+// streams W[n0 + 16 t + r][128 c + 32 g .. + 32] with two non-temporal
+// 16-byte loads per tile t, widens the 32 int8 to bf16 (exact) and feeds
+// v_mfma_f32_16x16x32 with the matching 32 k of each x row (x is [M, K] and
+// stays in cache).  The k order inside a chunk is the same for both
+// operands, so the sum is the plain dot product.  The 8 waves' partial
 // 16 x 16 tiles are added in a fixed order through LDS; the epilogue applies
 // the per-column scale and bias and rounds once.
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -666,7 +665,7 @@ constexpr int kSkN = 2;    // 16-row n-tiles per block (32 W rows)
 constexpr int kSkW = 8;    // waves per block, splitting K
 
 template <typename T, int MT, bool HAS_BIAS>
-__global__ __launch_bounds__(64 * kSkW) void int8_skinny_kernel(GemmArgs p) {
+__global__ __launch_bounds__(64 * kSkW, MT == 1 ? 4 : 1) void int8_skinny_kernel(GemmArgs p) {
   typedef typename Mfma16<T>::vec vec;
   __shared__ float red[kSkW][kSkN][16][17];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -712,7 +711,12 @@ __global__ __launch_bounds__(64 * kSkW) void int8_skinny_kernel(GemmArgs p) {
     for (int h = 0; h < 4; ++h)
 #pragma unroll
       for (int t = 0; t < kSkN; ++t) {
-        const vec wk = Mfma16<T>::widen(ch.w[t][h >> 1], h & 1);
+        // the empty asm pins the start of the byte unpacking here, so the
+        // compiler cannot unpack every loaded W byte into its own register
+        // right after the loads
+        int4v_t wd = ch.w[t][h >> 1];
+        asm volatile("" : "+v"(wd));
+        const vec wk = Mfma16<T>::widen(wd, h & 1);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt][t] = Mfma16<T>::mma(ch.x[mt][h], wk, acc[mt][t]);
       }
@@ -773,6 +777,158 @@ mi_status_t launch_skinny(const GemmArgs& q, hipStream_t s) {
     default: hipLaunchKernelGGL((int8_skinny_kernel<T, 4, HB>), grid, block, 0, s, q); break;
   }
   return check_launch("int8_linear skinny");
+}
+
+// ---- int8 weight-only linear for few rows, weight staged through LDS ------------------
+//
+// The contraction of int8_skinny_kernel for K % 1024 == 0 and 16-byte aligned
+// W rows.  A 512-lane block owns 32 W rows and walks K in 1 KiB slabs.  A
+// slab (32 rows x 1 KiB) is copied by global_load_lds_dwordx4 straight into
+// LDS, each wave load one contiguous 1 KiB row segment (HBM sees long
+// contiguous runs; a wave load spread over 16 rows, as the MFMA operand
+// layout would ask for, streams at about two thirds of the rate), into a
+// ring of two slabs; the slab's x fragments are loaded into registers right
+// after it.  Wave w multiplies k-steps 4w .. 4w + 3 (32 k each) of every
+// slab: 8-byte fragment reads from LDS (row pitch 1056 B, so the 16 rows of
+// a read land on different banks), widened to bf16 (exact), into
+// v_mfma_f32_16x16x32 with x as the 16-row operand.  The 8 waves' partial
+// tiles are added in a fixed order through LDS; the epilogue applies the
+// per-column scale and bias and rounds once.
+constexpr int kStRows = 32, kStSlab = 1024, kStPitch = kStSlab + 32, kStWaves = 8;
+constexpr int kStLds = 2 * kStRows * kStPitch;
+
+template <typename T, int MT, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * kStWaves, MT <= 2 ? 4 : 2) void int8_stream_kernel(GemmArgs p) {
+  typedef typename Mfma16<T>::vec vec;
+  extern __shared__ __align__(16) char st_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * kStRows;
+  const int S = (int)(p.K / kStSlab);
+  // the wave copies rows 4 wave .. 4 wave + 3 of every slab (rows past N are
+  // clamped to the last row and only feed columns never stored)
+  const int8_t* wsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    wsrc[i] = (const int8_t*)p.b + min<int64_t>(n0 + 4 * wave + i, p.N - 1) * p.ldb + lane * 16;
+  // x fragment of k-step ks of slab s: row 16 mt + r, k = 1024 s + 32 (4 wave + ks) + 8 g
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xrow[mt] = p.a + min<int64_t>(16 * mt + r, p.M - 1) * p.lda + 128 * wave + 8 * g;
+  auto issue = [&](int buf, int s) __attribute__((always_inline)) {
+    char* dst = st_lds + buf * (kStRows * kStPitch) + 4 * wave * kStPitch;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(wsrc[i] + (int64_t)s * kStSlab),
+                                       (lds_void_t*)(dst + i * kStPitch), 16, 0, 0);
+  };
+  auto loadx = [&](vec (&xf)[MT][4], int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        xf[mt][ks] = *(const vec*)(xrow[mt] + (int64_t)s * kStSlab + 32 * ks);
+  };
+  f32x4_t acc[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4_t{};
+  auto compute = [&](int buf, const vec (&xf)[MT][4]) __attribute__((always_inline)) {
+    const char* wb = st_lds + buf * (kStRows * kStPitch) + r * kStPitch + 128 * wave + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const vec wk = widen8<T>(*(const u32x2_t*)(wb + t * 16 * kStPitch + 32 * ks));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][t] = Mfma16<T>::mma(xf[mt][ks], wk, acc[mt][t]);
+      }
+  };
+  // slab s lives in LDS buffer s % 2 and x registers xa (s even) / xb (s odd);
+  // a slab is complete once at most the next slab's loads (4 W + 4 MT x) are
+  // outstanding, and the barrier makes every wave's copy visible
+  constexpr int NEXT = 4 + 4 * MT;
+  vec xa[MT][4], xb[MT][4];
+  issue(0, 0);
+  loadx(xa, 0);
+  if (S > 1) {
+    issue(1, 1);
+    loadx(xb, 1);
+  }
+  for (int s = 0; s < S; s += 2) {
+    if (s + 1 < S) wait_vmcnt<NEXT>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    compute(0, xa);
+    __syncthreads();
+    if (s + 2 < S) {
+      issue(0, s + 2);
+      loadx(xa, s + 2);
+    }
+    if (s + 1 >= S) break;
+    if (s + 2 < S) wait_vmcnt<NEXT>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    compute(1, xb);
+    __syncthreads();
+    if (s + 3 < S) {
+      issue(1, s + 3);
+      loadx(xb, s + 3);
+    }
+  }
+  // fixed-order combine of the 8 waves' partial tiles (the slab ring is free)
+  float(*red)[2][16][17] = (float(*)[2][16][17])st_lds;
+  const int tn = threadIdx.x & 15, tm = (threadIdx.x >> 4) & 15, tt = threadIdx.x >> 8;
+  const bool bias_f32 = p.bias_dtype == MI_F32;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    if (mt > 0) __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][t][4 * g + i][r] = acc[mt][t][i];
+    __syncthreads();
+    const int64_t m = mt * 16 + tm;
+    if (m >= p.M) continue;
+    const int64_t n = n0 + 16 * tt + tn;
+    if (n >= p.N) continue;
+    float sum = red[0][tt][tm][tn];
+#pragma unroll
+    for (int w = 1; w < kStWaves; ++w) sum += red[w][tt][tm][tn];
+    float v = p.alpha * p.scale[n] * sum;
+    if (HAS_BIAS) {
+      const int64_t bo = m * p.bias_sm + n * p.bias_sn;
+      v += p.beta * (bias_f32 ? ((const float*)p.bias)[bo]
+                              : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo]));
+    }
+    p.c[m * p.ldc + n] = MfmaOp<T>::store(v);
+  }
+}
+
+template <typename T, int MT, bool HB>
+mi_status_t launch_stream_mt(const GemmArgs& q, hipStream_t s) {
+  static bool attr = [] {
+    (void)hipFuncSetAttribute((const void*)int8_stream_kernel<T, MT, HB>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kStLds);
+    return true;
+  }();
+  (void)attr;
+  hipLaunchKernelGGL((int8_stream_kernel<T, MT, HB>), dim3(ceil_div_u(q.N, kStRows)),
+                     dim3(64 * kStWaves), kStLds, s, q);
+  return check_launch("int8_linear stream");
+}
+
+template <typename T, bool HB>
+mi_status_t launch_stream(const GemmArgs& q, hipStream_t s) {
+  switch ((int)((q.M + 15) / 16)) {
+    case 1: return launch_stream_mt<T, 1, HB>(q, s);
+    case 2: return launch_stream_mt<T, 2, HB>(q, s);
+    case 3: return launch_stream_mt<T, 3, HB>(q, s);
+    default: return launch_stream_mt<T, 4, HB>(q, s);
+  }
 }
 
 // ---- fp32: VALU tiled kernel (64 x 64 tile, 4 x 4 outputs per lane) ----------------
@@ -1171,7 +1327,16 @@ mi_status_t run_gemm(const mi_tensor_t* out, const mi_tensor_t* a, const mi_tens
   const bool skinny = int8 && batch == 1 && M <= 64 && K % 128 == 0 && (q.lda % 8) == 0 &&
                       (q.ldb % 16) == 0 && ((((uintptr_t)q.a) | ((uintptr_t)q.b)) & 15) == 0 &&
                       (N == 1 || Cw.s1 == 1);
-  if (skinny) {
+  // K in whole 1 KiB slabs: the LDS-staged weight stream; else the register one
+  const bool stream_ok = skinny && K % kStSlab == 0;
+  if (stream_ok) {
+    mi_status_t st;
+    if (A.dtype == MI_BF16)
+      st = has_bias ? launch_stream<BF16, true>(q, stream) : launch_stream<BF16, false>(q, stream);
+    else
+      st = has_bias ? launch_stream<F16, true>(q, stream) : launch_stream<F16, false>(q, stream);
+    MI_RETURN_IF(st);
+  } else if (skinny) {
     mi_status_t st;
     if (A.dtype == MI_BF16)
       st = has_bias ? launch_skinny<BF16, true>(q, stream) : launch_skinny<BF16, false>(q, stream);

@@ -18,17 +18,25 @@ __device__ __forceinline__ int64_t read_index(const IdxT* idx, int64_t i, int64_
   return (int64_t)idx[i * istride];
 }
 
-// Dense rows, moved as 16-byte (W = uint4) or 8/4/2/1-byte words.
+// Dense rows, moved as 16-byte (W = uint4) or 8/4/2/1-byte words, one word
+// per lane: the four lanes of a 64-byte row share its index load, and the
+// grid covers every word once, so each lane's index -> row load chain is
+// its only work.  When the words per row are a power of two (LOG2 >= 0) the
+// row and word come from a shift and a mask instead of a division.
 template <typename W, typename IdxT>
 __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
     W* __restrict__ out, const W* __restrict__ self, const IdxT* __restrict__ idx,
-    int64_t istride, int64_t outer, int64_t n_idx, int64_t src_rows, int64_t words_per_row) {
+    int64_t istride, int64_t outer, int64_t n_idx, int64_t src_rows, int64_t words_per_row,
+    int log2_wpr) {
   const int64_t total = outer * n_idx * words_per_row;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   const bool small = total < 0x7fffffffLL;
   for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
     int64_t row, w, o, i;
-    if (small) {  // 32-bit division is several times cheaper
+    if (log2_wpr >= 0) {
+      row = t >> log2_wpr;
+      w = t & (words_per_row - 1);
+    } else if (small) {  // 32-bit division is several times cheaper
       const uint32_t r32 = (uint32_t)t / (uint32_t)words_per_row;
       w = (uint32_t)t - r32 * (uint32_t)words_per_row;
       row = r32;
@@ -50,7 +58,8 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
     } else {
       v = W{};
     }
-    out[t] = v;
+    if constexpr (sizeof(W) == 16) st_stream(out + t, v);
+    else out[t] = v;
   }
 }
 
@@ -104,9 +113,14 @@ mi_status_t launch_rows(const mi_tensor_t* out, const mi_tensor_t* self, const I
     typedef decltype(word) W;
     const int64_t wpr = row_bytes / (int64_t)sizeof(W);
     const int64_t total = outer * n_idx * wpr;
+    int log2_wpr = -1;
+    if ((wpr & (wpr - 1)) == 0) {
+      log2_wpr = 0;
+      while ((int64_t(1) << log2_wpr) < wpr) ++log2_wpr;
+    }
     hipLaunchKernelGGL((gather_rows_kernel<W, IdxT>), dim3(grid_for(total)), dim3(kBlock), 0,
                        stream, (W*)out->data, (const W*)self->data, idx, istride, outer, n_idx,
-                       src_rows, wpr);
+                       src_rows, wpr, log2_wpr);
     return check_launch("index_select rows");
   };
   if (row_bytes % 16 == 0 && align % 16 == 0) return go(uint4{});

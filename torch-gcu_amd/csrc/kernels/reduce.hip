@@ -185,13 +185,14 @@ __global__ __launch_bounds__(256) void row_reduce_wave_kernel(
 }
 
 constexpr int kColBlock = 256;
-constexpr int kColUnroll = 8;
+constexpr int kColUnroll = 4;
 
 // [outer, R, inner] column reduction over R, first pass: 256 lanes side by
 // side along a row (a lane owns VEC adjacent columns, so a block reads
 // 256 * VEC contiguous elements of each row), each walking the rows of its
-// split with eight loads in flight.  Output layout [outer, splits, inner]
-// (Acc partials, or the final value when there is one split).
+// split in batches of four rows, two batches in flight.  Output layout
+// [outer, splits, inner] (Acc partials, or the final value when there is one
+// split).
 template <typename Tag, int VEC>
 __global__ __launch_bounds__(kColBlock) void col_reduce_kernel(
     const typename RT<Tag>::storage* __restrict__ in, int64_t R, int64_t inner,
@@ -214,17 +215,37 @@ __global__ __launch_bounds__(kColBlock) void col_reduce_kernel(
   };
   const V* base = (const V*)(in + (o * R) * inner) + cv;
   int64_t r = beg;
-  for (; r + kColUnroll <= end; r += kColUnroll) {
-    V x[kColUnroll];
+  // two batches of kColUnroll rows: the loads of batch b + 1 are issued
+  // before batch b is added, so up to 2 * kColUnroll loads are in flight;
+  // rows are still added in ascending order
+  V xa[kColUnroll], xb[kColUnroll];
+  auto fetch = [&](V* x, int64_t r0) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kColUnroll; ++u) {
-      if constexpr (sizeof(V) == 16) x[u] = ld_stream(base + (r + u) * ncv);
-      else x[u] = base[(r + u) * ncv];
+      if constexpr (sizeof(V) == 16) x[u] = ld_stream(base + (r0 + u) * ncv);
+      else x[u] = base[(r0 + u) * ncv];
     }
+  };
+  auto add = [&](const V* x) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kColUnroll; ++u)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[e] = red_combine(op, acc[e], RT<Tag>::load(x[u].s[e]));
+  };
+  if (r + kColUnroll <= end) {
+    fetch(xa, r);
+    while (true) {
+      const bool nb = r + 2 * kColUnroll <= end;
+      if (nb) fetch(xb, r + kColUnroll);
+      add(xa);
+      r += kColUnroll;
+      if (!nb) break;
+      const bool na = r + 2 * kColUnroll <= end;
+      if (na) fetch(xa, r + kColUnroll);
+      add(xb);
+      r += kColUnroll;
+      if (!na) break;
+    }
   }
   for (; r < end; ++r) {
     const V x = base[r * ncv];
@@ -252,12 +273,13 @@ __global__ __launch_bounds__(256) void col_finish_kernel(const A* __restrict__ p
     const int64_t o = c / inner, i = c - o * inner;
     const A* p = part + o * S * inner + i;
     int64_t s = ty;
-    for (; s + 112 < S; s += 128) {
-      A x[8];
+    // 16 loads in flight: 256 partials (config 2's split count) in one round
+    for (; s + 240 < S; s += 256) {
+      A x[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = p[(s + 16 * u) * inner];
+      for (int u = 0; u < 16; ++u) x[u] = p[(s + 16 * u) * inner];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc = red_combine(op, acc, x[u]);
+      for (int u = 0; u < 16; ++u) acc = red_combine(op, acc, x[u]);
     }
     for (; s < S; s += 16) acc = red_combine(op, acc, p[s * inner]);
   }
