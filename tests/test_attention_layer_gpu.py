@@ -13,6 +13,7 @@ import torch.nn.functional as F
 
 import torch_gcu  # noqa: F401
 from oracle import aten
+from oracle import numpy_ref as npr
 from oracle.tolerance import assert_close, assert_composed_close, assert_exact
 from torch_gcu import _abi
 from torch_gcu.utils import decoder_layer as dl
@@ -48,6 +49,34 @@ def test_flash_attention_parity(B, H, Hk, Sq, Sk, D, causal):
     lse = torch.empty(B, H, Sq, dtype=torch.float32, device="cuda")
     _abi.flash_attention_fwd(out, lse, q.cuda(), k.cuda(), v.cuda(), causal)
     assert_close(out, ref, "bf16", f"attention {B},{H},{Hk},{Sq},{Sk},{D},{causal}")
+    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2 * max(1.0, ref_lse.abs().max().item())
+
+
+@pytest.mark.parametrize("scale,ramp,causal", [
+    (0.3, False, True), (-0.05, False, True), (-0.05, False, False),
+    (None, True, True), (None, True, False), (-0.08, True, False),
+])
+def test_flash_attention_scale_and_rescale(scale, ramp, causal):
+    """Explicit positive and negative scales (the scale is folded into the
+    exponent, so the running max is taken over sign-adjusted raw scores), and
+    keys whose scores grow along the sequence (ramp), so the row max keeps
+    growing and O is rescaled many times."""
+    B, H, S, D = 1, 2, 320, 128
+    q, k, v = rn((B, H, S, D), 11), rn((B, H, S, D), 12), rn((B, H, S, D), 13)
+    if ramp:
+        k = (k.float() * torch.linspace(0.2, 3.0, S)[None, None, :, None]).to(torch.bfloat16)
+    if scale is None or scale > 0:
+        ref, ref_lse = ref_attention(q, k, v, causal, scale)
+    else:
+        # CPU ATen's flash attention returns NaN (causal) or zeros for a
+        # negative scale, so the float64 closed form is the reference there
+        ro, rl = npr.attention64(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal,
+                                 scale)
+        ref, ref_lse = torch.from_numpy(ro).bfloat16(), torch.from_numpy(rl).float()
+    out = torch.empty(B, H, S, D, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(B, H, S, dtype=torch.float32, device="cuda")
+    _abi.flash_attention_fwd(out, lse, q.cuda(), k.cuda(), v.cuda(), causal, scale)
+    assert_close(out, ref, "bf16", f"attention scale={scale} ramp={ramp} causal={causal}")
     assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2 * max(1.0, ref_lse.abs().max().item())
 
 

@@ -18,7 +18,8 @@
 //   3. the online softmax is therefore per lane, in fp32, in the log2
 //      domain: the row max needs one exchange between the two half-waves,
 //      the running sum none until the end, and the rescale factor is a
-//      per-lane scalar;
+//      per-lane scalar; the scale is folded into the exp2 argument (one
+//      FMA per score);
 //   4. P, rounded to the input type, is already laid out as the B operand of
 //      O^T += V^T P^T (keys are fed to the MFMA's k dimension in a permuted
 //      order that matches the S^T accumulator layout, and V^T is read in the
@@ -227,34 +228,46 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
         __builtin_amdgcn_sched_barrier(0);
       }
       // ---- mask, online softmax in the log2 domain ----
-      // accumulator r of tile st holds key kv0 + 32 st + 8 (r / 4) + 4 half + r % 4
+      // accumulator r of tile st holds key kv0 + 32 st + 8 (r / 4) + 4 half + r % 4.
+      // The max is taken over the raw scores times the sign of the scale (a
+      // free source negation) and the scale is folded into the exponent:
+      // p = exp2(s * scale_log2 - m_run).  Dead keys get the raw score whose
+      // scaled value is -inf.
+      const bool neg = p.scale_log2 < 0.f;
       float mx = -INFINITY;
       if ((kv0 + KT > Sk) || (p.causal && kv0 + KT - 1 > wq)) {
+        const float dead_s = neg ? INFINITY : -INFINITY;
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = kv0 + 32 * st + 8 * (r >> 2) + 4 * half + (r & 3);
             const bool dead = key >= Sk || (p.causal && key > qr);
-            const float x = dead ? -INFINITY : s[st][r] * p.scale_log2;
+            const float x = dead ? dead_s : s[st][r];
             s[st][r] = x;
-            mx = fmaxf(mx, x);
+            mx = fmaxf(mx, neg ? -x : x);
           }
+      } else if (!neg) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
       } else {
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float x = s[st][r] * p.scale_log2;
-            s[st][r] = x;
-            mx = fmaxf(mx, x);
-          }
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, -s[st][r]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // nothing visible yet
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
-      m_run = m_new;
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * fabsf(p.scale_log2);
+      // m_run is the running row max (scaled, log2 units); O and l are
+      // rescaled only when it grows
+      float corr = 1.0f;
+      if (mx > m_run) {
+        corr = __builtin_amdgcn_exp2f(m_run - mx);  // 0 when nothing was visible yet
+        m_run = mx;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;  // nothing visible yet
+      const float sc = p.scale_log2;
       // P as the B operand of O^T += V^T P^T: k-step t (16 keys) takes
       // accumulators 8 (t % 2) .. 8 (t % 2) + 7 of tile t / 2
       vec pk[KT / 16];
@@ -264,7 +277,7 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
         f32x8 pf;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          pf[i] = __builtin_amdgcn_exp2f(s[t >> 1][8 * (t & 1) + i] - m_use);
+          pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t >> 1][8 * (t & 1) + i], sc, -m_use));
           rs += pf[i];
         }
         pk[t] = __builtin_convertvector(pf, vec);
