@@ -363,6 +363,9 @@ constexpr size_t LDS_BYTES =
 constexpr int GROUP_M = 4;
 // int8 B: 64-byte rows (4 chunks of 16 B), 16 rows per 1 KiB wave load
 constexpr int CH8 = 4, RPK8 = 16, NQB8 = BN / RPK8 / NW, TB8 = BN * BK / 2;  // TB8 in 16-bit units
+// int8 B adds a bf16 copy of each stage's W rows: 160 KiB in all
+constexpr size_t LDS_BYTES8 = (size_t)STAGES * (TA + TB8) * 2 + (size_t)STAGES * TB * 2;
+static_assert(LDS_BYTES8 <= 160 * 1024 && LDS_BYTES8 >= (size_t)NW * TM * EP * 2, "int8 LDS");
 }  // namespace dl
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -465,14 +468,11 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
                                        (lds_void_t*)(bs + (wave * NQB + q) * 512), 16, 0, 0);
   };
   // fragment read offsets: lane supplies row l % 32, k chunk 2 s + l / 32
-  int roff[KS], roffb[KS];
+  int roff[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     roff[s] = (lane & 31) * BK + dl_swz(lane & 31, 2 * s + (lane >> 5)) * 8;
-    // int8 B: byte offset of k 16 s + 8 (lane / 32) .. + 8 in 64-byte rows
-    roffb[s] = (lane & 31) * BK + dl_swz64(lane & 31, s) * 16 + 8 * (lane >> 5);
   }
-  (void)roffb;
 
   // acc[j][i] = D^T tile (n rows j, m cols i): B fragments are the MFMA's A
   // operand, so a lane ends up owning one output row m and 4 runs of 4 n
@@ -487,9 +487,10 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) af[buf][i] = *(const vec*)(as + i * 32 * BK);
     if constexpr (B_INT8) {
-      const char* bs = (const char*)(smem + st * (TA + TB) + TA) + wn * TN * BK + roffb[s];
+      // the bf16 copy of the stage's W rows (converted once per block)
+      const uint16_t* bs = smem + STAGES * (TA + TB) + st * dl::TB + wn * TN * BK + roff[s];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bfr[buf][j] = widen8<T>(*(const u32x2_t*)(bs + j * 32 * BK));
+      for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * 32 * BK);
     } else {
       const uint16_t* bs = smem + st * (TA + TB) + TA + wn * TN * BK + roff[s];
 #pragma unroll
@@ -501,6 +502,25 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int i = 0; i < FM; ++i) acc[j][i] = MfmaOp<T>::mma(bfr[buf][j], af[buf][i], acc[j][i]);
+  };
+  // int8 W: wave w copied rows 32 w .. 32 w + 31 of every stage itself, so
+  // once its own loads have landed it widens exactly those rows into the
+  // stage's bf16 copy (same chunk swizzle as a 16-bit B tile); the barrier
+  // that follows publishes them.  Lane: row 32 w + l / 2, k half l % 2.
+  auto convert = [&](int st) __attribute__((always_inline)) {
+    if constexpr (B_INT8) {
+      const char* b8 = (const char*)(smem + st * (TA + TB) + TA);
+      uint16_t* bb = smem + STAGES * (TA + TB) + st * dl::TB;
+      const int r = wave * 32 + (lane >> 1), h = lane & 1;
+      const u32x4_t c0 = *(const u32x4_t*)(b8 + r * 64 + dl_swz64(r, 2 * h) * 16);
+      const u32x4_t c1 = *(const u32x4_t*)(b8 + r * 64 + dl_swz64(r, 2 * h + 1) * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4_t& c = j < 2 ? c0 : c1;
+        const u32x2_t w = {c[2 * (j & 1)], c[2 * (j & 1) + 1]};
+        *(vec*)(bb + r * BK + dl_swz(r, 4 * h + j) * 8) = widen8<T>(w);
+      }
+    }
   };
   constexpr int NMF = FM * FN, NDS = FM + FN;
   // one K step over stage st.  ISSUE: refill stage st with step kt + STAGES;
@@ -525,6 +545,7 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
           // are done reading stage st
           if (ISSUE) wait_vmcnt<(STAGES - 2) * LPS>();
           else wait_vmcnt<0>();
+          convert(st + 1 == STAGES ? 0 : st + 1);
           __syncthreads();
           if (ISSUE) issue(st, (kt + STAGES) * BK);
           read_frags(st + 1 == STAGES ? 0 : st + 1, 0, buf ^ 1);
@@ -547,6 +568,7 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
     if (s < KT) issue(s, s * BK);
   if (STAGES <= KT) wait_vmcnt<(STAGES - 1) * LPS>();
   else wait_vmcnt<0>();
+  convert(0);
   __syncthreads();
   read_frags(0, 0, 0);
   int st = 0, kt = 0;
@@ -1099,9 +1121,10 @@ bool dl_eligible(const GemmArgs& q, bool int8) {
 
 template <typename T, bool HB, bool I8>
 mi_status_t launch_dl(const GemmArgs& q0, int64_t batch, hipStream_t s, const char* what) {
+  constexpr size_t lds = I8 ? dl::LDS_BYTES8 : dl::LDS_BYTES;
   static bool attr = [] {
     (void)hipFuncSetAttribute((const void*)gemm_dl_kernel<T, HB, I8>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)dl::LDS_BYTES);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     return true;
   }();
   (void)attr;
@@ -1109,7 +1132,7 @@ mi_status_t launch_dl(const GemmArgs& q0, int64_t batch, hipStream_t s, const ch
   q.tiles_m = (int)((q.M + dl::BM - 1) / dl::BM);
   q.tiles_n = (int)((q.N + dl::BN - 1) / dl::BN);
   dim3 grid((unsigned)(q.tiles_m * q.tiles_n), (unsigned)batch);
-  hipLaunchKernelGGL((gemm_dl_kernel<T, HB, I8>), grid, dim3(dl::NT), dl::LDS_BYTES, s, q);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, HB, I8>), grid, dim3(dl::NT), lds, s, q);
   return check_launch(what);
 }
 
@@ -1121,6 +1144,10 @@ mi_status_t launch_mfma(const GemmArgs& q, int64_t batch, hipStream_t s, const c
   if (big >= cus) return Cfg<T, 256, 256, 2, 4, I8, HB>::launch(q, batch, s, what);
   if (q.M <= 32) return Cfg<T, 32, 64, 1, 2, I8, HB>::launch(q, batch, s, what);
   const int64_t mid = ((q.M + 127) / 128) * ((q.N + 127) / 128) * batch;
+  // int8 B (config 4's M = 256: 172 tiles of 128 x 128) runs 128 x 64 tiles:
+  // twice the blocks, so CUs hold two and overlap one's loads with the
+  // other's MFMAs (about 15 % faster)
+  if (mid >= cus / 2 && I8) return Cfg<T, 128, 64, 2, 2, I8, HB>::launch(q, batch, s, what);
   if (mid >= cus / 2) return Cfg<T, 128, 128, 2, 2, I8, HB>::launch(q, batch, s, what);
   return Cfg<T, 128, 64, 2, 2, I8, HB>::launch(q, batch, s, what);
 }
