@@ -269,6 +269,16 @@ def gemm_ops(torch, _abi):
                             lambda s: _abi.int8_linear(o, x, s["w"], scales), alg,
                             iters=20 if M < 4096 else 10, flops=2 * M * N * K,
                             bound="hbm" if M == 16 else "mfma"))
+    del W
+    # addmv (the GEMV behind mv / matmul(2-D, 1-D)): bf16 [11008, 4096] x [4096]
+    # plus a [11008] bias, eight matrices rotated (360 MiB, past the MALL)
+    mats = [(torch.randn(N, K, generator=gen) * 0.02).bfloat16().cuda() for _ in range(8)]
+    vec = torch.randn(K, generator=gen).bfloat16().cuda()
+    vb = torch.randn(N, generator=gen).bfloat16().cuda()
+    vo = torch.empty(N, dtype=torch.bfloat16, device="cuda")
+    res.append(bench_op(torch, "f2.addmv bf16 [11008,4096] x [4096]", [{"m": m} for m in mats],
+                        lambda s: _abi.addmv(vo, vb, s["m"], vec), N * K * 2 + K * 2 + 2 * N * 2,
+                        iters=40, flops=2 * N * K, bound="hbm"))
     return res
 
 

@@ -210,6 +210,15 @@ mi_status_t mi_addmm(const mi_tensor_t* out, const mi_tensor_t* self,
 /* out = self @ mat2, [M, K] x [K, N]. */
 mi_status_t mi_mm(const mi_tensor_t* out, const mi_tensor_t* self,
                   const mi_tensor_t* mat2, mi_stream_t stream);
+/* out = beta * self + alpha * (mat @ vec); mat [M, K], vec [K], out [M]
+ * (all one dtype: bf16, fp16 or fp32, fp32 accumulation, one rounding);
+ * self is 0-D or [M] (the output's dtype or fp32) and is ignored when
+ * beta == 0; mat and vec are ignored when alpha == 0.  Replaces
+ * topsatenAddmv (addmv.out, codegen/gcu_native_functions.yaml:206); mv is
+ * addmv with beta = 0. */
+mi_status_t mi_addmv(const mi_tensor_t* out, const mi_tensor_t* self,
+                     const mi_tensor_t* mat, const mi_tensor_t* vec,
+                     double beta, double alpha, mi_stream_t stream);
 /* out[b] = self[b] @ mat2[b], [B, M, K] x [B, K, N]. */
 mi_status_t mi_bmm(const mi_tensor_t* out, const mi_tensor_t* self,
                    const mi_tensor_t* mat2, mi_stream_t stream);

@@ -138,6 +138,19 @@ def addmm(bias, a, b, beta=1.0, alpha=1.0):
     return out.to(a.dtype)
 
 
+def addmv(bias, mat, vec, beta=1.0, alpha=1.0):
+    """aten::addmv.out -> topsatenAddmv (yaml :206): CPU ATen's addmv (the
+    reference's fallback path), fp32 for bf16/fp16 inputs then one cast, as
+    its bf16 gemv accumulates in fp32.  bias None means beta = 0 (mv).
+    Pinned by a float64 numpy product, alpha = 0 and beta = 0 ignoring NaN
+    operands, and mv == addmv with beta = 0."""
+    lowp = mat.dtype in (torch.bfloat16, torch.float16)
+    m, v = (mat.float(), vec.float()) if lowp else (mat, vec)
+    b = torch.zeros(mat.shape[0], dtype=m.dtype) if bias is None else bias.to(m.dtype)
+    out = torch.addmv(b, m, v, beta=beta if bias is not None else 0.0, alpha=alpha)
+    return out.to(mat.dtype)
+
+
 def bmm(a, b):
     """aten::bmm.out -> topsatenBmm (yaml :260), fp32 closed form."""
     return torch.bmm(a.float(), b.float()).to(a.dtype)

@@ -242,3 +242,144 @@ def test_int8_linear_large_tile_path(dtype, bias):
     out = torch.empty(M, N, dtype=dtype, device="cuda")
     _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda(), None if b is None else b.cuda())
     assert_close(out, aten.int8_linear(x, w, scales, b), "bf16", f"int8 large tile {dtype} {bias}")
+
+
+# ---- addmv (GEMV) and the linear / matmul override ---------------------------------
+
+def _kind(dtype):
+    return "fp32" if dtype == torch.float32 else "bf16"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("M,K", [(11008, 4096), (1000, 37), (1, 4096), (77, 1), (300, 520)])
+@pytest.mark.parametrize("layout", ["rows", "transposed", "sliced"])
+def test_addmv_parity(dtype, M, K, layout):
+    """mat K-contiguous (the kernel's own layout), a transposed view and a
+    column slice (row stride that breaks 16-byte alignment: both copied
+    densely first); bias [M], beta and alpha not 1."""
+    if layout == "rows":
+        mat = rn((M, K), 30, dtype, 1.0)
+    elif layout == "transposed":
+        mat = rn((K, M), 30, dtype, 1.0).t()
+    else:
+        mat = rn((M, K + 3), 30, dtype, 1.0)[:, 1:K + 1]
+    vec = rn((K,), 31, dtype, 1.0)
+    bias = rn((M,), 32, dtype, 1.0)
+    ref = aten.addmv(bias, mat, vec, beta=0.5, alpha=2.0)
+    md = mat.cuda() if layout == "rows" else (
+        mat.t().contiguous().cuda().t() if layout == "transposed" else
+        rn((M, K + 3), 30, dtype, 1.0).cuda()[:, 1:K + 1])
+    out = torch.empty(M, dtype=dtype, device="cuda")
+    _abi.addmv(out, bias.cuda(), md, vec.cuda(), beta=0.5, alpha=2.0)
+    assert_close(out, ref, _kind(dtype), f"addmv {dtype} {M}x{K} {layout}")
+
+
+def test_addmv_edges():
+    """Strided vec, scalar and fp32 bias, beta = 0 with a NaN bias, alpha = 0
+    with NaN in mat, K = 0, a strided output."""
+    M, K = 513, 300
+    mat, v2 = rn((M, K), 33, torch.bfloat16, 1.0), rn((2 * K,), 34, torch.bfloat16, 1.0)
+    vec = v2[::2]
+    out = torch.empty(M, dtype=torch.bfloat16, device="cuda")
+    _abi.addmv(out, torch.tensor([0.25], dtype=torch.bfloat16).cuda(), mat.cuda(), v2.cuda()[::2])
+    assert_close(out, aten.addmv(torch.full((M,), 0.25).bfloat16(), mat, vec), "bf16", "strided vec")
+    b32 = torch.randn(M, generator=g(35))
+    _abi.addmv(out, b32.cuda(), mat.cuda(), vec.contiguous().cuda(), beta=1.0, alpha=0.5)
+    assert_close(out, aten.addmv(b32, mat.float(), vec.float(), alpha=0.5).bfloat16(), "bf16",
+                 "fp32 bias")
+    nanb = torch.full((M,), float("nan"), dtype=torch.bfloat16)
+    _abi.addmv(out, nanb.cuda(), mat.cuda(), vec.contiguous().cuda(), beta=0.0)
+    assert torch.isfinite(out.float()).all()
+    nm = mat.clone()
+    nm[7, 11] = float("nan")
+    bias = rn((M,), 36, torch.bfloat16, 1.0)
+    _abi.addmv(out, bias.cuda(), nm.cuda(), vec.contiguous().cuda(), beta=1.0, alpha=0.0)
+    assert torch.equal(out.cpu(), bias)
+    e = torch.empty(M, 0, dtype=torch.bfloat16, device="cuda")
+    _abi.addmv(out, bias.cuda(), e, torch.empty(0, dtype=torch.bfloat16, device="cuda"), beta=2.0)
+    assert_close(out, (2.0 * bias.float()).bfloat16(), "bf16", "K = 0")
+    wide = torch.zeros(2 * M, dtype=torch.bfloat16, device="cuda")
+    _abi.addmv(wide[::2], None, mat.cuda(), vec.contiguous().cuda(), beta=0.0)
+    assert_close(wide[::2], aten.addmv(None, mat, vec), "bf16", "strided out")
+    assert torch.count_nonzero(wide[1::2].float()) == 0
+
+
+def test_mv_and_matmul_on_gcu_run_native_addmv():
+    """torch.mv / torch.addmv / matmul(2-D, 1-D) on gcu tensors reach the
+    native addmv (no CPU fallback counted)."""
+    import torch_gcu
+
+    mat = rn((640, 256), 37, torch.bfloat16, 1.0)
+    vec = rn((256,), 38, torch.bfloat16, 1.0)
+    bias = rn((640,), 39, torch.bfloat16, 1.0)
+    torch_gcu._C._set_op_debug_config("op_statistics=true")
+    torch_gcu._C._clear_op_statistics()
+    try:
+        mg, vg, bg = mat.to("gcu"), vec.to("gcu"), bias.to("gcu")
+        r1 = torch.mv(mg, vg)
+        r2 = torch.addmv(bg, mg, vg, beta=0.5, alpha=1.5)
+        r3 = mg @ vg
+        stats = torch_gcu._C._op_statistics()
+    finally:
+        torch_gcu._C._set_op_debug_config("")
+    ref = aten.addmv(None, mat, vec)
+    assert_close(r1.cpu(), ref, "bf16", "mv")
+    assert_close(r3.cpu(), ref, "bf16", "matmul 2-D x 1-D")
+    assert_close(r2.cpu(), aten.addmv(bias, mat, vec, beta=0.5, alpha=1.5), "bf16", "addmv")
+    native = {k: v for k, v in stats.items() if k.startswith("addmv")}
+    assert sum(v[0] for v in native.values()) >= 3, stats
+    assert all(v[1] == 0 for v in native.values()), stats
+
+
+_OVERRIDE_SCRIPT = r"""
+import sys, torch, torch.nn.functional as F
+import torch_gcu
+from oracle import aten
+from oracle.tolerance import assert_close
+names = ("aten::linear", "aten::linear.out", "aten::matmul", "aten::matmul.out")
+assert all(torch._C._dispatch_has_kernel_for_dispatch_key(n, "PrivateUse1") for n in names)
+g = torch.Generator().manual_seed(40)
+x3 = torch.randn(4, 96, 256, generator=g).bfloat16()
+w = (torch.randn(384, 256, generator=g) * 0.05).bfloat16()
+b = torch.randn(384, generator=g).bfloat16()
+torch_gcu._C._set_op_debug_config("op_statistics=true")
+torch_gcu._C._clear_op_statistics()
+y = F.linear(x3.to("gcu"), w.to("gcu"), b.to("gcu"))
+y2 = F.linear(x3[:, ::2].to("gcu"), w.to("gcu"))            # strided input, no bias
+m = torch.matmul(x3.to("gcu"), w.t().to("gcu"))              # 3-D x 2-D: folded to mm
+mv = torch.matmul(w.to("gcu"), x3[0, 0].to("gcu"))           # 2-D x 1-D: mv
+bm = torch.matmul(x3.to("gcu"), x3.transpose(1, 2).contiguous().to("gcu"))  # batched
+out = torch.empty(0, dtype=torch.bfloat16, device="gcu")
+torch.matmul(x3[0].to("gcu"), w.t().to("gcu"), out=out)
+stats = torch_gcu._C._op_statistics()
+torch_gcu._C._set_op_debug_config("")
+ref = (x3.float() @ w.float().t() + b.float()).bfloat16()
+assert_close(y.cpu(), ref, "bf16", "linear 3-D + bias")
+assert_close(y2.cpu(), (x3[:, ::2].float() @ w.float().t()).bfloat16(), "bf16", "linear strided")
+assert_close(m.cpu(), (x3.float() @ w.float().t()).bfloat16(), "bf16", "matmul 3-D x 2-D")
+assert_close(mv.cpu(), aten.addmv(None, w, x3[0, 0]), "bf16", "matmul 2-D x 1-D")
+assert_close(bm.cpu(), aten.bmm(x3, x3.transpose(1, 2).contiguous()), "bf16", "matmul batched")
+assert_close(out.cpu(), (x3[0].float() @ w.float().t()).bfloat16(), "bf16", "matmul.out")
+assert stats.get("linear", (0, 0))[0] == 2, stats
+assert stats.get("matmul", (0, 0))[0] == 3 and stats.get("matmul.out", (0, 0))[0] == 1, stats
+assert all(v[1] == 0 for k, v in stats.items()), stats   # nothing fell back to CPU
+print("override ok")
+"""
+
+
+def test_linear_matmul_override_on_gpu():
+    """With ENFLAME_PT_ENABLE_LINEAR_OVERRIDE=true (read at library load, so
+    in a child process), linear and matmul on gcu run the native folding
+    onto mm / addmm / bmm / addmv and match CPU ATen."""
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, ENFLAME_PT_ENABLE_LINEAR_OVERRIDE="true")
+    env["PYTHONPATH"] = os.pathsep.join([os.path.join(repo, "torch-gcu_amd"), repo,
+                                         env.get("PYTHONPATH", "")])
+    r = subprocess.run([sys.executable, "-c", _OVERRIDE_SCRIPT], env=env, capture_output=True,
+                       text=True, timeout=110)
+    assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-3000:])
+    assert "override ok" in r.stdout

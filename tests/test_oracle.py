@@ -154,6 +154,25 @@ def test_addmm_bmm_vs_float64():
     assert_exact(aten.addmm(None, a[5:9], b), aten.addmm(None, a, b)[5:9], "addmm rows")
 
 
+def test_addmv_vs_float64_and_ignored_operands():
+    mat = torch.randn(70, 300, generator=g(90)).bfloat16()
+    vec = torch.randn(300, generator=g(91)).bfloat16()
+    bias = torch.randn(70, generator=g(92)).bfloat16()
+    ref = npr.matmul64(mat.float().numpy(), vec.double().numpy()[:, None])[:, 0] * 0.5 \
+        + 2.0 * bias.double().numpy()
+    assert_close(aten.addmv(bias, mat, vec, beta=2.0, alpha=0.5), torch.from_numpy(ref).bfloat16(),
+                 "bf16", "addmv")
+    m32, v32 = mat.float(), vec.float()
+    ref32 = npr.matmul64(m32.numpy(), v32.double().numpy()[:, None])[:, 0]
+    assert_close(aten.addmv(None, m32, v32), torch.from_numpy(ref32).float(), "fp32", "mv")
+    # beta = 0 ignores a NaN bias; alpha = 0 ignores NaN in mat
+    nan_b = torch.full((70,), float("nan")).bfloat16()
+    assert torch.isfinite(aten.addmv(nan_b, mat, vec, beta=0.0).float()).all()
+    nan_m = mat.clone()
+    nan_m[3, 7] = float("nan")
+    assert_exact(aten.addmv(bias, nan_m, vec, beta=1.0, alpha=0.0), bias, "addmv alpha 0")
+
+
 def test_int8_linear_vs_float64_and_weight_int8pack_mm():
     x = torch.randn(16, 128, generator=g(25)).bfloat16()
     w = torch.randint(-128, 128, (64, 128), generator=g(26), dtype=torch.int8)

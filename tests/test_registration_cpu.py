@@ -28,7 +28,32 @@ def test_every_yaml_op_has_a_schema_and_a_kernel():
         assert e.name in schemas, e.name
         name, _, overload = e.name.partition(".")
         full = f"aten::{name}" + (f".{overload}" if overload else "")
-        assert torch._C._dispatch_has_kernel_for_dispatch_key(full, "PrivateUse1"), full
+        want = e.env_gate is None or os.environ.get(e.env_gate, "").strip().lower() == "true"
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(full, "PrivateUse1") == want, full
+
+
+@pytest.mark.parametrize("value,registered", [("true", True), (" TRUE ", True), ("false", False),
+                                              ("1", False), (None, False)])
+def test_linear_override_is_env_gated(value, registered):
+    """linear / matmul (and their .out forms) are registered on PrivateUse1
+    only when ENFLAME_PT_ENABLE_LINEAR_OVERRIDE reads "true" at library load,
+    as the reference's RegisterLinearOverrideGCU.cpp:575-590 does."""
+    import subprocess
+
+    env = dict(os.environ)
+    env.pop("ENFLAME_PT_ENABLE_LINEAR_OVERRIDE", None)
+    if value is not None:
+        env["ENFLAME_PT_ENABLE_LINEAR_OVERRIDE"] = value
+    code = ("import torch, torch_gcu\n"
+            "print([torch._C._dispatch_has_kernel_for_dispatch_key(o, 'PrivateUse1') for o in "
+            "('aten::linear', 'aten::linear.out', 'aten::matmul', 'aten::matmul.out', 'aten::addmv')])")
+    env["PYTHONPATH"] = os.pathsep.join([os.path.join(REPO, "torch-gcu_amd"), REPO,
+                                         env.get("PYTHONPATH", "")])
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    flags = eval(r.stdout.strip().splitlines()[-1])
+    assert flags == [registered] * 4 + [True], flags
 
 
 def test_generated_sources_are_deterministic():
@@ -39,6 +64,8 @@ def test_generated_sources_are_deterministic():
             assert open(os.path.join(d1, f)).read() == open(os.path.join(d2, f)).read()
         src = open(os.path.join(d1, "RegisterGCU.cpp")).read()
         assert 'm.impl("add.out", TORCH_FN(wrapper_PrivateUse1_add_out));' in src
+        assert ('if (torch_gcu::env_true("ENFLAME_PT_ENABLE_LINEAR_OVERRIDE")) '
+                'm.impl("linear", TORCH_FN(wrapper_PrivateUse1_linear));') in src
         # factory ops guard on their device argument, compute ops on a tensor
         assert "const c10::OptionalDeviceGuard device_guard(device);" in src
         assert "call_fallback_fn<&torch_gcu::gcu_cpu_fallback, ATEN_OP2(mul, Tensor)>" in src

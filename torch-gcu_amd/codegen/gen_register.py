@@ -36,6 +36,7 @@ class OpEntry:
     device_guard: bool = True
     fallback_cpu: bool = True
     op_check: bool = True
+    env_gate: str | None = None  # registered only when this variable reads "true"
 
 
 def load_entries(path: str | None = None) -> list[OpEntry]:
@@ -48,7 +49,8 @@ def load_entries(path: str | None = None) -> list[OpEntry]:
         out.append(OpEntry(name=e["name"], device_check=e.get("device_check", True),
                            device_guard=e.get("device_guard", True),
                            fallback_cpu=e.get("fallback_cpu", True),
-                           op_check=e.get("op_check", True)))
+                           op_check=e.get("op_check", True),
+                           env_gate=e.get("env_gate")))
     names = [e.name for e in out]
     dup = {n for n in names if names.count(n) > 1}
     assert not dup, f"duplicate ops in {path}: {sorted(dup)}"
@@ -198,7 +200,11 @@ def generate(out_dir: str) -> list[str]:
             body.append("  torch_gcu::after_op();")
             body.append("  return r_;")
         wrappers.append(f"{ret} wrapper_PrivateUse1_{fn}({decl_args}) {{\n" + "\n".join(body) + "\n}\n")
-        regs.append(f"  m.impl(\"{e.name}\", TORCH_FN(wrapper_PrivateUse1_{fn}));")
+        reg = f"m.impl(\"{e.name}\", TORCH_FN(wrapper_PrivateUse1_{fn}));"
+        if e.env_gate:
+            regs.append(f"  if (torch_gcu::env_true(\"{e.env_gate}\")) {reg}")
+        else:
+            regs.append(f"  {reg}")
 
     header_text = (
         "// Generated by codegen/gen_register.py from codegen/gcu_native_functions.yaml.\n"

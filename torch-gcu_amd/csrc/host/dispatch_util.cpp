@@ -2,6 +2,10 @@
 
 #include <c10/util/Exception.h>
 
+#include <cctype>
+#include <cstdlib>
+#include <string>
+
 namespace torch_gcu {
 
 namespace {
@@ -19,6 +23,16 @@ OpCheckScope::~OpCheckScope() { --tls_op_check_depth; }
 
 void after_op() {
   if (C10_UNLIKELY(OpDebugConfig::get().op_sync_mode)) maybe_sync_after_op(current_hip_stream());
+}
+
+bool env_true(const char* name) {
+  const char* e = std::getenv(name);
+  if (e == nullptr) return false;
+  std::string v(e);
+  const auto b = v.find_first_not_of(' '), en = v.find_last_not_of(' ');
+  v = b == std::string::npos ? std::string() : v.substr(b, en - b + 1);
+  for (auto& c : v) c = (char)std::tolower((unsigned char)c);
+  return v == "true";
 }
 
 mi_tensor_t desc(const at::Tensor& t) {

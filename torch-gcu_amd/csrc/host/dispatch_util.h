@@ -54,6 +54,11 @@ struct OpCheckScope {
 // Per-op epilogue: op_sync_mode synchronisation.
 void after_op();
 
+// True when environment variable `name` reads "true" (case-insensitive,
+// surrounding spaces ignored), the way the reference reads
+// ENFLAME_PT_ENABLE_LINEAR_OVERRIDE (RegisterLinearOverrideGCU.cpp:575-583).
+bool env_true(const char* name);
+
 // ---- kernel-library bridge (replaces createTopsatenTensor and
 // CHECK_TOPSATEN_CALL, torch_gcu/csrc/gcu/gcu_utils.cpp:64-108) -------------
 

@@ -1,6 +1,7 @@
-// Native kernels for the dense contractions: mm, addmm, bmm, baddbmm
+// Native kernels for the dense contractions: mm, addmm, bmm, baddbmm, addmv
 // (codegen/gcu_native_functions.yaml mm.out :452, addmm.out :205, bmm.out
-// :260, baddbmm.out :238; shape rules of shape_inference/blas.cpp).  bf16 /
+// :260, baddbmm.out :238, addmv.out :206; shape rules of
+// shape_inference/blas.cpp).  bf16 /
 // fp16 run on the MFMA kernel, fp32 on the VALU kernel; other dtypes take the
 // CPU fallback as every unregistered op does.
 #include <ATen/ExpandUtils.h>
@@ -135,6 +136,47 @@ at::Tensor baddbmm(const at::Tensor& self, const at::Tensor& batch1, const at::T
                    const at::Scalar& beta, const at::Scalar& alpha) {
   at::Tensor out = at::empty({0}, batch1.options());
   return baddbmm_out(self, batch1, batch2, beta, alpha, out);
+}
+
+// ---- addmv (addmv.out, codegen/gcu_native_functions.yaml:206); mv reaches it
+// through ATen's composite mv -> addmv_ ------------------------------------------
+
+at::Tensor& addmv_out(const at::Tensor& self, const at::Tensor& mat, const at::Tensor& vec,
+                      const at::Scalar& beta, const at::Scalar& alpha, at::Tensor& out) {
+  TORCH_CHECK(mat.dim() == 2 && vec.dim() == 1 && self.dim() <= 1,
+              "vector + matrix @ vector expected, got ", self.dim(), ", ", mat.dim(), ", ",
+              vec.dim());
+  TORCH_CHECK(mat.size(1) == vec.size(0) && (mat.size(0) == self.numel() || self.numel() == 1),
+              "size mismatch, got input (", self.dim() == 0 ? 1 : self.size(0), "), mat (",
+              mat.size(0), "x", mat.size(1), "), vec (", vec.size(0), ")");
+  check_same_dtype(mat, vec, "addmv");
+  if (!native_dtype(mat.scalar_type()))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP2(addmv, out)>::call(
+        self, mat, vec, beta, alpha, out);
+  at::native::resize_output(out, {mat.size(0)});
+  if (out.numel() == 0) return out;
+  at::Tensor bias = self.device().is_cpu() ? self.to(out.device()) : self;
+  if (bias.scalar_type() != out.scalar_type() && bias.scalar_type() != at::kFloat)
+    bias = bias.to(out.scalar_type());
+  const mi_tensor_t o = desc(out), s = desc(bias), a = desc(mat), v = desc(vec);
+  check_mi(mi_addmv(&o, &s, &a, &v, beta.toDouble(), alpha.toDouble(), mi_stream(out)), "addmv");
+  return out;
+}
+
+at::Tensor addmv(const at::Tensor& self, const at::Tensor& mat, const at::Tensor& vec,
+                 const at::Scalar& beta, const at::Scalar& alpha) {
+  at::Tensor out = at::empty({0}, vec.options());
+  return addmv_out(self, mat, vec, beta, alpha, out);
+}
+
+at::Tensor& addmv_(at::Tensor& self, const at::Tensor& mat, const at::Tensor& vec,
+                   const at::Scalar& beta, const at::Scalar& alpha) {
+  TORCH_CHECK(self.dim() == 1 && self.size(0) == mat.size(0),
+              "addmv_: self must have the output's shape");
+  // self is both bias and output: compute into a temporary, then copy
+  at::Tensor tmp = aotops::addmv(self, mat, vec, beta, alpha);
+  self.copy_(tmp);
+  return self;
 }
 
 }  // namespace aotops

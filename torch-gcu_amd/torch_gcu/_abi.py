@@ -86,6 +86,7 @@ _SIGNATURES = {
     "mi_rope": ([_T, _T, _T, _T, _T, ctypes.c_double, _S], ctypes.c_int),
     "mi_silu_mul": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_addmm": ([_T, _T, _T, _T, ctypes.c_double, ctypes.c_double, _S], ctypes.c_int),
+    "mi_addmv": ([_T, _T, _T, _T, ctypes.c_double, ctypes.c_double, _S], ctypes.c_int),
     "mi_mm": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_bmm": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_baddbmm": ([_T, _T, _T, _T, ctypes.c_double, ctypes.c_double, _S], ctypes.c_int),
@@ -284,6 +285,12 @@ def silu_mul(out, gate, up):
 
 def addmm(out, bias, a, b, beta=1.0, alpha=1.0):
     check("mi_addmm", lib().mi_addmm(desc(out), desc(bias), desc(a), desc(b), beta, alpha,
+                                     stream_of(out)))
+    return out
+
+
+def addmv(out, bias, mat, vec, beta=1.0, alpha=1.0):
+    check("mi_addmv", lib().mi_addmv(desc(out), desc(bias), desc(mat), desc(vec), beta, alpha,
                                      stream_of(out)))
     return out
 
