@@ -34,6 +34,8 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "torch-gcu_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# PCIe 5.0 x16 (32 GT/s x 16 lanes, 128b/130b): the MI355X host link, per direction
+PCIE5_X16_GBS = 63.0
 CAL_COPY_BYTES = 512 * 2**20
 METRIC = "HBM GB/s (elementwise/norm), MFMA TFLOPS (addmm/int8), decoder-layer tok/s"
 
@@ -319,8 +321,75 @@ def other_ops(torch, _abi, synthetic):
                         lambda s: _abi.silu_mul(s["o"], s["g"], s["u"]), 1082130432))
     del gs, gt, up, c3
     res.extend(gemm_ops(torch, _abi))
+    res.extend(transfer_ops(torch, _abi))
     res.extend(attention_ops(torch, _abi))
     res.extend(decoder_ops(torch))
+    return res
+
+
+def transfer_ops(torch, _abi):
+    """The copy and transfer step around the ops: cat (a KV-cache append and
+    the rotate-half halves), a dtype-cast and a transposing device copy, and
+    host <-> device copies through the gcu device from pinned (caching host
+    allocator) and pageable memory."""
+    res = []
+    log("bench: copy and transfer")
+    gen = torch.Generator().manual_seed(20261207)
+    B, H, S, D = 8, 32, 2048, 128
+    kv = [[torch.randn(B, H, S, D, generator=gen).bfloat16().cuda() for _ in range(2)]
+          for _ in range(2)]
+    out = torch.empty(B, H, 2 * S, D, dtype=torch.bfloat16, device="cuda")
+    res.append(bench_op(torch, "f3.cat bf16 2x[8,32,2048,128] dim 2", [{"x": x} for x in kv],
+                        lambda s: _abi.cat(out, s["x"], 2), 2 * out.numel() * 2, iters=20))
+    del kv, out
+    halves = [[torch.randn(16384 * 32, 64, generator=gen).bfloat16().cuda() for _ in range(2)]
+              for _ in range(2)]
+    out = torch.empty(16384 * 32, 128, dtype=torch.bfloat16, device="cuda")
+    res.append(bench_op(torch, "f3.cat bf16 2x[524288,64] dim -1 (128-byte rows)",
+                        [{"x": x} for x in halves], lambda s: _abi.cat(out, s["x"], 1),
+                        2 * out.numel() * 2, iters=20))
+    del halves, out
+    n = 8192
+    src = [torch.randn(n, n, generator=gen).cuda() for _ in range(2)]
+    o16 = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
+    res.append(bench_op(torch, "f3.copy f32 -> bf16 [8192,8192]", [{"x": x} for x in src],
+                        lambda s: _abi.copy_(o16, s["x"]), n * n * 6, iters=20))
+    src16 = [x.bfloat16() for x in src]
+    del src
+    res.append(bench_op(torch, "f3.copy bf16 transpose [8192,8192]", [{"x": x.t()} for x in src16],
+                        lambda s: _abi.copy_(o16, s["x"]), n * n * 4, iters=20))
+    del src16, o16
+    res.extend(host_transfer_ops(torch))
+    return res
+
+
+def host_transfer_ops(torch, nbytes=256 << 20, iters=8):
+    """PCIe copies of 256 MiB through the gcu device: wall time per copy over
+    `iters` back-to-back copies (synchronised once), against the published
+    PCIe 5.0 x16 rate of the MI355X host link."""
+    import torch_gcu  # noqa: F401
+
+    res = []
+    n = nbytes // 4
+    d = torch.empty(n, device="gcu")
+    pinned = torch.randn(n).pin_memory()
+    pageable = torch.randn(n)
+    back = torch.empty(n, pin_memory=True)
+    cases = [("f3.h2d pinned non_blocking 256 MiB", lambda: d.copy_(pinned, non_blocking=True)),
+             ("f3.h2d pageable 256 MiB", lambda: d.copy_(pageable)),
+             ("f3.d2h pinned non_blocking 256 MiB", lambda: back.copy_(d, non_blocking=True))]
+    for name, fn in cases:
+        fn()
+        torch.gcu.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.gcu.synchronize()
+        sec = (time.perf_counter() - t0) / iters
+        gbs = nbytes / sec / 1e9
+        res.append({"op": name, "ms": round(sec * 1e3, 3), "GB/s": round(gbs, 1),
+                    "frac_pcie5_x16": round(gbs / PCIE5_X16_GBS, 4), "alg_bytes": nbytes})
+    assert torch.equal(back, pageable), "round trip through the device"
     return res
 
 

@@ -120,6 +120,16 @@ int32_t mi_device_cu_count(void);
 mi_status_t mi_copy(const mi_tensor_t* out, const mi_tensor_t* src,
                     mi_stream_t stream);
 
+/* out = cat(inputs[0..n_inputs), dim): every input has out's rank and sizes
+ * except along `dim`, where they add up to out's.  Dense inputs of out's
+ * dtype with a dense out take one batched-row-copy launch (32 inputs per
+ * launch); other layouts and dtype casts copy input by input (mi_copy).
+ * ATen's shape rules (the skipped legacy 1-D empty inputs, dtype promotion,
+ * memory format of out) are the host layer's.  Replaces topsatenCat
+ * (codegen/gcu_native_functions.yaml cat.out :263). */
+mi_status_t mi_cat(const mi_tensor_t* out, const mi_tensor_t* const* inputs,
+                   int32_t n_inputs, int32_t dim, mi_stream_t stream);
+
 /* out[...] = value.  Replaces topsatenFill_ (yaml fill_.Scalar :316). */
 mi_status_t mi_fill(const mi_tensor_t* out, mi_scalar_t value,
                     mi_stream_t stream);

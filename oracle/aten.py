@@ -47,6 +47,25 @@ def index_select(self: torch.Tensor, dim: int, index: torch.Tensor) -> torch.Ten
     return torch.index_select(self, dim, index)
 
 
+# ---- copy and transfer -----------------------------------------------------------
+
+def copy(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """aten::copy_ into a tensor shaped and typed like dst: src broadcast to
+    dst's shape and cast to its dtype (the reference's _copy_from,
+    torch_gcu/csrc/aten/aot_ops/gcu_copy.cpp:279-386, device side topsatenCopy
+    :116-150).  Pinned by numpy astype / broadcast_to (bit-exact)."""
+    out = torch.empty_like(dst)
+    out.copy_(src)
+    return out
+
+
+def cat(tensors, dim: int = 0) -> torch.Tensor:
+    """aten::cat.out -> topsatenCat (codegen/gcu_native_functions.yaml:263):
+    result_type promotion, legacy 1-D empty inputs skipped.  Pinned by
+    numpy.concatenate and a brute-force walk over output positions."""
+    return torch.cat(list(tensors), dim)
+
+
 # ---- config 2: reductions and softmax --------------------------------------
 
 def sum_(x: torch.Tensor, dim=None, keepdim=False, dtype=None) -> torch.Tensor:

@@ -42,6 +42,28 @@ def index_select_brute(table: np.ndarray, idx: np.ndarray) -> np.ndarray:
     return out
 
 
+def cat_brute(arrays, dim: int) -> np.ndarray:
+    """Concatenation by an explicit walk over output positions along dim (tiny
+    inputs only): position j of out comes from the input whose range holds j."""
+    nd = arrays[0].ndim
+    dim = dim % nd
+    total = sum(a.shape[dim] for a in arrays)
+    shape = list(arrays[0].shape)
+    shape[dim] = total
+    out = np.empty(shape, dtype=np.result_type(*arrays))
+    for j in range(total):
+        k, base = 0, 0
+        while j >= base + arrays[k].shape[dim]:
+            base += arrays[k].shape[dim]
+            k += 1
+        src = [slice(None)] * nd
+        dst = [slice(None)] * nd
+        src[dim] = j - base
+        dst[dim] = j
+        out[tuple(dst)] = arrays[k][tuple(src)]
+    return out
+
+
 def sum64(x, axis):
     return np.sum(np.asarray(x, dtype=np.float64), axis=axis)
 

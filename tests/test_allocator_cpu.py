@@ -157,3 +157,46 @@ def test_alloc_conf_parsing():
         except RuntimeError:
             pass
     """)
+
+
+def test_pinned_host_allocator_bookkeeping():
+    """The caching host allocator (torch_gcu/csrc/gcu/gcu_caching_host_allocator.cpp)
+    on ordinary host memory: pin_memory() / pin_memory=True come from it and
+    read back as pinned, freed blocks are reused by size class, a cached block
+    is taken only by a request of at most its class and no less than half of
+    it, slices of a block are pinned, and empty_cache releases what is cached."""
+    run("""
+    C._host_allocator_use_plain_memory()
+    hs = C._host_memory_stats
+    a = torch.empty(1000, pin_memory=True)          # 4000 B -> 4 KiB class
+    assert a.is_pinned() and a[500:].is_pinned()
+    assert hs()["num_host_alloc"] == 1 and hs()["reserved_bytes"] == 4096, hs()
+    pa = a.data_ptr()
+    del a
+    b = torch.empty(1024, pin_memory=True)           # same class: reused
+    assert b.data_ptr() == pa and hs()["num_cache_hits"] == 1, hs()
+    c = torch.empty(3000, pin_memory=True)           # 12000 B -> 16 KiB
+    assert hs()["reserved_bytes"] == 4096 + 16384 and hs()["allocated_bytes"] == 4096 + 16384
+    x = torch.randn(5, 7)
+    y = x.pin_memory()
+    assert y.is_pinned() and not x.is_pinned() and torch.equal(x, y)
+    assert not torch.randn(3).is_pinned()
+    del b, c, y
+    assert hs()["allocated_bytes"] == 0, hs()
+    # 100 MiB -> 2 MiB multiples above 64 MiB; a 40 MiB request (64 MiB class)
+    # may take it, a 20 MiB one (32 MiB class) may not
+    big = torch.empty(100 * MiB, dtype=torch.uint8, pin_memory=True)
+    pb = big.data_ptr()
+    assert hs()["reserved_bytes"] == 4096 + 16384 + 4096 + 100 * MiB, hs()
+    del big
+    s1 = torch.empty(20 * MiB, dtype=torch.uint8, pin_memory=True)
+    assert s1.data_ptr() != pb
+    s2 = torch.empty(40 * MiB, dtype=torch.uint8, pin_memory=True)
+    assert s2.data_ptr() == pb
+    del s1, s2
+    torch.gcu.host_empty_cache()
+    st = torch.gcu.host_memory_stats()
+    assert st["reserved_bytes"] == 0 and st["num_blocks"] == 0, st
+    assert st["num_host_free"] == st["num_host_alloc"], st
+    print("ok")
+    """)

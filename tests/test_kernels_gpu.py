@@ -524,3 +524,72 @@ def test_transpose_copy(dtype, shape):
     out = torch.empty(view.shape, dtype=dtype, device=DEV)
     _abi.copy_(out, _strided_on_device(view))
     assert_exact(out, view.contiguous(), f"transpose copy {shape}")
+
+
+# ---- cat ------------------------------------------------------------------------------
+
+_CAT_CASES = [
+    ([(4, 5, 8), (4, 3, 8), (4, 1, 8)], 1),      # 16-byte rows of several lengths
+    ([(7, 33), (7, 31)], 1),                      # odd row lengths: narrower words
+    ([(1000, 128), (24, 128)], 0),                # outer == 1: one run per input
+    ([(2, 8, 64, 64), (2, 8, 64, 64)], 3),        # halves of a head (rotate-half pattern)
+    ([(3, 4, 5)], 2),                             # one input
+    ([(0, 5), (3, 5), (0, 5)], 0),                # empty inputs
+    ([(2, 3)] * 40, 0),                           # more inputs than one launch takes
+    ([(5, 7, 3), (5, 1, 3), (5, 12, 3)], -2),     # negative dim
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.int64, torch.uint8])
+@pytest.mark.parametrize("shapes,dim", _CAT_CASES)
+def test_cat_parity(dtype, shapes, dim):
+    """mi_cat on dense inputs (the batched row copy) is bit-exact with CPU ATen's cat."""
+    xs = [rand(s, dtype, 50 + i) for i, s in enumerate(shapes)]
+    ref = aten.cat(xs, dim)
+    out = torch.empty(ref.shape, dtype=dtype, device=DEV)
+    _abi.cat(out, [dev(x) for x in xs], dim % ref.dim())
+    assert_exact(out, ref, f"cat {shapes} dim {dim}")
+
+
+def test_cat_layouts_casts_and_alignment():
+    """The other paths of mi_cat: channels-last inputs and out (row copy in
+    memory order), strided inputs and dtype casts (copy per input), inputs at
+    addresses that are not 16-byte aligned (byte words), a strided out."""
+    a = rand((2, 3, 5, 6), torch.bfloat16, 60).contiguous(memory_format=torch.channels_last)
+    b = rand((2, 4, 5, 6), torch.bfloat16, 61).contiguous(memory_format=torch.channels_last)
+    ref = aten.cat([a, b], 1)
+    out = torch.empty(ref.shape, dtype=torch.bfloat16, device=DEV).contiguous(
+        memory_format=torch.channels_last)
+    _abi.cat(out, [dev(a), dev(b)], 1)
+    assert_exact(out, ref, "channels-last")
+    # a transposed input and an int32 input cast into a float32 out
+    t = rand((6, 9), torch.float32, 62).t()
+    i = rand((4, 6), torch.int32, 63)
+    ref = aten.cat([t, i.float()], 0)
+    out = torch.empty(ref.shape, dtype=torch.float32, device=DEV)
+    _abi.cat(out, [_strided_on_device(t), dev(i)], 0)
+    assert_exact(out, ref, "strided + cast")
+    # uint8 inputs one byte off alignment
+    base = rand((1 + 5 * 17,), torch.uint8, 64)
+    x = base[1:].view(5, 17)
+    y = rand((5, 3), torch.uint8, 65)
+    ref = aten.cat([x, y], 1)
+    out = torch.empty(ref.shape, dtype=torch.uint8, device=DEV)
+    _abi.cat(out, [_strided_on_device(x), dev(y)], 1)
+    assert_exact(out, ref, "misaligned bytes")
+    # out is a column slice of a wider buffer
+    wide = torch.zeros(5, 30, dtype=torch.uint8, device=DEV)
+    _abi.cat(wide[:, 4:24], [_strided_on_device(x), dev(y)], 1)
+    assert_exact(wide[:, 4:24], ref, "strided out")
+    assert int(wide[:, :4].sum()) == 0 and int(wide[:, 24:].sum()) == 0
+
+
+def test_cat_rejects_bad_shapes():
+    x = dev(rand((4, 5), torch.float32, 66))
+    y = dev(rand((3, 5), torch.float32, 67))
+    with pytest.raises(_abi.MiError, match="size"):
+        _abi.cat(torch.empty(7, 6, device=DEV), [x, y], 0)
+    with pytest.raises(_abi.MiError, match="add up"):
+        _abi.cat(torch.empty(8, 5, device=DEV), [x, y], 0)
+    with pytest.raises(_abi.MiError, match="dims"):
+        _abi.cat(torch.empty(7, 5, device=DEV), [x, y[0]], 0)

@@ -55,6 +55,46 @@ def test_index_select_vs_numpy_and_brute_force():
                  torch.from_numpy(table.numpy()[:, [7, 1]]), "dim1")
 
 
+def test_cat_vs_numpy_and_brute_force():
+    a = torch.randint(-2**63, 2**63 - 1, (3, 5, 4), generator=g(40), dtype=torch.int64)
+    b = torch.randint(-2**63, 2**63 - 1, (3, 2, 4), generator=g(41), dtype=torch.int64)
+    c = torch.randint(-2**63, 2**63 - 1, (3, 7, 4), generator=g(42), dtype=torch.int64)
+    for dim in (1, -2):
+        got = aten.cat([a, b, c], dim)
+        assert_exact(got, torch.from_numpy(np.concatenate([a.numpy(), b.numpy(), c.numpy()], 1)),
+                     "concatenate")
+        assert_exact(got, torch.from_numpy(npr.cat_brute([a.numpy(), b.numpy(), c.numpy()], dim)),
+                     "brute")
+    x = torch.randn(4, 3, generator=g(43))
+    y = torch.randn(4, 5, generator=g(44))
+    assert_exact(aten.cat([x, y], 1), torch.from_numpy(npr.cat_brute([x.numpy(), y.numpy()], 1)),
+                 "last dim")
+    # legacy: a 1-D empty input is skipped whatever the rank of the others
+    assert_exact(aten.cat([x, torch.empty(0), x], 0), torch.from_numpy(np.concatenate([x.numpy()] * 2)),
+                 "skip 1-D empty")
+    # promotion: int32 with float32 gives float32 holding the converted ints
+    i = torch.arange(-6, 6, dtype=torch.int32).reshape(4, 3)
+    got = aten.cat([i, x], 0)
+    assert got.dtype == torch.float32
+    assert_exact(got, torch.from_numpy(np.concatenate([i.numpy().astype(np.float32), x.numpy()])),
+                 "promotion")
+
+
+def test_copy_casts_vs_numpy():
+    x = torch.randn(64, 33, generator=g(45)) * 300
+    for dt, npdt in [(torch.float16, np.float16), (torch.int32, np.int32), (torch.float64, np.float64),
+                     (torch.int8, None), (torch.bool, np.bool_)]:
+        got = aten.copy(torch.empty(64, 33, dtype=dt), x)
+        if npdt is None:  # float -> int8 goes through int64 in ATen (wraps)
+            want = x.numpy().astype(np.int64).astype(np.int8)
+        else:
+            want = x.numpy().astype(npdt)
+        assert_exact(got, torch.from_numpy(want), f"cast {dt}")
+    row = torch.randn(33, generator=g(46))
+    assert_exact(aten.copy(torch.empty(5, 33), row),
+                 torch.from_numpy(np.broadcast_to(row.numpy(), (5, 33)).copy()), "broadcast")
+
+
 # ---- config 2 -------------------------------------------------------------------
 
 def test_sum_amax_bf16_vs_float64():
@@ -246,3 +286,6 @@ def test_planted_mistakes_are_caught():
     unscaled = torch.softmax((q @ q.transpose(-1, -2)).masked_fill(
         torch.ones(16, 16, dtype=torch.bool).triu(1), float("-inf")), -1) @ q
     assert (unscaled.double() - torch.from_numpy(ro)).abs().max() > 1e-2  # dropped 1/sqrt(d)
+    p1, p2 = torch.arange(6).reshape(2, 3), torch.arange(6, 10).reshape(2, 2)
+    want = torch.from_numpy(npr.cat_brute([p1.numpy(), p2.numpy()], 1))
+    assert not torch.equal(aten.cat([p2, p1], 1), want)  # inputs in the wrong order

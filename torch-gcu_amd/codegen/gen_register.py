@@ -57,7 +57,7 @@ def load_entries(path: str | None = None) -> list[OpEntry]:
     return out
 
 
-def native_schemas() -> dict[str, tuple[str, bool]]:
+def native_schemas() -> dict[str, tuple[str, bool, bool]]:
     import torchgen
 
     path = os.path.join(os.path.dirname(torchgen.__file__), "packaged", "ATen", "native",
@@ -69,7 +69,10 @@ def native_schemas() -> dict[str, tuple[str, bool]]:
     for e in doc:
         func = e["func"]
         head = func.split("(", 1)[0]
-        out[head] = (func, bool(e.get("use_const_ref_for_mutable_tensors", False)))
+        # members of a structured group take Tensor[] as ITensorListRef in
+        # the dispatcher's C++ signature (cat, cat.out)
+        structured = bool(e.get("structured", False)) or "structured_delegate" in e
+        out[head] = (func, bool(e.get("use_const_ref_for_mutable_tensors", False)), structured)
     return out
 
 
@@ -77,13 +80,13 @@ def cpp_name(opname: str) -> str:
     return opname.replace(".", "_")
 
 
-def _signature(schema_str: str, const_mut: bool = False):
+def _signature(schema_str: str, const_mut: bool = False, structured: bool = False):
     from torchgen import local
     from torchgen.api.types import DispatcherSignature
     from torchgen.model import FunctionSchema
 
     with local.parametrize(use_const_ref_for_mutable_tensors=const_mut,
-                           use_ilistref_for_tensor_lists=False):
+                           use_ilistref_for_tensor_lists=structured):
         schema = FunctionSchema.parse(schema_str)
         sig = DispatcherSignature.from_schema(schema, symint=False)
         args = [(a.type if hasattr(a, "type") else None, a.name) for a in sig.arguments()]

@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "gcu_caching_allocator.h"
+#include "gcu_caching_host_allocator.h"
 #include "gcu_runtime.h"
 #include "mi355x_ops.h"
 
@@ -112,9 +113,22 @@ struct GCUHooks final : public at::PrivateUse1HooksInterface {
     return at::Device(kGCU, (c10::DeviceIndex)attr.device);
   }
 
-  bool isPinnedPtr(const void*) const override { return false; }
+  // Blocks of the caching host allocator, and any other page-locked memory
+  // HIP knows of (gcu_hooks.cpp:39-58 asks the runtime the same way).
+  bool isPinnedPtr(const void* data) const override {
+    if (data == nullptr) return false;
+    if (host_allocator::owns(data)) return true;
+    if (allocator::host_memory_mode() || device_count() == 0) return false;
+    hipPointerAttribute_t attr;
+    const hipError_t e = hipPointerGetAttributes(&attr, data);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // pageable memory is not known to HIP
+      return false;
+    }
+    return attr.type == hipMemoryTypeHost;
+  }
 
-  at::Allocator* getPinnedMemoryAllocator() const override { return c10::GetCPUAllocator(); }
+  at::Allocator* getPinnedMemoryAllocator() const override { return host_allocator::get(); }
 
   void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {
     c10::StorageImpl* impl = storage.unsafeGetStorageImpl();

@@ -6,6 +6,7 @@
 
 #include "efficient_ops.h"
 #include "gcu_caching_allocator.h"
+#include "gcu_caching_host_allocator.h"
 #include "gcu_graph.h"
 #include "gcu_runtime.h"
 #include "op_debug.h"
@@ -111,6 +112,20 @@ PYBIND11_MODULE(_C, m) {
   m.def("_reset_peak_memory_stats", &allocator::reset_peak_stats);
   m.def("_reset_accumulated_memory_stats", &allocator::reset_accumulated_stats);
   m.def("_empty_cache", []() { allocator::empty_cache(); });
+  m.def("_host_empty_cache", &host_allocator::empty_cache);
+  m.def("_host_memory_stats", []() {
+    const host_allocator::Stats s = host_allocator::stats();
+    py::dict d;
+    d["allocated_bytes"] = s.allocated_bytes;
+    d["reserved_bytes"] = s.reserved_bytes;
+    d["num_blocks"] = s.num_blocks;
+    d["num_host_alloc"] = s.num_host_alloc;
+    d["num_host_free"] = s.num_host_free;
+    d["num_cache_hits"] = s.num_cache_hits;
+    d["pending_events"] = s.pending_events;
+    return d;
+  });
+  m.def("_host_allocator_use_plain_memory", &host_allocator::use_plain_memory_for_tests);
   m.def("_set_memory_fraction", &allocator::set_memory_fraction);
   m.def("_get_memory_fraction", &allocator::get_memory_fraction);
   m.def("_memory_snapshot", []() {

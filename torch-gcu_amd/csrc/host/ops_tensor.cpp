@@ -7,6 +7,11 @@
 // reference, 64-bit dtypes keep their full width on the device
 // (gcu_empty_tensor.cpp:50-58 halves them there).
 #include <ATen/EmptyTensor.h>
+#include <ATen/MemoryOverlap.h>
+#include <ATen/NamedTensorUtils.h>
+#include <ATen/Operators.h>
+#include <ATen/native/CPUFallback.h>
+#include <ATen/ops/cat_meta.h>
 #include <ATen/native/Resize.h>
 #include <ATen/native/TensorFactories.h>
 #include <ATen/ops/as_strided_native.h>
@@ -18,6 +23,7 @@
 #include "aotops.h"
 #include "dispatch_util.h"
 #include "gcu_caching_allocator.h"
+#include "gcu_caching_host_allocator.h"
 
 namespace torch_gcu {
 namespace aotops {
@@ -145,6 +151,117 @@ void copy_d2d(const at::Tensor& dst, const at::Tensor& src) {
 
 }  // namespace
 
+namespace {
+
+// A tensor whose elements tile [data_ptr, data_ptr + nbytes) exactly: its
+// bytes move as one block and keep their meaning under the same strides.
+bool dense_block(const at::Tensor& t) { return t.is_non_overlapping_and_dense(); }
+
+// Host-device copies (gcu_copy.cpp:279-386).  The host side is one dense
+// block: the tensor itself when it is dense, else a contiguous host staging
+// copy.  The device side is that block's image (same sizes and strides, the
+// host dtype): dst itself when its layout and dtype already match, else a
+// device staging tensor that mi_copy casts, broadcasts and re-strides from or
+// into.  Dtype casts thus run on the GPU, and the PCIe transfer is one
+// hipMemcpyAsync on the current stream.
+//
+// Synchronisation: a non-blocking copy whose host block is pinned returns at
+// once; the block is marked as used by the stream in the caching host
+// allocator, so freeing it before the copy has run does not hand it out
+// again.  Every other copy synchronises the stream before returning, since
+// pageable memory may be reused by the caller as soon as the copy returns.
+// Under graph capture only the first kind can be recorded.
+void check_capturable(hipStream_t s, bool async_ok, const char* what) {
+  TORCH_CHECK(async_ok || !stream_is_capturing(s), "gcu: ", what,
+              " during graph capture needs pinned host memory, non_blocking=True and a dense "
+              "host tensor");
+}
+
+// dtypes the copy kernel converts between; a cast that involves another
+// dtype (complex, unsigned 16/32/64-bit, fp8) runs in CPU ATen on the host side
+bool kernel_dtype(at::ScalarType t) {
+  switch (t) {
+    case at::kByte: case at::kChar: case at::kShort: case at::kInt: case at::kLong:
+    case at::kHalf: case at::kFloat: case at::kDouble: case at::kBool: case at::kBFloat16:
+      return true;
+    default:
+      return false;
+  }
+}
+
+void mark_pinned_use(const at::Tensor& host, hipStream_t s, int device) {
+  host_allocator::record_event(host.data_ptr(), host.storage().data_ptr().get_context(), s,
+                               device);
+}
+
+at::Tensor copy_h2d(const at::Tensor& dst, const at::Tensor& src, bool non_blocking) {
+  c10::DeviceGuard g(dst.device());
+  const int dev = dst.device().index();
+  const hipStream_t s = current_hip_stream(dst.device().index());
+  const bool host_cast = src.scalar_type() != dst.scalar_type() &&
+                         !(kernel_dtype(src.scalar_type()) && kernel_dtype(dst.scalar_type()));
+  const bool dense = !host_cast && dense_block(src);
+  const bool pinned = dense && src.is_pinned();
+  // a non-dense (or host-cast) source is staged, in pinned memory when the
+  // copy is non-blocking, so that it need not wait
+  const bool async = non_blocking && (pinned || !dense);
+  check_capturable(s, non_blocking && pinned, "a host-to-device copy");
+  at::Tensor h = src;
+  if (!dense) {
+    h = at::empty(src.sizes(), src.options().dtype(host_cast ? dst.scalar_type() : src.scalar_type())
+                                   .pinned_memory(async));
+    h.copy_(src);
+  }
+  const size_t nbytes = (size_t)h.numel() * h.element_size();
+  const bool direct = h.scalar_type() == dst.scalar_type() && h.sizes() == dst.sizes() &&
+                      dense_block(dst) && h.strides() == dst.strides();
+  if (direct) {
+    GCU_HIP_CHECK(hipMemcpyAsync(dst.data_ptr(), h.data_ptr(), nbytes, hipMemcpyHostToDevice, s));
+  } else {
+    at::Tensor d = at::empty_strided(h.sizes(), h.strides(), dst.options().dtype(h.scalar_type()));
+    GCU_HIP_CHECK(hipMemcpyAsync(d.data_ptr(), h.data_ptr(), nbytes, hipMemcpyHostToDevice, s));
+    copy_d2d(dst, d.expand(dst.sizes()));
+  }
+  if (async)
+    mark_pinned_use(h, s, dev);
+  else
+    GCU_HIP_CHECK(hipStreamSynchronize(s));
+  return dst;
+}
+
+at::Tensor copy_d2h(const at::Tensor& dst, const at::Tensor& src, bool non_blocking) {
+  c10::DeviceGuard g(src.device());
+  const int dev = src.device().index();
+  const hipStream_t s = current_hip_stream(src.device().index());
+  const bool host_cast = src.scalar_type() != dst.scalar_type() &&
+                         !(kernel_dtype(src.scalar_type()) && kernel_dtype(dst.scalar_type()));
+  const bool dense = !host_cast && dense_block(dst);
+  const bool async = non_blocking && dense && dst.is_pinned();
+  check_capturable(s, async, "a device-to-host copy");
+  // the host block the bytes land in: dst itself, or a staging copy in the
+  // dtype the device holds when the cast happens on the host
+  const at::Tensor h =
+      dense ? dst : at::empty(dst.sizes(), dst.options().dtype(host_cast ? src.scalar_type()
+                                                                           : dst.scalar_type()));
+  at::Tensor d = src;
+  if (!(src.scalar_type() == h.scalar_type() && src.sizes() == h.sizes() && dense_block(src) &&
+        src.strides() == h.strides())) {
+    d = at::empty_strided(h.sizes(), h.strides(), src.options().dtype(h.scalar_type()));
+    copy_d2d(d, src.expand(h.sizes()));
+  }
+  GCU_HIP_CHECK(hipMemcpyAsync(h.data_ptr(), d.data_ptr(), (size_t)h.numel() * h.element_size(),
+                               hipMemcpyDeviceToHost, s));
+  if (async) {
+    mark_pinned_use(h, s, dev);
+    return dst;
+  }
+  GCU_HIP_CHECK(hipStreamSynchronize(s));
+  if (!dense) dst.copy_(h);
+  return dst;
+}
+
+}  // namespace
+
 at::Tensor _copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_blocking) {
   if (self.numel() == 0) return dst;
   const bool src_gcu = is_gcu(self), dst_gcu = is_gcu(dst);
@@ -165,47 +282,10 @@ at::Tensor _copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_bl
     copy_d2d(dst, self);
     return dst;
   }
-  if (!src_gcu && dst_gcu) {
-    // host -> device: dense host staging in dst's dtype, one H2D copy, then a
-    // device-side strided copy if dst is not dense
-    c10::DeviceGuard g(dst.device());
-    at::Tensor host = self.to(dst.scalar_type()).expand(dst.sizes()).contiguous();
-    const hipStream_t s = current_hip_stream(dst.device().index());
-    if (dst.is_contiguous()) {
-      GCU_HIP_CHECK(hipMemcpyAsync(dst.data_ptr(), host.data_ptr(), host.nbytes(),
-                                   hipMemcpyHostToDevice, s));
-    } else {
-      at::Tensor staging = at::empty(dst.sizes(), dst.options().memory_format(at::MemoryFormat::Contiguous));
-      GCU_HIP_CHECK(hipMemcpyAsync(staging.data_ptr(), host.data_ptr(), host.nbytes(),
-                                   hipMemcpyHostToDevice, s));
-      copy_d2d(dst, staging);
-    }
-    // a pageable host buffer may be reused as soon as this returns
-    if (!(non_blocking && self.is_pinned())) GCU_HIP_CHECK(hipStreamSynchronize(s));
-    return dst;
-  }
+  if (!src_gcu && dst_gcu) return copy_h2d(dst, self, non_blocking);
   if (src_gcu && !dst_gcu) {
     TORCH_CHECK(dst.device().is_cpu(), "gcu: cannot copy to device ", dst.device());
-    c10::DeviceGuard g(self.device());
-    const hipStream_t s = current_hip_stream(self.device().index());
-    at::Tensor dense = self;
-    if (!self.is_contiguous() || self.scalar_type() != dst.scalar_type() ||
-        self.sizes() != dst.sizes()) {
-      dense = at::empty(dst.sizes(), self.options().dtype(dst.scalar_type()));
-      copy_d2d(dense, self);
-    }
-    if (dst.is_contiguous()) {
-      GCU_HIP_CHECK(hipMemcpyAsync(dst.data_ptr(), dense.data_ptr(), dense.nbytes(),
-                                   hipMemcpyDeviceToHost, s));
-      GCU_HIP_CHECK(hipStreamSynchronize(s));
-    } else {
-      at::Tensor host = at::empty(dst.sizes(), dst.options().memory_format(at::MemoryFormat::Contiguous));
-      GCU_HIP_CHECK(hipMemcpyAsync(host.data_ptr(), dense.data_ptr(), dense.nbytes(),
-                                   hipMemcpyDeviceToHost, s));
-      GCU_HIP_CHECK(hipStreamSynchronize(s));
-      dst.copy_(host);
-    }
-    return dst;
+    return copy_d2h(dst, self, non_blocking);
   }
   TORCH_CHECK(false, "gcu _copy_from: neither tensor is on a gcu device");
 }
@@ -229,6 +309,94 @@ at::Scalar _local_scalar_dense(const at::Tensor& self) {
                                hipMemcpyDeviceToHost, s));
   GCU_HIP_CHECK(hipStreamSynchronize(s));
   return host.item();
+}
+
+// ---- cat ----------------------------------------------------------------------
+
+namespace {
+
+// cat's shape, dtype and memory-format rules are ATen's own structured meta
+// function (at::meta::structured_cat: legacy 1-D empty inputs skipped, dim
+// wrapped, sizes checked, result_type promotion, canCast into out, the
+// memory format the inputs share); this subclass supplies the output as the
+// in-tree backends' wrappers do, and mi_cat fills it.
+struct GcuCat final : at::meta::structured_cat {
+  explicit GcuCat(const at::Tensor* out) : is_out(out != nullptr) {
+    if (out != nullptr) result = *out;
+  }
+  const at::Tensor& maybe_get_output(int64_t) override { return result; }
+  void set_output_strided(int64_t i, at::IntArrayRef sizes, at::IntArrayRef strides,
+                          at::TensorOptions options, at::DimnameList names) override {
+    set_output_raw_strided(i, sizes, strides, options, names);
+  }
+  void set_output_raw_strided(int64_t, at::IntArrayRef sizes, at::IntArrayRef strides,
+                              at::TensorOptions options, at::DimnameList names) override {
+    if (!is_out) {
+      result = strides.empty() ? at::empty(sizes, options) : at::empty_strided(sizes, strides, options);
+    } else {
+      TORCH_CHECK(options.dtype() == result.dtype(), "Expected out tensor to have dtype ",
+                  options.dtype(), ", but got ", result.dtype(), " instead");
+      TORCH_CHECK(options.device() == result.device(), "Expected out tensor to have device ",
+                  options.device(), ", but got ", result.device(), " instead");
+      // a resized out takes the layout the meta function asks for; an out of
+      // the right size keeps its own strides
+      if (at::native::resize_output(result, sizes)) {
+        if (!strides.empty())
+          result.as_strided_(sizes, strides);
+        else if (options.memory_format_opt().has_value())
+          result.unsafeGetTensorImpl()->empty_tensor_restride(*options.memory_format_opt());
+      }
+    }
+    if (!names.empty()) at::namedinference::propagate_names(result, names);
+  }
+  at::Tensor result;
+  bool is_out;
+};
+
+bool kernel_dtype_all(const at::Tensor& out, const at::ITensorListRef& tensors) {
+  if (!kernel_dtype(out.scalar_type())) return false;
+  for (const at::Tensor& t : tensors)
+    if (!kernel_dtype(t.scalar_type())) return false;
+  return true;
+}
+
+void cat_fill(const at::Tensor& out, const at::ITensorListRef& tensors, int64_t dim) {
+  if (out.numel() == 0) return;
+  at::assert_no_internal_overlap(out);
+  std::vector<mi_tensor_t> descs;
+  for (const at::Tensor& t : tensors) {
+    TORCH_CHECK(t.device() == out.device(), "torch.cat(): all input tensors and out must be on the "
+                "same device, got ", t.device(), " and ", out.device());
+    at::assert_no_overlap(out, t);
+    // empty inputs add nothing (the legacy 1-D empty ones have another rank)
+    if (t.numel() > 0) descs.push_back(desc(t));
+  }
+  std::vector<const mi_tensor_t*> ptrs;
+  for (const auto& d : descs) ptrs.push_back(&d);
+  const mi_tensor_t o = desc(out);
+  check_mi(mi_cat(&o, ptrs.data(), (int32_t)ptrs.size(), (int32_t)dim, mi_stream(out)), "cat");
+}
+
+}  // namespace
+
+at::Tensor cat(const at::ITensorListRef& tensors, int64_t dim) {
+  GcuCat m(nullptr);
+  const auto pre = m.meta(tensors, dim);
+  if (!kernel_dtype_all(m.result, tensors))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP(cat)>::call(tensors, dim);
+  c10::DeviceGuard g(m.result.device());
+  cat_fill(m.result, tensors, pre.dim);
+  return m.result;
+}
+
+at::Tensor& cat_out(const at::ITensorListRef& tensors, int64_t dim, at::Tensor& out) {
+  GcuCat m(&out);
+  const auto pre = m.meta(tensors, dim);
+  if (!kernel_dtype_all(out, tensors))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP2(cat, out)>::call(tensors, dim,
+                                                                                     out);
+  cat_fill(out, tensors, pre.dim);
+  return out;
 }
 
 // ---- fills --------------------------------------------------------------------

@@ -66,6 +66,7 @@ _SIGNATURES = {
     "mi_device_cu_count": ([], ctypes.c_int32),
     "mi_copy": ([_T, _T, _S], ctypes.c_int),
     "mi_fill": ([_T, MiScalar, _S], ctypes.c_int),
+    "mi_cat": ([_T, ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_int32, _S], ctypes.c_int),
     "mi_add": ([_T, _T, _T, MiScalar, _S], ctypes.c_int),
     "mi_sub": ([_T, _T, _T, MiScalar, _S], ctypes.c_int),
     "mi_mul": ([_T, _T, _T, _S], ctypes.c_int),
@@ -190,6 +191,14 @@ def _dims(dims: Sequence[int]):
 
 def copy_(out, src):
     check("mi_copy", lib().mi_copy(desc(out), desc(src), stream_of(out)))
+    return out
+
+
+def cat(out, inputs, dim):
+    """out = cat(inputs, dim) through mi_cat; every input has out's rank."""
+    descs = [desc(t) for t in inputs]  # kept alive for the call
+    arr = (_T * max(1, len(descs)))(*[ctypes.pointer(d) for d in descs])
+    check("mi_cat", lib().mi_cat(desc(out), arr, len(descs), dim, stream_of(out)))
     return out
 
 

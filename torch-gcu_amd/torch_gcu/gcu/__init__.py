@@ -11,8 +11,8 @@ import torch
 from .. import _C
 from .graphs import GCUGraph, graph, graph_pool_handle  # noqa: F401
 from .memory import (  # noqa: F401
-    empty_cache, get_per_process_memory_fraction, max_memory_allocated, max_memory_reserved,
-    mem_get_info, memory_allocated, memory_reserved, memory_snapshot, memory_stats,
+    empty_cache, get_per_process_memory_fraction, host_empty_cache, host_memory_stats,
+    max_memory_allocated, max_memory_reserved, mem_get_info, memory_allocated, memory_reserved, memory_snapshot, memory_stats,
     reset_accumulated_memory_stats, reset_max_memory_allocated, reset_peak_memory_stats,
     set_per_process_memory_fraction,
 )

@@ -52,6 +52,17 @@ def empty_cache() -> None:
     _C._empty_cache()
 
 
+def host_memory_stats() -> dict[str, int]:
+    """Counters of the caching allocator of pinned host memory (pin_memory(),
+    torch.empty(..., pin_memory=True) and non-blocking copy staging)."""
+    return dict(sorted(_C._host_memory_stats().items()))
+
+
+def host_empty_cache() -> None:
+    """Unpins (hipHostFree) every cached pinned block that no copy still uses."""
+    _C._host_empty_cache()
+
+
 def set_per_process_memory_fraction(fraction: float, device=None) -> None:
     if not isinstance(fraction, float):
         raise TypeError("Invalid type for fraction argument, must be `float`")
