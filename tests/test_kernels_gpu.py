@@ -516,7 +516,8 @@ def test_fused_edge_cases():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.int16])
-@pytest.mark.parametrize("shape", [(1000, 777), (64, 64), (3, 130, 70)])
+@pytest.mark.parametrize("shape", [(1000, 777), (64, 64), (3, 130, 70), (1000, 776), (3, 136, 72),
+                                   (8, 2048)])
 def test_transpose_copy(dtype, shape):
     """copy_ of a transposed view (the tiled-transpose path) is bit-exact."""
     x = rand(shape, dtype, 40)
@@ -593,3 +594,14 @@ def test_cat_rejects_bad_shapes():
         _abi.cat(torch.empty(8, 5, device=DEV), [x, y], 0)
     with pytest.raises(_abi.MiError, match="dims"):
         _abi.cat(torch.empty(7, 5, device=DEV), [x, y[0]], 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_transpose_copy_partial_tiles(dtype):
+    """Transposes whose rows or columns end inside a 16-byte piece (views cut
+    from wider, aligned tensors): the edge lanes copy element by element."""
+    x = rand((200, 136), dtype, 41)
+    for view in [x[:, :130].t(), x[:195, :].t(), x[:3, :9].t(), x[:197, :133].t()]:
+        out = torch.empty(view.shape, dtype=dtype, device=DEV)
+        _abi.copy_(out, _strided_on_device(view))
+        assert_exact(out, view.contiguous(), f"transpose copy {tuple(view.shape)}")
