@@ -360,7 +360,29 @@ def transfer_ops(torch, _abi):
                         lambda s: _abi.copy_(o16, s["x"]), n * n * 4, iters=20))
     del src16, o16
     res.extend(host_transfer_ops(torch))
+    res.extend(optimizer_ops(torch, _abi))
     return res
+
+
+def optimizer_ops(torch, _abi):
+    """One fused AdamW step over the fp32 parameters of one Llama-7B decoder
+    layer (q, k, v, o [4096, 4096], gate and up [11008, 4096], down
+    [4096, 11008], two norm weights [4096]: 202 M elements); per element 4
+    reads and 3 writes of 4 bytes."""
+    log("bench: fused AdamW")
+    gen = torch.Generator().manual_seed(20261208)
+    shapes = [(4096, 4096)] * 4 + [(11008, 4096)] * 2 + [(4096, 11008), (4096,), (4096,)]
+    lists = [[torch.randn(s, generator=gen).cuda() for s in shapes] for _ in range(2)]
+    grads = [torch.randn(s, generator=gen).cuda() * 1e-3 for s in shapes]
+    m = [torch.zeros(s, device="cuda") for s in shapes]
+    v = [torch.zeros(s, device="cuda") for s in shapes]
+    steps = [torch.ones((), device="cuda") for _ in shapes]
+    n = sum(int(torch.Size(s).numel()) for s in shapes)
+    hp = dict(lr=1e-4, beta1=0.9, beta2=0.95, weight_decay=0.1, eps=1e-8)
+    return [bench_op(torch, "f4.fused_adamw fp32, one Llama-7B layer (202M params)",
+                     [{"p": p} for p in lists],
+                     lambda s: _abi.fused_adamw(s["p"], grads, m, v, [], steps, **hp),
+                     n * 4 * 7, iters=10)]
 
 
 def host_transfer_ops(torch, nbytes=256 << 20, iters=8):

@@ -165,6 +165,37 @@ mi_status_t mi_mul_scalar(const mi_tensor_t* out, const mi_tensor_t* self,
 mi_status_t mi_div_scalar(const mi_tensor_t* out, const mi_tensor_t* self,
                           mi_scalar_t other, mi_stream_t stream);
 
+/* ---- optimizer ---------------------------------------------------------- */
+
+/* Hyper-parameters of one fused AdamW step (the float arguments of
+ * torch._fused_adamw_). */
+typedef struct {
+  double lr; /* used when the lr tensor is NULL */
+  double beta1, beta2, weight_decay, eps;
+  int32_t amsgrad, maximize;
+} mi_adamw_hparams_t;
+
+/* One AdamW step over n_tensors parameters, in place: params, grads,
+ * exp_avgs, exp_avg_sqs (and max_exp_avg_sqs with amsgrad) are arrays of
+ * n_tensors descriptors of one dtype (f32, bf16, f16 or f64), each tensor
+ * dense and laid out like its param; state_steps are one-element f32 step
+ * counts (read, not advanced).  lr_tensor (one f32/f64 element) overrides
+ * hp->lr when not NULL; grad_scale unscales the grads (written back) and
+ * found_inf = 1 skips the step (both one-element f32, optional).  Every
+ * scalar tensor is read on the device, so the call can be captured.
+ * Replaces topsatenFusedAdamw (torch_gcu/csrc/aten/aot_ops/_fused_adamw_.cpp:
+ * 15-52; yaml _fused_adamw_ :144-145). */
+mi_status_t mi_fused_adamw(const mi_tensor_t* const* params,
+                           const mi_tensor_t* const* grads,
+                           const mi_tensor_t* const* exp_avgs,
+                           const mi_tensor_t* const* exp_avg_sqs,
+                           const mi_tensor_t* const* max_exp_avg_sqs,
+                           const mi_tensor_t* const* state_steps,
+                           int32_t n_tensors, const mi_tensor_t* lr_tensor,
+                           const mi_adamw_hparams_t* hp,
+                           const mi_tensor_t* grad_scale,
+                           const mi_tensor_t* found_inf, mi_stream_t stream);
+
 /* ---- indexing ---------------------------------------------------------- */
 
 /* out = self.index_select(dim, index); index is 1-D (or 0-D) int32/int64;

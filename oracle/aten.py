@@ -208,3 +208,20 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     yaml :561, then mul.out).  Pinned by float64 numpy and
     tests/golden/silu_mul.npz."""
     return (torch.nn.functional.silu(gate.float()) * up.float()).to(gate.dtype)
+
+
+# ---- training-side neighbours -------------------------------------------------------
+
+def fused_adamw(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, *, lr,
+                beta1, beta2, weight_decay, eps, amsgrad, maximize, grad_scale=None,
+                found_inf=None):
+    """aten::_fused_adamw_ -> topsatenFusedAdamw (codegen/gcu_native_functions.yaml:144-145,
+    torch_gcu/csrc/aten/aot_ops/_fused_adamw_.cpp:15-52): CPU ATen's fused AdamW
+    run on clones.  Returns the updated (params, grads, exp_avgs, exp_avg_sqs,
+    max_exp_avg_sqs).  Pinned by the float64 AdamW closed form
+    (numpy_ref.adamw64) and its planted-mistake variant."""
+    c = [[t.clone() for t in lst] for lst in (params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs)]
+    torch._fused_adamw_(*c, [s.clone() for s in state_steps], lr=lr, beta1=beta1, beta2=beta2,
+                        weight_decay=weight_decay, eps=eps, amsgrad=amsgrad, maximize=maximize,
+                        grad_scale=grad_scale, found_inf=found_inf)
+    return c

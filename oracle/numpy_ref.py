@@ -129,3 +129,29 @@ def attention64(q, k, v, causal, scale=None):
     e = np.exp(s - m)
     z = e.sum(-1, keepdims=True)
     return np.einsum("bhqk,bhkd->bhqd", e / z, v), (m + np.log(z))[..., 0]
+
+
+def adamw64(p, g, m, v, vmax, step, lr, beta1, beta2, wd, eps, amsgrad, maximize,
+            grad_scale=None, found_inf=None):
+    """One AdamW step in float64 (Loshchilov and Hutter's decoupled weight
+    decay with Adam's bias corrections, as torch.optim.AdamW documents it).
+    Returns (p, g, m, v, vmax); g comes back unscaled when grad_scale is given."""
+    p, g, m, v = (np.asarray(x, dtype=np.float64).copy() for x in (p, g, m, v))
+    vmax = None if vmax is None else np.asarray(vmax, dtype=np.float64).copy()
+    if found_inf is not None and found_inf == 1.0:
+        return p, g, m, v, vmax
+    if grad_scale is not None:
+        g = g / grad_scale
+    d = -g if maximize else g
+    p = p * (1.0 - lr * wd)
+    m = beta1 * m + (1.0 - beta1) * d
+    v = beta2 * v + (1.0 - beta2) * d * d
+    bc1 = 1.0 - beta1 ** step
+    bc2 = 1.0 - beta2 ** step
+    if amsgrad:
+        vmax = np.maximum(vmax, v)
+        den = np.sqrt(vmax) / np.sqrt(bc2) + eps
+    else:
+        den = np.sqrt(v) / np.sqrt(bc2) + eps
+    p = p - (lr / bc1) * m / den
+    return p, g, m, v, vmax

@@ -605,3 +605,41 @@ def test_transpose_copy_partial_tiles(dtype):
         out = torch.empty(view.shape, dtype=dtype, device=DEV)
         _abi.copy_(out, _strided_on_device(view))
         assert_exact(out, view.contiguous(), f"transpose copy {tuple(view.shape)}")
+
+
+# ---- fused AdamW ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_fused_adamw_abi(dtype, amsgrad):
+    """mi_fused_adamw through the C ABI, lr read from a device tensor."""
+    shapes = [(4097,), (64, 33), (1,)]
+    p = [rand(s, dtype, 70 + i) for i, s in enumerate(shapes)]
+    grads = [rand(s, dtype, 80 + i) for i, s in enumerate(shapes)]
+    m = [(rand(s, torch.float32, 90 + i) * 0.01).to(dtype) for i, s in enumerate(shapes)]
+    v = [(torch.rand(s, generator=g(95 + i)) * 1e-3).to(dtype) for i, s in enumerate(shapes)]
+    vm = [t.clone() for t in v] if amsgrad else []
+    steps = [torch.tensor(5.0) for _ in shapes]
+    hp = dict(beta1=0.9, beta2=0.999, weight_decay=0.01, eps=1e-8, amsgrad=amsgrad, maximize=False)
+    want = aten.fused_adamw(p, grads, m, v, vm, steps, lr=3e-4, **hp)
+    dp, dg, dm, dv, dvm, ds = ([dev(t) for t in lst] for lst in (p, grads, m, v, vm, steps))
+    _abi.fused_adamw(dp, dg, dm, dv, dvm, ds, lr=dev(torch.tensor(3e-4)), **hp)
+    kind = "fp32" if dtype == torch.float32 else "bf16"
+    for i in range(len(shapes)):
+        assert_close(dp[i], want[0][i], kind, f"param {i}")
+        assert_close(dm[i], want[2][i], kind, f"exp_avg {i}")
+        assert_close(dv[i], want[3][i], kind, f"exp_avg_sq {i}")
+        if amsgrad:
+            assert_close(dvm[i], want[4][i], kind, f"max_exp_avg_sq {i}")
+
+
+def test_fused_adamw_abi_rejects_mismatched_lists():
+    p = [dev(rand((8,), torch.float32, 1))]
+    with pytest.raises(_abi.MiError, match="exp_avg"):
+        _abi.fused_adamw(p, [dev(rand((8,), torch.float32, 2))], [dev(rand((9,), torch.float32, 3))],
+                         [dev(rand((8,), torch.float32, 4))], [], [dev(torch.tensor(1.0))],
+                         lr=1e-3, beta1=0.9, beta2=0.999, weight_decay=0.0, eps=1e-8)
+    with pytest.raises(_abi.MiError, match="state_step"):
+        _abi.fused_adamw(p, [dev(rand((8,), torch.float32, 2))], [dev(rand((8,), torch.float32, 3))],
+                         [dev(rand((8,), torch.float32, 4))], [], [dev(torch.tensor([1.0, 2.0]))],
+                         lr=1e-3, beta1=0.9, beta2=0.999, weight_decay=0.0, eps=1e-8)

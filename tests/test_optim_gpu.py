@@ -1,0 +1,132 @@
+"""torch._fused_adamw_ and torch.optim.AdamW(fused=True) on the gcu device,
+against CPU ATen's fused AdamW (oracle.aten.fused_adamw) on the same inputs:
+fp32 / fp64 within the fp32 bar, bf16 / fp16 within the bf16 bar (a stored
+value may differ by one rounding of the fp32 result)."""
+import pytest
+import torch
+
+import torch_gcu
+from oracle import aten
+from oracle.tolerance import assert_close
+
+pytestmark = pytest.mark.gpu
+
+C = torch_gcu._C
+
+SHAPES = [(1000,), (33, 65), (4096, 130), (7,), (0,), (3, 5, 17), (8,)]
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def make_lists(dtype, amsgrad, seed, shapes=SHAPES):
+    p = [torch.randn(s, generator=g(seed + i)).to(dtype) for i, s in enumerate(shapes)]
+    m = [(torch.randn(s, generator=g(seed + 100 + i)) * 0.01).to(dtype) for i, s in enumerate(shapes)]
+    v = [(torch.rand(s, generator=g(seed + 200 + i)) * 1e-4).to(dtype) for i, s in enumerate(shapes)]
+    vm = [(torch.rand(s, generator=g(seed + 300 + i)) * 1e-4).to(dtype) for i, s in enumerate(shapes)] \
+        if amsgrad else []
+    return p, m, v, vm
+
+
+def bar_of(dtype):
+    return "fp32" if dtype in (torch.float32, torch.float64) else "bf16"
+
+
+CONFIGS = {
+    "plain": dict(amsgrad=False, maximize=False, wd=0.01, scaled=False, lr="float"),
+    "amsgrad_maximize": dict(amsgrad=True, maximize=True, wd=0.1, scaled=False, lr="float"),
+    "grad_scale": dict(amsgrad=False, maximize=False, wd=0.01, scaled=True, lr="float"),
+    "no_decay_lr_on_gcu": dict(amsgrad=False, maximize=False, wd=0.0, scaled=False, lr="gcu"),
+    "lr_on_cpu": dict(amsgrad=True, maximize=False, wd=0.01, scaled=True, lr="cpu"),
+}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
+@pytest.mark.parametrize("cfg", list(CONFIGS))
+def test_fused_adamw_parity(dtype, cfg):
+    c = CONFIGS[cfg]
+    p, m, v, vm = make_lists(dtype, c["amsgrad"], 10)
+    dev = [[t.to("gcu") for t in lst] for lst in (p, m, v, vm)]
+    hp = dict(beta1=0.9, beta2=0.999, weight_decay=c["wd"], eps=1e-8, amsgrad=c["amsgrad"],
+              maximize=c["maximize"])
+    lr = 1e-3
+    gs = torch.tensor(1024.0) if c["scaled"] else None
+    for step in (1, 2, 3):
+        grads = [(torch.randn(s, generator=g(50 + 10 * step + i)) * (1024.0 if c["scaled"] else 1.0)).to(dtype)
+                 for i, s in enumerate(SHAPES)]
+        dgrads = [t.to("gcu") for t in grads]
+        steps = [torch.tensor(float(step)) for _ in SHAPES]
+        want = aten.fused_adamw(p, grads, m, v, vm, steps, lr=lr, grad_scale=gs, **hp)
+        lr_arg = {"float": lr, "gcu": torch.tensor(lr, device="gcu"), "cpu": torch.tensor(lr)}[c["lr"]]
+        torch._fused_adamw_(dev[0], dgrads, dev[1], dev[2], dev[3], [s.to("gcu") for s in steps],
+                            lr=lr_arg, grad_scale=None if gs is None else gs.to("gcu"), **hp)
+        torch.gcu.synchronize()
+        for k, name, lst in [(0, "param", dev[0]), (2, "exp_avg", dev[1]), (3, "exp_avg_sq", dev[2])] + \
+                ([(1, "grad", dgrads)] if c["scaled"] else []) + \
+                ([(4, "max_exp_avg_sq", dev[3])] if c["amsgrad"] else []):
+            for i, s in enumerate(SHAPES):
+                assert_close(lst[i].cpu(), want[k][i], bar_of(dtype), f"{cfg} {name} {s} step {step}")
+        if not c["scaled"]:
+            for i in range(len(SHAPES)):  # grads untouched without grad_scale
+                assert torch.equal(dgrads[i].cpu(), grads[i])
+        p, m, v = want[0], want[2], want[3]
+        vm = want[4] if c["amsgrad"] else []
+
+
+def test_fused_adamw_found_inf_many_tensors_and_misaligned():
+    """found_inf = 1 leaves every tensor untouched; 40 tensors span two
+    launches; a tensor at an address that is not 16-byte aligned takes the
+    element path."""
+    shapes = [(17 + 3 * i,) for i in range(40)]
+    p, m, v, _ = make_lists(torch.float32, False, 30, shapes)
+    base = torch.randn(1 + 4096, generator=g(31))
+    p.append(base[1:])  # 4-byte offset
+    m.append(torch.zeros(4096))
+    v.append(torch.zeros(4096))
+    shapes.append((4096,))
+    grads = [torch.randn(s, generator=g(400 + i)) for i, s in enumerate(shapes)]
+    hp = dict(lr=1e-2, beta1=0.8, beta2=0.95, weight_decay=0.02, eps=1e-6, amsgrad=False, maximize=False)
+    dbase = base.to("gcu")
+    dp = [t.to("gcu") for t in p[:-1]] + [dbase[1:]]
+    dm, dv, dg = ([t.to("gcu") for t in lst] for lst in (m, v, grads))
+    steps = [torch.tensor(1.0, device="gcu") for _ in shapes]
+    torch._fused_adamw_(dp, dg, dm, dv, [], steps, found_inf=torch.tensor(1.0, device="gcu"), **hp)
+    torch.gcu.synchronize()
+    assert all(torch.equal(a.cpu(), b) for a, b in zip(dp, p))
+    torch._fused_adamw_(dp, dg, dm, dv, [], steps, found_inf=torch.tensor(0.0, device="gcu"), **hp)
+    want = aten.fused_adamw(p, grads, m, v, [], [torch.tensor(1.0)] * len(shapes), **hp)
+    for i in range(len(shapes)):
+        assert_close(dp[i].cpu(), want[0][i], "fp32", f"param {i}")
+        assert_close(dm[i].cpu(), want[2][i], "fp32", f"exp_avg {i}")
+    assert float(dbase[0].cpu()) == float(base[0])  # the element before the view is untouched
+
+
+def test_optim_adamw_fused_trains_on_gcu():
+    """torch.optim.AdamW(fused=True) over a small model's gcu parameters runs
+    the native kernel (no CPU fallback) and follows the same optimizer on CPU."""
+    torch.manual_seed(0)
+    model = torch.nn.Sequential(torch.nn.Linear(64, 128), torch.nn.SiLU(), torch.nn.Linear(128, 10))
+    ref = [t.detach().clone() for t in model.parameters()]
+    dparams = [torch.nn.Parameter(t.to("gcu")) for t in ref]
+    cparams = [torch.nn.Parameter(t.clone()) for t in ref]
+    dopt = torch.optim.AdamW(dparams, lr=1e-2, weight_decay=0.1, fused=True)
+    copt = torch.optim.AdamW(cparams, lr=1e-2, weight_decay=0.1, fused=True)
+    C._set_op_debug_config("op_statistics=true")
+    C._clear_op_statistics()
+    try:
+        for it in range(4):
+            grads = [torch.randn(t.shape, generator=g(500 + 10 * it + i)) for i, t in enumerate(ref)]
+            for dp_, cp_, gr in zip(dparams, cparams, grads):
+                dp_.grad = gr.to("gcu")
+                cp_.grad = gr.clone()
+            dopt.step()
+            copt.step()
+        torch.gcu.synchronize()
+        stats = C._op_statistics()
+    finally:
+        C._set_op_debug_config("")
+    for dp_, cp_ in zip(dparams, cparams):
+        assert_close(dp_.detach().cpu(), cp_.detach(), "fp32", "AdamW(fused=True) params")
+    assert stats.get("_fused_adamw_", (0, 0))[0] == 4, stats
+    assert stats.get("_fused_adamw_", (0, 0))[1] == 0, stats

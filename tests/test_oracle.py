@@ -95,6 +95,39 @@ def test_copy_casts_vs_numpy():
                  torch.from_numpy(np.broadcast_to(row.numpy(), (5, 33)).copy()), "broadcast")
 
 
+@pytest.mark.parametrize("amsgrad,maximize,scaled", [(False, False, False), (True, True, False),
+                                                      (False, False, True)])
+def test_fused_adamw_vs_float64_closed_form(amsgrad, maximize, scaled):
+    shapes = [(37,), (8, 9)]
+    p = [torch.randn(s, generator=g(60 + i)) for i, s in enumerate(shapes)]
+    m = [torch.zeros(s) for s in shapes]
+    v = [torch.zeros(s) for s in shapes]
+    vm = [torch.zeros(s) for s in shapes] if amsgrad else []
+    hp = dict(lr=2e-3, beta1=0.9, beta2=0.99, weight_decay=0.05, eps=1e-8, amsgrad=amsgrad,
+              maximize=maximize)
+    gs = torch.tensor(8.0) if scaled else None
+    for step in (1, 2, 3):
+        grads = [torch.randn(s, generator=g(70 + 10 * step + i)) for i, s in enumerate(shapes)]
+        out = aten.fused_adamw(p, grads, m, v, vm, [torch.tensor(float(step))] * len(shapes),
+                               grad_scale=gs, **hp)
+        for i in range(len(shapes)):
+            want = npr.adamw64(p[i].numpy(), grads[i].numpy(), m[i].numpy(), v[i].numpy(),
+                               vm[i].numpy() if amsgrad else None, step, hp["lr"], hp["beta1"],
+                               hp["beta2"], hp["weight_decay"], hp["eps"], amsgrad, maximize,
+                               8.0 if scaled else None)
+            for k, name in [(0, "param"), (2, "exp_avg"), (3, "exp_avg_sq")] + \
+                    ([(1, "grad")] if scaled else []) + ([(4, "max_exp_avg_sq")] if amsgrad else []):
+                assert_close(out[k][i].double(), torch.from_numpy(want[k]), "fp32", f"{name} step {step}")
+        p, m, v = out[0], out[2], out[3]
+        vm = out[4] if amsgrad else []
+    # found_inf = 1 leaves everything as it was
+    grads = [torch.randn(s, generator=g(99)) for s in shapes]
+    out = aten.fused_adamw(p, grads, m, v, vm, [torch.tensor(4.0)] * 2, found_inf=torch.tensor(1.0),
+                           grad_scale=gs, **hp)
+    assert all(torch.equal(a, b) for a, b in zip(out[0], p))
+    assert all(torch.equal(a, b) for a, b in zip(out[1], grads))
+
+
 # ---- config 2 -------------------------------------------------------------------
 
 def test_sum_amax_bf16_vs_float64():
@@ -289,3 +322,10 @@ def test_planted_mistakes_are_caught():
     p1, p2 = torch.arange(6).reshape(2, 3), torch.arange(6, 10).reshape(2, 2)
     want = torch.from_numpy(npr.cat_brute([p1.numpy(), p2.numpy()], 1))
     assert not torch.equal(aten.cat([p2, p1], 1), want)  # inputs in the wrong order
+    # AdamW without the first-moment bias correction misses the closed form
+    pa, ga = torch.randn(16, generator=g(18)), torch.randn(16, generator=g(19))
+    want = npr.adamw64(pa.numpy(), ga.numpy(), np.zeros(16), np.zeros(16), None, 1, 1e-2, 0.9,
+                       0.999, 0.0, 1e-8, False, False)[0]
+    no_bc1 = pa.double() - 1e-2 * (0.1 * ga.double()) / (
+        (0.001 * ga.double() ** 2).sqrt() / math.sqrt(0.001) + 1e-8)
+    assert (no_bc1 - torch.from_numpy(want)).abs().max() > 1e-3

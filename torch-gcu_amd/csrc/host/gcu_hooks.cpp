@@ -8,6 +8,7 @@
 #include <c10/core/GeneratorImpl.h>
 #include <c10/core/impl/alloc_cpu.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -74,6 +75,7 @@ struct GCUGeneratorImpl : public c10::GeneratorImpl {
 namespace {
 
 std::mutex g_gen_mu;
+std::atomic<bool> g_initialized{false};
 std::vector<at::Generator> g_default_gens;
 
 struct GCUHooks final : public at::PrivateUse1HooksInterface {
@@ -84,6 +86,7 @@ struct GCUHooks final : public at::PrivateUse1HooksInterface {
   void init() const override {
     static std::once_flag once;
     std::call_once(once, [] {
+      g_initialized.store(true);
       allocator::init(device_count());
       mi_set_workspace_allocator(
           reinterpret_cast<mi_alloc_fn>(&allocator::workspace_alloc),
@@ -155,5 +158,7 @@ const bool g_registered = [] {
 }  // namespace
 
 void ensure_initialized() { g_hooks->init(); }
+
+bool is_initialized() { return g_initialized.load(); }
 
 }  // namespace torch_gcu

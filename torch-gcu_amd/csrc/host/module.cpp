@@ -13,6 +13,7 @@
 
 namespace torch_gcu {
 void ensure_initialized();
+bool is_initialized();
 }
 
 namespace py = pybind11;
@@ -65,6 +66,7 @@ PYBIND11_MODULE(_C, m) {
   m.doc() = "torch_gcu MI355X runtime";
 
   m.def("_init", &ensure_initialized);
+  m.def("_is_initialized", &is_initialized);
   m.def("_device_count", []() { return (int)device_count(); });
   m.def("_current_device", []() { return (int)current_device(); });
   m.def("_set_device", [](int d) { set_device((c10::DeviceIndex)d); });

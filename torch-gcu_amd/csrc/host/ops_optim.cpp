@@ -1,0 +1,150 @@
+// torch._fused_adamw_ on gcu tensors (the reference's
+// torch_gcu/csrc/aten/aot_ops/_fused_adamw_.cpp:15-52 with the checks of
+// shape_inference/_fused_adamw_.cpp:12-60): the parameter lists go to
+// mi_fused_adamw in one launch per 32 tensors.  A CPU lr tensor is read on
+// the host (as the reference does); a gcu one, like the step counts,
+// grad_scale and found_inf, is read by the kernel.
+#include <ATen/native/CPUFallback.h>
+#include <ATen/native/ForeachUtils.h>
+#include <ATen/Operators.h>
+
+#include <vector>
+
+#include "aotops.h"
+#include "dispatch_util.h"
+
+namespace torch_gcu {
+namespace aotops {
+namespace {
+
+bool kernel_dtype(at::ScalarType t) {
+  return t == at::kFloat || t == at::kBFloat16 || t == at::kHalf || t == at::kDouble;
+}
+
+// The reference's checks: the lists agree in dtype, device, sizes and
+// strides and are dense; the scalar tensors sit on the params' device.
+void check_adamw(at::TensorList self, at::TensorList grads, at::TensorList exp_avgs,
+                 at::TensorList exp_avg_sqs, at::TensorList max_exp_avg_sqs,
+                 at::TensorList state_steps, bool amsgrad, const at::Tensor* lr,
+                 const std::optional<at::Tensor>& grad_scale,
+                 const std::optional<at::Tensor>& found_inf) {
+  const size_t n = self.size();
+  TORCH_CHECK(grads.size() == n && exp_avgs.size() == n && exp_avg_sqs.size() == n &&
+                  state_steps.size() == n && (!amsgrad || max_exp_avg_sqs.size() == n),
+              "_fused_adamw_: all tensor lists must have the same length");
+  if (amsgrad) {
+    TORCH_CHECK(at::native::check_fast_path_restrictions(
+                    {self, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs}),
+                "self, grads, exp_avgs, exp_avg_sqs, and max_exp_avg_sqs must have same dtype, "
+                "device, and layout");
+  } else {
+    TORCH_CHECK(at::native::check_fast_path_restrictions({self, grads, exp_avgs, exp_avg_sqs}),
+                "self, grads, exp_avgs, and exp_avg_sqs must have same dtype, device, and layout");
+  }
+  const at::Device dev = self[0].device();
+  if (grad_scale.has_value())
+    TORCH_CHECK(grad_scale->device() == dev, "grad_scale must be on the same GCU device as the params");
+  if (found_inf.has_value())
+    TORCH_CHECK(found_inf->device() == dev, "found_inf must be on the same GCU device as the params");
+  if (lr != nullptr && !lr->is_cpu())
+    TORCH_CHECK(lr->device() == dev, "lr must be on the same GCU device as the params");
+}
+
+// Everything the kernel reads as a one-element fp32 scalar (step counts,
+// grad_scale, found_inf) is fp32 on the params' device.
+bool scalars_fit(at::TensorList state_steps, const std::optional<at::Tensor>& grad_scale,
+                 const std::optional<at::Tensor>& found_inf, const at::Device dev) {
+  auto ok = [&](const at::Tensor& t) {
+    return t.device() == dev && t.scalar_type() == at::kFloat && t.numel() == 1;
+  };
+  for (const at::Tensor& t : state_steps)
+    if (!ok(t)) return false;
+  return (!grad_scale.has_value() || ok(*grad_scale)) && (!found_inf.has_value() || ok(*found_inf));
+}
+
+void run_adamw(at::TensorList self, at::TensorList grads, at::TensorList exp_avgs,
+               at::TensorList exp_avg_sqs, at::TensorList max_exp_avg_sqs,
+               at::TensorList state_steps, const at::Tensor* lr_dev, double lr, double beta1,
+               double beta2, double weight_decay, double eps, bool amsgrad, bool maximize,
+               const std::optional<at::Tensor>& grad_scale,
+               const std::optional<at::Tensor>& found_inf) {
+  c10::DeviceGuard g(self[0].device());
+  const size_t n = self.size();
+  std::vector<mi_tensor_t> d(n * 6);
+  std::vector<const mi_tensor_t*> ptr(n * 6);
+  for (size_t i = 0; i < n; ++i) {
+    d[i] = desc(self[i]);
+    d[n + i] = desc(grads[i]);
+    d[2 * n + i] = desc(exp_avgs[i]);
+    d[3 * n + i] = desc(exp_avg_sqs[i]);
+    d[4 * n + i] = amsgrad ? desc(max_exp_avg_sqs[i]) : mi_tensor_t{};
+    d[5 * n + i] = desc(state_steps[i]);
+  }
+  for (size_t i = 0; i < 6 * n; ++i) ptr[i] = &d[i];
+  mi_adamw_hparams_t hp{};
+  hp.lr = lr;
+  hp.beta1 = beta1;
+  hp.beta2 = beta2;
+  hp.weight_decay = weight_decay;
+  hp.eps = eps;
+  hp.amsgrad = amsgrad ? 1 : 0;
+  hp.maximize = maximize ? 1 : 0;
+  mi_tensor_t lr_d{}, gs_d{}, fi_d{};
+  if (lr_dev != nullptr) lr_d = desc(*lr_dev);
+  if (grad_scale.has_value()) gs_d = desc(*grad_scale);
+  if (found_inf.has_value()) fi_d = desc(*found_inf);
+  check_mi(mi_fused_adamw(ptr.data(), ptr.data() + n, ptr.data() + 2 * n, ptr.data() + 3 * n,
+                          amsgrad ? ptr.data() + 4 * n : nullptr, ptr.data() + 5 * n, (int32_t)n,
+                          lr_dev != nullptr ? &lr_d : nullptr, &hp,
+                          grad_scale.has_value() ? &gs_d : nullptr,
+                          found_inf.has_value() ? &fi_d : nullptr, mi_stream(self[0])),
+           "_fused_adamw_");
+}
+
+}  // namespace
+
+void _fused_adamw_(at::TensorList self, at::TensorList grads, at::TensorList exp_avgs,
+                   at::TensorList exp_avg_sqs, at::TensorList max_exp_avg_sqs,
+                   at::TensorList state_steps, double lr, double beta1, double beta2,
+                   double weight_decay, double eps, bool amsgrad, bool maximize,
+                   const std::optional<at::Tensor>& grad_scale,
+                   const std::optional<at::Tensor>& found_inf) {
+  if (self.empty()) return;
+  check_adamw(self, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, nullptr,
+              grad_scale, found_inf);
+  if (!kernel_dtype(self[0].scalar_type()) ||
+      !scalars_fit(state_steps, grad_scale, found_inf, self[0].device()))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP(_fused_adamw_)>::call(
+        self, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, lr, beta1, beta2,
+        weight_decay, eps, amsgrad, maximize, grad_scale, found_inf);
+  run_adamw(self, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, nullptr, lr, beta1,
+            beta2, weight_decay, eps, amsgrad, maximize, grad_scale, found_inf);
+}
+
+void _fused_adamw__tensor_lr(at::TensorList self, at::TensorList grads, at::TensorList exp_avgs,
+                             at::TensorList exp_avg_sqs, at::TensorList max_exp_avg_sqs,
+                             at::TensorList state_steps, const at::Tensor& lr, double beta1,
+                             double beta2, double weight_decay, double eps, bool amsgrad,
+                             bool maximize, const std::optional<at::Tensor>& grad_scale,
+                             const std::optional<at::Tensor>& found_inf) {
+  if (self.empty()) return;
+  check_adamw(self, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, amsgrad, &lr,
+              grad_scale, found_inf);
+  const bool lr_ok = lr.is_cpu() || ((lr.scalar_type() == at::kFloat ||
+                                      lr.scalar_type() == at::kDouble) && lr.numel() == 1);
+  if (!kernel_dtype(self[0].scalar_type()) || !lr_ok ||
+      !scalars_fit(state_steps, grad_scale, found_inf, self[0].device()))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP2(_fused_adamw_, tensor_lr)>::call(
+        self, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, lr, beta1, beta2,
+        weight_decay, eps, amsgrad, maximize, grad_scale, found_inf);
+  if (lr.is_cpu())
+    run_adamw(self, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, nullptr,
+              lr.item<double>(), beta1, beta2, weight_decay, eps, amsgrad, maximize, grad_scale,
+              found_inf);
+  else
+    run_adamw(self, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, &lr, 0.0, beta1,
+              beta2, weight_decay, eps, amsgrad, maximize, grad_scale, found_inf);
+}
+
+}  // namespace aotops
+}  // namespace torch_gcu

@@ -46,6 +46,12 @@ class MiScalar(ctypes.Structure):
                 ("wrapped", ctypes.c_int32)]
 
 
+class MiAdamwHparams(ctypes.Structure):
+    _fields_ = [("lr", ctypes.c_double), ("beta1", ctypes.c_double), ("beta2", ctypes.c_double),
+                ("weight_decay", ctypes.c_double), ("eps", ctypes.c_double),
+                ("amsgrad", ctypes.c_int32), ("maximize", ctypes.c_int32)]
+
+
 class MiError(RuntimeError):
     """A kernel-library call returned a status other than MI_OK."""
 
@@ -67,6 +73,8 @@ _SIGNATURES = {
     "mi_copy": ([_T, _T, _S], ctypes.c_int),
     "mi_fill": ([_T, MiScalar, _S], ctypes.c_int),
     "mi_cat": ([_T, ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_int32, _S], ctypes.c_int),
+    "mi_fused_adamw": ([ctypes.POINTER(_T)] * 6 + [ctypes.c_int32, _T, ctypes.POINTER(MiAdamwHparams),
+                                                   _T, _T, _S], ctypes.c_int),
     "mi_add": ([_T, _T, _T, MiScalar, _S], ctypes.c_int),
     "mi_sub": ([_T, _T, _T, MiScalar, _S], ctypes.c_int),
     "mi_mul": ([_T, _T, _T, _S], ctypes.c_int),
@@ -200,6 +208,36 @@ def cat(out, inputs, dim):
     arr = (_T * max(1, len(descs)))(*[ctypes.pointer(d) for d in descs])
     check("mi_cat", lib().mi_cat(desc(out), arr, len(descs), dim, stream_of(out)))
     return out
+
+
+def fused_adamw(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, *, lr,
+                beta1, beta2, weight_decay, eps, amsgrad=False, maximize=False, grad_scale=None,
+                found_inf=None):
+    """One AdamW step in place through mi_fused_adamw; lr is a float or a
+    one-element device tensor."""
+    n = len(params)
+
+    def arr(lst):
+        if lst is None or len(lst) == 0:
+            return None, []
+        ds = [desc(t) for t in lst]
+        return (_T * len(ds))(*[ctypes.pointer(d) for d in ds]), ds
+
+    keep = []
+    arrays = []
+    for lst in (params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs if amsgrad else None,
+                state_steps):
+        a, ds = arr(lst)
+        keep.append(ds)
+        arrays.append(a)
+    hp = MiAdamwHparams(lr if not isinstance(lr, torch.Tensor) else 0.0, beta1, beta2,
+                        weight_decay, eps, int(amsgrad), int(maximize))
+    lr_d = desc(lr) if isinstance(lr, torch.Tensor) else None
+    gs_d = desc(grad_scale) if grad_scale is not None else None
+    fi_d = desc(found_inf) if found_inf is not None else None
+    check("mi_fused_adamw", lib().mi_fused_adamw(
+        *arrays, n, lr_d, ctypes.byref(hp), gs_d, fi_d,
+        stream_of(params[0]) if n else torch.cuda.current_stream().cuda_stream))
 
 
 def fill_(out, value, dtype=None):

@@ -4,6 +4,7 @@ memory.py:54-914, graphs.py:50-224, random.py:23-173)."""
 from __future__ import annotations
 
 import contextlib
+import os
 from typing import Any, Optional, Union
 
 import torch
@@ -37,7 +38,7 @@ def is_available() -> bool:
 
 
 def is_initialized() -> bool:
-    return True
+    return bool(_C._is_initialized())
 
 
 def _lazy_init() -> None:
@@ -189,6 +190,33 @@ def get_rng_state(device: _DeviceLike = None) -> torch.Tensor:
 
 def set_rng_state(new_state: torch.Tensor, device: _DeviceLike = None) -> None:
     _gens(_index(device)).set_state(new_state)
+
+
+def get_rng_state_all() -> list:
+    return [get_rng_state(i) for i in range(device_count())]
+
+
+def set_rng_state_all(new_states) -> None:
+    for i, st in enumerate(new_states):
+        set_rng_state(st, i)
+
+
+_BAD_FORK = False
+
+
+def _after_fork_in_child() -> None:
+    global _BAD_FORK
+    _BAD_FORK = is_initialized()  # the HIP runtime does not survive a fork
+
+
+def _is_in_bad_fork() -> bool:
+    """True in a child forked after the device was initialised (torch.manual_seed
+    then leaves the gcu generators alone, as it does for CUDA)."""
+    return _BAD_FORK
+
+
+if hasattr(os, "register_at_fork"):
+    os.register_at_fork(after_in_child=_after_fork_in_child)
 
 
 from . import efficient  # noqa: E402,F401
