@@ -361,6 +361,52 @@ def transfer_ops(torch, _abi):
     del src16, o16
     res.extend(host_transfer_ops(torch))
     res.extend(optimizer_ops(torch, _abi))
+    res.extend(backward_ops(torch, _abi))
+    return res
+
+
+def backward_ops(torch, _abi):
+    """The training-side backward ops at the shapes of configs 2 and 3:
+    silu_backward bf16 [16384, 11008], log_softmax backward bf16
+    [8192, 32000], layer-norm backward bf16 [16384, 4096] with all three
+    gradients (two reads and one write per element, plus the weight and the
+    column sums)."""
+    log("bench: backward ops")
+    gen = torch.Generator().manual_seed(20261209)
+    res = []
+    M, N = 16384, 11008
+    sets = [{"dy": torch.randn(M, N, generator=gen).bfloat16().cuda(),
+             "x": torch.randn(M, N, generator=gen).bfloat16().cuda()} for _ in range(2)]
+    o = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    res.append(bench_op(torch, "f4.silu_backward bf16 [16384,11008]", sets,
+                        lambda s: _abi.silu_backward(o, s["dy"], s["x"]), M * N * 6))
+    del sets, o
+    M, N = 8192, 32000
+    sets = []
+    for _ in range(2):
+        x = torch.randn(M, N, generator=gen).bfloat16().cuda()
+        sets.append({"dy": torch.randn(M, N, generator=gen).bfloat16().cuda(),
+                     "y": torch.log_softmax(x.float(), -1).bfloat16()})
+        del x
+    o = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    res.append(bench_op(torch, "f4.log_softmax_backward bf16 [8192,32000]", sets,
+                        lambda s: _abi.log_softmax_backward(o, s["dy"], s["y"], -1), M * N * 6))
+    del sets, o
+    M, N = 16384, 4096
+    w = torch.randn(N, generator=gen).bfloat16().cuda()
+    sets = []
+    for _ in range(2):
+        x = torch.randn(M, N, generator=gen).bfloat16().cuda()
+        mean = x.float().mean(-1, keepdim=True)
+        rstd = torch.rsqrt(x.float().var(-1, unbiased=False, keepdim=True) + 1e-5)
+        sets.append({"dy": torch.randn(M, N, generator=gen).bfloat16().cuda(), "x": x,
+                     "mean": mean, "rstd": rstd})
+    dx = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    dw, db = torch.empty_like(w), torch.empty_like(w)
+    res.append(bench_op(torch, "f4.layer_norm_backward bf16 [16384,4096] (dx, dgamma, dbeta)", sets,
+                        lambda s: _abi.layer_norm_backward(dx, dw, db, s["dy"], s["x"], s["mean"],
+                                                           s["rstd"], w, N),
+                        M * N * 6 + M * 8 + N * 6))
     return res
 
 

@@ -234,6 +234,23 @@ mi_status_t mi_softmax(const mi_tensor_t* out, const mi_tensor_t* self,
 mi_status_t mi_log_softmax(const mi_tensor_t* out, const mi_tensor_t* self,
                            int64_t dim, mi_stream_t stream);
 
+/* Gradients of the two, from the forward output y and grad_output dy (one
+ * dtype; grad_input may be f16/bf16 when they are float, the half_to_float
+ * case), row sums in float:
+ *   log_softmax: grad_input = dy - exp(y) * sum(dy)
+ *   softmax:     grad_input = y * (dy - sum(dy * y))
+ * Contiguous operands.  Replace topsatenLogSoftmaxBackward
+ * (_log_softmax_backward_data.out :157) and topsatenSoftmaxBackward
+ * (_softmax_backward_data.out :184). */
+mi_status_t mi_log_softmax_backward(const mi_tensor_t* grad_input,
+                                    const mi_tensor_t* grad_output,
+                                    const mi_tensor_t* output, int64_t dim,
+                                    mi_stream_t stream);
+mi_status_t mi_softmax_backward(const mi_tensor_t* grad_input,
+                                const mi_tensor_t* grad_output,
+                                const mi_tensor_t* output, int64_t dim,
+                                mi_stream_t stream);
+
 /* ---- dense contractions ------------------------------------------------------
  * bf16 / fp16 operands run on MFMA (v_mfma_f32_32x32x16) with fp32
  * accumulation and one rounding of the result; fp32 operands on the VALU.
@@ -318,6 +335,33 @@ mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out,
 /* out = silu(gate) * up, fp32 math: silu(g) = g / (1 + exp(-g)). */
 mi_status_t mi_silu_mul(const mi_tensor_t* out, const mi_tensor_t* gate,
                         const mi_tensor_t* up, mi_stream_t stream);
+
+/* grad_input = dy * s * (1 + x * (1 - s)), s = sigmoid(x), fp32 math; dy and
+ * x broadcast to grad_input, all one dtype.  Replaces topsatenSiluBackward
+ * (yaml silu_backward.grad_input :563). */
+mi_status_t mi_silu_backward(const mi_tensor_t* grad_input,
+                             const mi_tensor_t* grad_output,
+                             const mi_tensor_t* self, mi_stream_t stream);
+
+/* native_layer_norm_backward over rows of normalized_numel elements: with
+ * xh = (x - mean) * rstd and gw = dy * weight,
+ *   grad_input  = rstd * (gw - mean_row(gw) - xh * mean_row(gw * xh))
+ *   grad_weight = sum_rows(dy * xh),  grad_bias = sum_rows(dy)
+ * in fp32; any of the three outputs may be NULL (not computed).  input and
+ * grad_out contiguous of one dtype (f32/bf16/f16); mean and rstd one element
+ * per row, fp32 or the input's dtype; weight fp32 or the input's dtype, or
+ * NULL.  The column sums are added in a fixed order (workspace of at most
+ * 2048 x 2 x normalized_numel floats).  Replaces
+ * topsatenNativeLayerNormBackward (yaml native_layer_norm_backward :483). */
+mi_status_t mi_layer_norm_backward(const mi_tensor_t* grad_input,
+                                   const mi_tensor_t* grad_weight,
+                                   const mi_tensor_t* grad_bias,
+                                   const mi_tensor_t* grad_out,
+                                   const mi_tensor_t* input,
+                                   const mi_tensor_t* mean,
+                                   const mi_tensor_t* rstd,
+                                   const mi_tensor_t* weight,
+                                   int64_t normalized_numel, mi_stream_t stream);
 
 #ifdef __cplusplus
 }

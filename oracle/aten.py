@@ -225,3 +225,35 @@ def fused_adamw(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_ste
                         weight_decay=weight_decay, eps=eps, amsgrad=amsgrad, maximize=maximize,
                         grad_scale=grad_scale, found_inf=found_inf)
     return c
+
+
+def silu_backward(grad_output, x):
+    """aten::silu_backward -> topsatenSiluBackward (yaml silu_backward.grad_input :563),
+    sent to CPU on s60 (codegen/gcu_op_fallback.yaml:22-25).  Pinned by the
+    float64 closed form s * (1 + x * (1 - s)) and a central difference of silu."""
+    return torch.ops.aten.silu_backward(grad_output, x)
+
+
+def log_softmax_backward(grad_output, output, dim, input_dtype):
+    """aten::_log_softmax_backward_data (yaml :157; s60 fallback list).  Pinned
+    by float64 dy - exp(y) * sum(dy) and a central difference of log_softmax."""
+    return torch.ops.aten._log_softmax_backward_data(grad_output, output, dim, input_dtype)
+
+
+def softmax_backward(grad_output, output, dim, input_dtype):
+    """aten::_softmax_backward_data (yaml :184; s60 fallback list).  Pinned by
+    float64 y * (dy - sum(dy * y))."""
+    return torch.ops.aten._softmax_backward_data(grad_output, output, dim, input_dtype)
+
+
+def layer_norm_forward(x, normalized_shape, weight, bias, eps):
+    """aten::native_layer_norm on CPU: (out, mean, rstd), the inputs of the backward."""
+    return torch.native_layer_norm(x, normalized_shape, weight, bias, eps)
+
+
+def layer_norm_backward(grad_out, x, normalized_shape, mean, rstd, weight, bias, mask):
+    """aten::native_layer_norm_backward -> topsatenNativeLayerNormBackward
+    (yaml :483; s60 fallback list).  Pinned by the float64 closed form of
+    numpy_ref.layer_norm_backward64 and central differences of layer norm."""
+    return torch.ops.aten.native_layer_norm_backward(grad_out, x, normalized_shape, mean, rstd,
+                                                     weight, bias, mask)

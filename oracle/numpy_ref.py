@@ -155,3 +155,62 @@ def adamw64(p, g, m, v, vmax, step, lr, beta1, beta2, wd, eps, amsgrad, maximize
         den = np.sqrt(v) / np.sqrt(bc2) + eps
     p = p - (lr / bc1) * m / den
     return p, g, m, v, vmax
+
+
+def silu_backward64(dy, x):
+    x = np.asarray(x, dtype=np.float64)
+    s = 1.0 / (1.0 + np.exp(-x))
+    return np.asarray(dy, dtype=np.float64) * s * (1.0 + x * (1.0 - s))
+
+
+def log_softmax_backward64(dy, y, axis=-1):
+    dy = np.asarray(dy, dtype=np.float64)
+    return dy - np.exp(np.asarray(y, dtype=np.float64)) * dy.sum(axis=axis, keepdims=True)
+
+
+def softmax_backward64(dy, y, axis=-1):
+    dy, y = np.asarray(dy, dtype=np.float64), np.asarray(y, dtype=np.float64)
+    return y * (dy - (dy * y).sum(axis=axis, keepdims=True))
+
+
+def layer_norm64(x, w, b, eps):
+    """Rows of the last axis: (out, mean, rstd)."""
+    x = np.asarray(x, dtype=np.float64)
+    mu = x.mean(axis=-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(axis=-1, keepdims=True)
+    rs = 1.0 / np.sqrt(var + eps)
+    out = (x - mu) * rs
+    if w is not None:
+        out = out * np.asarray(w, dtype=np.float64)
+    if b is not None:
+        out = out + np.asarray(b, dtype=np.float64)
+    return out, mu, rs
+
+
+def layer_norm_backward64(dy, x, mu, rs, w):
+    """Closed form of the layer-norm gradient over the last axis (float64):
+    returns (dx, dgamma, dbeta) with dgamma / dbeta summed over all rows."""
+    dy = np.asarray(dy, dtype=np.float64)
+    x = np.asarray(x, dtype=np.float64)
+    n = x.shape[-1]
+    xh = (x - mu) * rs
+    gw = dy * (np.asarray(w, dtype=np.float64) if w is not None else 1.0)
+    dx = rs * (gw - gw.sum(-1, keepdims=True) / n - xh * (gw * xh).sum(-1, keepdims=True) / n)
+    rows = dy.reshape(-1, n)
+    return dx, (rows * xh.reshape(-1, n)).sum(0), rows.sum(0)
+
+
+def central_difference(f, x, eps=1e-6):
+    """d(sum(f(x) * c)) / dx for a fixed random c, by central differences
+    (float64, tiny inputs only); returns (grad, c)."""
+    x = np.asarray(x, dtype=np.float64)
+    c = np.random.default_rng(7).standard_normal(np.shape(f(x)))
+    g = np.zeros_like(x)
+    it = np.nditer(x, flags=["multi_index"])
+    for _ in it:
+        i = it.multi_index
+        xp, xm = x.copy(), x.copy()
+        xp[i] += eps
+        xm[i] -= eps
+        g[i] = ((f(xp) * c).sum() - (f(xm) * c).sum()) / (2 * eps)
+    return g, c

@@ -643,3 +643,39 @@ def test_fused_adamw_abi_rejects_mismatched_lists():
         _abi.fused_adamw(p, [dev(rand((8,), torch.float32, 2))], [dev(rand((8,), torch.float32, 3))],
                          [dev(rand((8,), torch.float32, 4))], [], [dev(torch.tensor([1.0, 2.0]))],
                          lr=1e-3, beta1=0.9, beta2=0.999, weight_decay=0.0, eps=1e-8)
+
+
+# ---- backward ops -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_backward_ops_abi(dtype):
+    """mi_silu_backward, mi_log_softmax_backward / mi_softmax_backward and
+    mi_layer_norm_backward through the C ABI (16-bit layer-norm column sums
+    against the float64 closed form: CPU ATen adds them in 16-bit)."""
+    from oracle import numpy_ref as npr
+    kind = "fp32" if dtype == torch.float32 else "bf16"
+    dy = rand((300, 1024), dtype, 90)
+    x = rand((300, 1024), dtype, 91) * 2
+    out = torch.empty(300, 1024, dtype=dtype, device=DEV)
+    _abi.silu_backward(out, dev(dy), dev(x))
+    assert_close(out, aten.silu_backward(dy, x), kind, "silu_backward")
+    y = torch.log_softmax(x.float(), -1).to(dtype)
+    _abi.log_softmax_backward(out, dev(dy), dev(y), -1)
+    assert_close(out, aten.log_softmax_backward(dy, y, -1, dtype), kind, "log_softmax_backward")
+    p = torch.softmax(x.float(), -1).to(dtype)
+    _abi.softmax_backward(out, dev(dy), dev(p), -1)
+    assert_close(out, aten.softmax_backward(dy, p, -1, dtype), kind, "softmax_backward")
+    w, b = rand((1024,), dtype, 92), rand((1024,), dtype, 93)
+    _, mean, rstd = aten.layer_norm_forward(x, [1024], w, b, 1e-5)
+    want = aten.layer_norm_backward(dy, x, [1024], mean, rstd, w, b, [True, True, True])
+    dw, db = torch.empty(1024, dtype=dtype, device=DEV), torch.empty(1024, dtype=dtype, device=DEV)
+    _abi.layer_norm_backward(out, dw, db, dev(dy), dev(x), dev(mean), dev(rstd), dev(w), 1024)
+    assert_close(out, want[0], kind, "layer_norm dx")
+    _, rdw, rdb = npr.layer_norm_backward64(dy.float().numpy(), x.float().numpy(),
+                                            mean.double().numpy(), rstd.double().numpy(),
+                                            w.float().numpy())
+    assert_close(dw, torch.from_numpy(rdw).to(dtype), kind, "layer_norm dgamma")
+    assert_close(db, torch.from_numpy(rdb).to(dtype), kind, "layer_norm dbeta")
+    # only the column sums, no weight
+    _abi.layer_norm_backward(None, None, db, dev(dy), dev(x), dev(mean), dev(rstd), None, 1024)
+    assert_close(db, torch.from_numpy(rdb).to(dtype), kind, "layer_norm dbeta alone")

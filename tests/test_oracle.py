@@ -128,6 +128,58 @@ def test_fused_adamw_vs_float64_closed_form(amsgrad, maximize, scaled):
     assert all(torch.equal(a, b) for a, b in zip(out[1], grads))
 
 
+def test_backward_closed_forms_match_central_differences():
+    """The float64 closed forms the backward oracles are pinned to are the
+    derivatives of their forward ops (central differences on tiny inputs)."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 6))
+    silu = lambda t: t / (1.0 + np.exp(-t))  # noqa: E731
+    num, c = npr.central_difference(silu, x)
+    assert np.abs(num - npr.silu_backward64(c, x)).max() < 1e-7
+
+    def log_softmax(t):
+        m = t.max(-1, keepdims=True)
+        return t - m - np.log(np.exp(t - m).sum(-1, keepdims=True))
+    num, c = npr.central_difference(log_softmax, x)
+    assert np.abs(num - npr.log_softmax_backward64(c, log_softmax(x))).max() < 1e-7
+    softmax = lambda t: np.exp(log_softmax(t))  # noqa: E731
+    num, c = npr.central_difference(softmax, x)
+    assert np.abs(num - npr.softmax_backward64(c, softmax(x))).max() < 1e-7
+
+    w, b = rng.standard_normal(6), rng.standard_normal(6)
+    num, c = npr.central_difference(lambda t: npr.layer_norm64(t, w, b, 1e-5)[0], x)
+    _, mu, rs = npr.layer_norm64(x, w, b, 1e-5)
+    dx, dw, db = npr.layer_norm_backward64(c, x, mu, rs, w)
+    assert np.abs(num - dx).max() < 1e-6
+    numw, _ = npr.central_difference(lambda ww: npr.layer_norm64(x, ww, b, 1e-5)[0], w)
+    numb, _ = npr.central_difference(lambda bb: npr.layer_norm64(x, w, bb, 1e-5)[0], b)
+    # the same random cotangent c (seeded) is used for every difference
+    assert np.abs(numw - dw).max() < 1e-6 and np.abs(numb - db).max() < 1e-6
+
+
+def test_backward_oracles_vs_float64():
+    x = torch.randn(64, 333, generator=g(80))
+    dy = torch.randn(64, 333, generator=g(81))
+    assert_close(aten.silu_backward(dy, x).double(),
+                 torch.from_numpy(npr.silu_backward64(dy.numpy(), x.numpy())), "fp32", "silu_backward")
+    y = torch.log_softmax(x, -1)
+    assert_close(aten.log_softmax_backward(dy, y, -1, torch.float32).double(),
+                 torch.from_numpy(npr.log_softmax_backward64(dy.numpy(), y.numpy())), "fp32",
+                 "log_softmax_backward")
+    p = torch.softmax(x, 0)
+    assert_close(aten.softmax_backward(dy, p, 0, torch.float32).double(),
+                 torch.from_numpy(npr.softmax_backward64(dy.numpy(), p.numpy(), 0)), "fp32",
+                 "softmax_backward dim 0")
+    w, b = torch.randn(333, generator=g(82)), torch.randn(333, generator=g(83))
+    out, mean, rstd = aten.layer_norm_forward(x, [333], w, b, 1e-5)
+    dx, dw, db = aten.layer_norm_backward(dy, x, [333], mean, rstd, w, b, [True, True, True])
+    rdx, rdw, rdb = npr.layer_norm_backward64(dy.numpy(), x.numpy(), mean.double().numpy(),
+                                              rstd.double().numpy(), w.numpy())
+    assert_close(dx.double(), torch.from_numpy(rdx), "fp32", "layer_norm dx")
+    assert_close(dw.double(), torch.from_numpy(rdw), "fp32", "layer_norm dgamma")
+    assert_close(db.double(), torch.from_numpy(rdb), "fp32", "layer_norm dbeta")
+
+
 # ---- config 2 -------------------------------------------------------------------
 
 def test_sum_amax_bf16_vs_float64():
@@ -329,3 +381,10 @@ def test_planted_mistakes_are_caught():
     no_bc1 = pa.double() - 1e-2 * (0.1 * ga.double()) / (
         (0.001 * ga.double() ** 2).sqrt() / math.sqrt(0.001) + 1e-8)
     assert (no_bc1 - torch.from_numpy(want)).abs().max() > 1e-3
+    # a layer-norm gradient without the xh * mean(gw * xh) term misses its central difference
+    rng = np.random.default_rng(4)
+    xs = rng.standard_normal((2, 5))
+    num, c = npr.central_difference(lambda t: npr.layer_norm64(t, None, None, 1e-5)[0], xs)
+    _, mu, rs = npr.layer_norm64(xs, None, None, 1e-5)
+    dropped = rs * (c - c.sum(-1, keepdims=True) / 5)
+    assert np.abs(num - dropped).max() > 1e-2

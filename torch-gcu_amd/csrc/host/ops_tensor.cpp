@@ -24,6 +24,7 @@
 #include "dispatch_util.h"
 #include "gcu_caching_allocator.h"
 #include "gcu_caching_host_allocator.h"
+#include "structured_out.h"
 
 namespace torch_gcu {
 namespace aotops {
@@ -318,40 +319,8 @@ namespace {
 // cat's shape, dtype and memory-format rules are ATen's own structured meta
 // function (at::meta::structured_cat: legacy 1-D empty inputs skipped, dim
 // wrapped, sizes checked, result_type promotion, canCast into out, the
-// memory format the inputs share); this subclass supplies the output as the
-// in-tree backends' wrappers do, and mi_cat fills it.
-struct GcuCat final : at::meta::structured_cat {
-  explicit GcuCat(const at::Tensor* out) : is_out(out != nullptr) {
-    if (out != nullptr) result = *out;
-  }
-  const at::Tensor& maybe_get_output(int64_t) override { return result; }
-  void set_output_strided(int64_t i, at::IntArrayRef sizes, at::IntArrayRef strides,
-                          at::TensorOptions options, at::DimnameList names) override {
-    set_output_raw_strided(i, sizes, strides, options, names);
-  }
-  void set_output_raw_strided(int64_t, at::IntArrayRef sizes, at::IntArrayRef strides,
-                              at::TensorOptions options, at::DimnameList names) override {
-    if (!is_out) {
-      result = strides.empty() ? at::empty(sizes, options) : at::empty_strided(sizes, strides, options);
-    } else {
-      TORCH_CHECK(options.dtype() == result.dtype(), "Expected out tensor to have dtype ",
-                  options.dtype(), ", but got ", result.dtype(), " instead");
-      TORCH_CHECK(options.device() == result.device(), "Expected out tensor to have device ",
-                  options.device(), ", but got ", result.device(), " instead");
-      // a resized out takes the layout the meta function asks for; an out of
-      // the right size keeps its own strides
-      if (at::native::resize_output(result, sizes)) {
-        if (!strides.empty())
-          result.as_strided_(sizes, strides);
-        else if (options.memory_format_opt().has_value())
-          result.unsafeGetTensorImpl()->empty_tensor_restride(*options.memory_format_opt());
-      }
-    }
-    if (!names.empty()) at::namedinference::propagate_names(result, names);
-  }
-  at::Tensor result;
-  bool is_out;
-};
+// memory format the inputs share); mi_cat fills the output.
+using GcuCat = OneOutput<at::meta::structured_cat>;
 
 bool kernel_dtype_all(const at::Tensor& out, const at::ITensorListRef& tensors) {
   if (!kernel_dtype(out.scalar_type())) return false;

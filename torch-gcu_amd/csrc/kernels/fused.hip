@@ -330,7 +330,23 @@ mi_status_t rope_view(const mi_tensor_t* o, const mi_tensor_t* in, int64_t token
 
 // ---- SiLU-mul ---------------------------------------------------------------------
 
-template <typename Tag>
+// The two elementwise SiLU pairs: silu(a) * b (the fused SwiGLU product) and
+// silu's derivative applied to a gradient, a * s * (1 + b * (1 - s)) with
+// s = sigmoid(b), a = grad_output, b = the forward input (ATen's
+// silu_backward formula, aten/src/ATen/native/cpu/Activation.cpp).
+enum PairOp { P_SILU_MUL = 0, P_SILU_BWD = 1 };
+
+template <int OP>
+__device__ __forceinline__ float pair_op(float a, float b) {
+  if constexpr (OP == P_SILU_MUL) {
+    return a * __builtin_amdgcn_rcpf(1.0f + fast_exp(-a)) * b;
+  } else {
+    const float sg = __builtin_amdgcn_rcpf(1.0f + fast_exp(-b));
+    return a * sg * (1.0f + b * (1.0f - sg));
+  }
+}
+
+template <typename Tag, int OP>
 __global__ __launch_bounds__(256) void silu_mul_kernel(typename FT<Tag>::storage* __restrict__ out,
                                                        const typename FT<Tag>::storage* __restrict__ g,
                                                        const typename FT<Tag>::storage* __restrict__ u,
@@ -359,11 +375,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(typename FT<Tag>::storage
     if (i < nvec) {
       V o;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float x = FT<Tag>::load(vg[k].s[e]);
-        const float sig = __builtin_amdgcn_rcpf(1.0f + fast_exp(-x));
-        o.s[e] = FT<Tag>::store(x * sig * FT<Tag>::load(vu[k].s[e]));
-      }
+      for (int e = 0; e < VEC; ++e)
+        o.s[e] = FT<Tag>::store(pair_op<OP>(FT<Tag>::load(vg[k].s[e]), FT<Tag>::load(vu[k].s[e])));
       st_stream((V*)out + i, o);
     }
   }
@@ -372,12 +385,11 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(typename FT<Tag>::storage
   const int64_t rem = n - nvec * VEC;
   if (blockIdx.x == 0 && t < rem) {
     const int64_t i = nvec * VEC + t;
-    const float x = FT<Tag>::load(g[i]);
-    out[i] = FT<Tag>::store(x * __builtin_amdgcn_rcpf(1.0f + fast_exp(-x)) * FT<Tag>::load(u[i]));
+    out[i] = FT<Tag>::store(pair_op<OP>(FT<Tag>::load(g[i]), FT<Tag>::load(u[i])));
   }
 }
 
-template <typename Tag>
+template <typename Tag, int OP>
 __global__ __launch_bounds__(256) void silu_mul_strided_kernel(char* out, const char* g,
                                                                const char* u, OffsetCalc<3> oc,
                                                                int64_t n) {
@@ -386,14 +398,12 @@ __global__ __launch_bounds__(256) void silu_mul_strided_kernel(char* out, const 
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
     int64_t off[3];
     oc.get(i, off);
-    const float x = FT<Tag>::load(((const St*)g)[off[1]]);
-    const float y = x * __builtin_amdgcn_rcpf(1.0f + fast_exp(-x)) *
-                    FT<Tag>::load(((const St*)u)[off[2]]);
-    ((St*)out)[off[0]] = FT<Tag>::store(y);
+    ((St*)out)[off[0]] = FT<Tag>::store(
+        pair_op<OP>(FT<Tag>::load(((const St*)g)[off[1]]), FT<Tag>::load(((const St*)u)[off[2]])));
   }
 }
 
-template <typename Tag>
+template <typename Tag, int OP>
 mi_status_t silu_mul_t(const mi_tensor_t* out, const mi_tensor_t* g, const mi_tensor_t* u,
                        hipStream_t stream) {
   typedef typename FT<Tag>::storage St;
@@ -406,14 +416,14 @@ mi_status_t silu_mul_t(const mi_tensor_t* out, const mi_tensor_t* g, const mi_te
     constexpr int VEC = 16 / sizeof(St);
     const int64_t nvec = it.numel / VEC;
     const unsigned grid = nvec > 0 ? ceil_div_u(nvec, 256 * 4) : 1;
-    hipLaunchKernelGGL(silu_mul_kernel<Tag>, dim3(grid), dim3(256), 0, stream, (St*)it.data[0],
+    hipLaunchKernelGGL((silu_mul_kernel<Tag, OP>), dim3(grid), dim3(256), 0, stream, (St*)it.data[0],
                        (const St*)it.data[1], (const St*)it.data[2], it.numel);
     return check_launch("silu_mul");
   }
   OffsetCalc<3> oc = make_offset_calc<3>(it);
   const int64_t want = (it.numel + 255) / 256;
   const unsigned grid = (unsigned)(want < 65536 ? want : 65536);
-  hipLaunchKernelGGL(silu_mul_strided_kernel<Tag>, dim3(grid), dim3(256), 0, stream, it.data[0],
+  hipLaunchKernelGGL((silu_mul_strided_kernel<Tag, OP>), dim3(grid), dim3(256), 0, stream, it.data[0],
                      (const char*)it.data[1], (const char*)it.data[2], oc, it.numel);
   return check_launch("silu_mul_strided");
 }
@@ -529,10 +539,27 @@ mi_status_t mi_silu_mul(const mi_tensor_t* out, const mi_tensor_t* gate, const m
   MI_CHECK_ARG(gate->dtype == up->dtype && out->dtype == gate->dtype,
                "silu_mul: gate, up and out must share a dtype");
   switch (out->dtype) {
-    case MI_BF16: return silu_mul_t<BF16>(out, gate, up, stream);
-    case MI_F16: return silu_mul_t<F16>(out, gate, up, stream);
-    case MI_F32: return silu_mul_t<float>(out, gate, up, stream);
+    case MI_BF16: return silu_mul_t<BF16, P_SILU_MUL>(out, gate, up, stream);
+    case MI_F16: return silu_mul_t<F16, P_SILU_MUL>(out, gate, up, stream);
+    case MI_F32: return silu_mul_t<float, P_SILU_MUL>(out, gate, up, stream);
     default: MI_FAIL(MI_ERR_UNSUPPORTED, "silu_mul: dtype %s", dtype_name(out->dtype));
+  }
+}
+
+mi_status_t mi_silu_backward(const mi_tensor_t* grad_input, const mi_tensor_t* grad_output,
+                             const mi_tensor_t* self, mi_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = (hipStream_t)stream_;
+  MI_RETURN_IF(validate(grad_input, "grad_input"));
+  MI_RETURN_IF(validate(grad_output, "grad_output"));
+  MI_RETURN_IF(validate(self, "self"));
+  MI_CHECK_ARG(grad_output->dtype == self->dtype && grad_input->dtype == self->dtype,
+               "silu_backward: grad_input, grad_output and self must share a dtype");
+  switch (self->dtype) {
+    case MI_BF16: return silu_mul_t<BF16, P_SILU_BWD>(grad_input, grad_output, self, stream);
+    case MI_F16: return silu_mul_t<F16, P_SILU_BWD>(grad_input, grad_output, self, stream);
+    case MI_F32: return silu_mul_t<float, P_SILU_BWD>(grad_input, grad_output, self, stream);
+    default: MI_FAIL(MI_ERR_UNSUPPORTED, "silu_backward: dtype %s", dtype_name(self->dtype));
   }
 }
 

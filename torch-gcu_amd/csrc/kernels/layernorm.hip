@@ -1,0 +1,451 @@
+// native_layer_norm_backward over the last N elements (normalized_shape
+// flattened): with xh = (x - mean) * rstd and gw = dy * gamma (dy without a
+// weight), per row
+//   dx = rstd * (gw - sum(gw) / N - xh * sum(gw * xh) / N)
+// and per column, over all M rows,
+//   dgamma = sum(dy * xh)      dbeta = sum(dy)
+// all in fp32 (ATen's LayerNormBackwardKernelImpl,
+// aten/src/ATen/native/cpu/layer_norm_kernel.cpp, is the same arithmetic in
+// the form a*dy*gamma + b*x + c).  mean and rstd may be fp32 or the input's
+// dtype, gamma fp32 or the input's dtype.
+//
+// HBM-bound.  Fused path (dense rows, N <= 2048 16-byte vectors, aligned):
+// a block walks kLnRows (or more, so that there are at most kLnMaxParts
+// blocks) consecutive rows, two at a time with all their loads in flight and
+// one block reduction for their sums; each lane owns the same column
+// vectors in every row, so gamma stays in registers and the dgamma / dbeta
+// column sums over the block's rows accumulate in registers.  Per row: one
+// read of dy and x, two block sums, one write of dx.  The block's column
+// partials go to workspace (one row of 2N floats per block) and a finish pass
+// adds them in a fixed order.  Other shapes: one block per row for dx (two
+// reads of the row) and a column-partial pass for dgamma / dbeta.
+#include "iter.h"
+
+namespace mi {
+namespace {
+
+constexpr int kLnBlock = 256;
+constexpr int kLnRows = 32;       // rows per block (at least), fused path
+constexpr int kLnMaxVpl = 4;      // 16-byte vectors per lane and row (512 lanes), fused path
+constexpr int kLnColRows = 64;    // rows per partial (at least), column pass
+constexpr int64_t kLnMaxParts = 2048;  // partial rows: at most 2048 x 2N floats
+
+struct LnArgs {
+  void* dx;
+  const void* dy;
+  const void* x;
+  const void* mean;
+  const void* rstd;
+  const void* gamma;
+  float* part;  // [nparts, 2, N]: dgamma partials, then dbeta partials
+  int64_t M, N;
+  int64_t rows_per_part;  // rows summed into one partial row
+  int mean_dt, gamma_dt;
+  int need_dx, need_dw, need_db;
+};
+
+__device__ __forceinline__ float2 block_sum2(float a, float b, float* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  a = wave_sum(a);
+  b = wave_sum(b);
+  if (lane == 0) {
+    red[2 * wid] = a;
+    red[2 * wid + 1] = b;
+  }
+  __syncthreads();
+  float ra = red[0], rb = red[1];
+#pragma unroll
+  for (int w = 1; w < kLnBlock / 64; ++w) {
+    ra += red[2 * w];
+    rb += red[2 * w + 1];
+  }
+  __syncthreads();
+  return make_float2(ra, rb);
+}
+
+// The sums of RS rows at once: one pair of barriers for all of them.
+template <int RS, int NT>
+__device__ __forceinline__ void block_sums(float (&s1)[RS], float (&s2)[RS], float* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+  for (int q = 0; q < RS; ++q) {
+    s1[q] = wave_sum(s1[q]);
+    s2[q] = wave_sum(s2[q]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < RS; ++q) {
+      red[(2 * q) * (NT / 64) + wid] = s1[q];
+      red[(2 * q + 1) * (NT / 64) + wid] = s2[q];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < RS; ++q) {
+    float a = red[(2 * q) * (NT / 64)], b = red[(2 * q + 1) * (NT / 64)];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) {
+      a += red[(2 * q) * (NT / 64) + w];
+      b += red[(2 * q + 1) * (NT / 64) + w];
+    }
+    s1[q] = a;
+    s2[q] = b;
+  }
+  __syncthreads();
+}
+
+// RS rows per step: their loads are all in flight together (RS * 2 * VPL
+// 16-byte loads per lane) and their sums share one block reduction.
+template <typename Tag, int VPL, int RS, int NT>
+__global__ __launch_bounds__(NT) void ln_bwd_fused_kernel(LnArgs a) {
+  typedef typename Num<Tag>::storage St;
+  constexpr int VEC = 16 / sizeof(St);
+  union V {
+    uint4 u;
+    St s[VEC];
+  };
+  __shared__ float red[2 * RS * NT / 64];
+  const int64_t nv = a.N / VEC;
+  const float invN = 1.0f / (float)a.N;
+  float gam[VPL][VEC], pw[VPL][VEC], pb[VPL][VEC];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int64_t v = threadIdx.x + (int64_t)k * NT;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      gam[k][e] = (a.gamma != nullptr && v < nv) ? load_as<float>(a.gamma, v * VEC + e, a.gamma_dt) : 1.0f;
+      pw[k][e] = 0.f;
+      pb[k][e] = 0.f;
+    }
+  }
+  const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_part;
+  const int64_t r1 = r0 + a.rows_per_part < a.M ? r0 + a.rows_per_part : a.M;
+  for (int64_t rb = r0; rb < r1; rb += RS) {
+    V vd[RS][VPL], vx[RS][VPL];
+    float mu[RS], rs[RS], s1[RS], s2[RS];
+#pragma unroll
+    for (int q = 0; q < RS; ++q) {
+      const int64_t r = rb + q;
+      if (r < r1) {
+        const V* pdy = (const V*)((const St*)a.dy + r * a.N);
+        const V* px = (const V*)((const St*)a.x + r * a.N);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+          const int64_t v = threadIdx.x + (int64_t)k * NT;
+          if (v < nv) {
+            vd[q][k] = ld_stream(pdy + v);
+            vx[q][k] = ld_stream(px + v);
+          }
+        }
+        mu[q] = load_as<float>(a.mean, r, a.mean_dt);
+        rs[q] = load_as<float>(a.rstd, r, a.mean_dt);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RS; ++q) {
+      s1[q] = 0.f;
+      s2[q] = 0.f;
+      if (rb + q < r1) {
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+          if (threadIdx.x + (int64_t)k * NT < nv) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+              const float dy = Num<Tag>::load(vd[q][k].s[e]);
+              const float xh = (Num<Tag>::load(vx[q][k].s[e]) - mu[q]) * rs[q];
+              const float gw = dy * gam[k][e];
+              s1[q] += gw;
+              s2[q] += gw * xh;
+              pw[k][e] += dy * xh;
+              pb[k][e] += dy;
+            }
+          }
+        }
+      }
+    }
+    if (a.need_dx) {
+      block_sums<RS, NT>(s1, s2, red);
+#pragma unroll
+      for (int q = 0; q < RS; ++q) {
+        const int64_t r = rb + q;
+        if (r < r1) {
+          const float m1 = s1[q] * invN, m2 = s2[q] * invN;
+          V* pdx = (V*)((St*)a.dx + r * a.N);
+#pragma unroll
+          for (int k = 0; k < VPL; ++k) {
+            const int64_t v = threadIdx.x + (int64_t)k * NT;
+            if (v < nv) {
+              V o;
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) {
+                const float dy = Num<Tag>::load(vd[q][k].s[e]);
+                const float xh = (Num<Tag>::load(vx[q][k].s[e]) - mu[q]) * rs[q];
+                o.s[e] = Num<Tag>::store(rs[q] * (dy * gam[k][e] - m1 - xh * m2));
+              }
+              st_stream(pdx + v, o);
+            }
+          }
+        }
+      }
+    }
+  }
+  if (a.need_dw || a.need_db) {
+    float* pwr = a.part + (int64_t)blockIdx.x * 2 * a.N;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int64_t v = threadIdx.x + (int64_t)k * NT;
+      if (v < nv) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          pwr[v * VEC + e] = pw[k][e];
+          pwr[a.N + v * VEC + e] = pb[k][e];
+        }
+      }
+    }
+  }
+}
+
+// dx of one row per block, any N (the row is read twice).
+template <typename Tag>
+__global__ __launch_bounds__(kLnBlock) void ln_bwd_row_kernel(LnArgs a) {
+  typedef typename Num<Tag>::storage St;
+  __shared__ float red[2 * kLnBlock / 64];
+  const int64_t r = blockIdx.x;
+  const St* dy = (const St*)a.dy + r * a.N;
+  const St* x = (const St*)a.x + r * a.N;
+  const float mu = load_as<float>(a.mean, r, a.mean_dt);
+  const float rs = load_as<float>(a.rstd, r, a.mean_dt);
+  float s1 = 0.f, s2 = 0.f;
+  for (int64_t j = threadIdx.x; j < a.N; j += kLnBlock) {
+    const float g = a.gamma != nullptr ? load_as<float>(a.gamma, j, a.gamma_dt) : 1.0f;
+    const float gw = Num<Tag>::load(dy[j]) * g;
+    s1 += gw;
+    s2 += gw * (Num<Tag>::load(x[j]) - mu) * rs;
+  }
+  const float2 s = block_sum2(s1, s2, red);
+  const float m1 = s.x / (float)a.N, m2 = s.y / (float)a.N;
+  St* dx = (St*)a.dx + r * a.N;
+  for (int64_t j = threadIdx.x; j < a.N; j += kLnBlock) {
+    const float g = a.gamma != nullptr ? load_as<float>(a.gamma, j, a.gamma_dt) : 1.0f;
+    const float xh = (Num<Tag>::load(x[j]) - mu) * rs;
+    dx[j] = Num<Tag>::store(rs * (Num<Tag>::load(dy[j]) * g - m1 - xh * m2));
+  }
+}
+
+// Column partials for dgamma / dbeta: block (cx, p) sums rows_per_part rows
+// starting at p * rows_per_part for 256 columns.
+template <typename Tag>
+__global__ __launch_bounds__(kLnBlock) void ln_bwd_col_kernel(LnArgs a) {
+  typedef typename Num<Tag>::storage St;
+  const int64_t j = (int64_t)blockIdx.x * kLnBlock + threadIdx.x;
+  const int64_t p = blockIdx.y;
+  if (j >= a.N) return;
+  const int64_t r0 = p * a.rows_per_part;
+  const int64_t r1 = r0 + a.rows_per_part < a.M ? r0 + a.rows_per_part : a.M;
+  float sw = 0.f, sb = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float dy = Num<Tag>::load(((const St*)a.dy)[r * a.N + j]);
+    const float xh = (Num<Tag>::load(((const St*)a.x)[r * a.N + j]) -
+                      load_as<float>(a.mean, r, a.mean_dt)) *
+                     load_as<float>(a.rstd, r, a.mean_dt);
+    sw += dy * xh;
+    sb += dy;
+  }
+  a.part[p * 2 * a.N + j] = sw;
+  a.part[p * 2 * a.N + a.N + j] = sb;
+}
+
+// dgamma / dbeta: the partial rows added in order.  A block owns 64 columns;
+// its 16 groups of 64 lanes take every 16th partial row (256 contiguous
+// bytes per row and group), and the groups' sums are added in group order.
+constexpr int kFinCols = 64, kFinGroups = 16;
+
+__global__ __launch_bounds__(kFinCols * kFinGroups) void ln_bwd_finish_kernel(
+    const float* __restrict__ part, int64_t nparts, int64_t N, void* dw, int dw_dt, void* db,
+    int db_dt) {
+  __shared__ float sw[kFinGroups][kFinCols], sb[kFinGroups][kFinCols];
+  const int lane = threadIdx.x % kFinCols, grp = threadIdx.x / kFinCols;
+  const int64_t j = (int64_t)blockIdx.x * kFinCols + lane;
+  float w = 0.f, b = 0.f;
+  if (j < N) {
+    for (int64_t p = grp; p < nparts; p += kFinGroups) {
+      w += part[p * 2 * N + j];
+      b += part[p * 2 * N + N + j];
+    }
+  }
+  sw[grp][lane] = w;
+  sb[grp][lane] = b;
+  __syncthreads();
+  if (grp == 0 && j < N) {
+    float tw = sw[0][lane], tb = sb[0][lane];
+#pragma unroll
+    for (int q = 1; q < kFinGroups; ++q) {
+      tw += sw[q][lane];
+      tb += sb[q][lane];
+    }
+    if (dw != nullptr) store_as<float>(dw, j, dw_dt, tw);
+    if (db != nullptr) store_as<float>(db, j, db_dt, tb);
+  }
+}
+
+template <typename Tag>
+mi_status_t launch_ln_bwd(LnArgs& a, void* dw, int dw_dt, void* db, int db_dt,
+                          hipStream_t stream) {
+  typedef typename Num<Tag>::storage St;
+  constexpr int VEC = 16 / sizeof(St);
+  const bool cols = a.need_dw || a.need_db;
+  const uintptr_t bits = (uintptr_t)a.dy | (uintptr_t)a.x | (uintptr_t)a.dx;
+  const int64_t nv = a.N / VEC;
+  const bool fused = a.N % VEC == 0 && bits % 16 == 0 && nv <= (int64_t)512 * kLnMaxVpl;
+  Workspace ws;
+  int64_t nparts = 0;
+  if (fused) {
+    a.rows_per_part = kLnRows;
+    if ((a.M + kLnRows - 1) / kLnRows > kLnMaxParts) a.rows_per_part = (a.M + kLnMaxParts - 1) / kLnMaxParts;
+    const int64_t blocks = (a.M + a.rows_per_part - 1) / a.rows_per_part;
+    if (cols) {
+      nparts = blocks;
+      MI_RETURN_IF(ws.alloc((size_t)(nparts * 2 * a.N) * sizeof(float), stream));
+      a.part = (float*)ws.get();
+    }
+    auto go = [&](auto vpl_c, auto rs_c, auto nt_c) -> mi_status_t {
+      constexpr int VPL = decltype(vpl_c)::value;
+      constexpr int RS = decltype(rs_c)::value;
+      constexpr int NT = decltype(nt_c)::value;
+      hipLaunchKernelGGL((ln_bwd_fused_kernel<Tag, VPL, RS, NT>), dim3((unsigned)blocks),
+                         dim3(NT), 0, stream, a);
+      return check_launch("layer_norm_backward");
+    };
+    // measured on bf16 [16384, 4096]: 512 lanes, 2 rows a step and 32 rows
+    // a block take 99 us (4.1 TB/s with the finish pass) against 108-158 us
+    // for 256 lanes or 1, 4 rows a step, 16 or 64 rows a block
+    typedef std::integral_constant<int, 1> I1;
+    typedef std::integral_constant<int, 2> I2;
+    typedef std::integral_constant<int, 4> I4;
+    typedef std::integral_constant<int, 256> T256;
+    typedef std::integral_constant<int, 512> T512;
+    if (nv <= 256) MI_RETURN_IF(go(I1(), I2(), T256()));
+    else if (nv <= 512) MI_RETURN_IF(go(I1(), I2(), T512()));
+    else if (nv <= 1024) MI_RETURN_IF(go(I2(), I2(), T512()));
+    else MI_RETURN_IF(go(I4(), I1(), T512()));
+  } else {
+    if (a.need_dx) {
+      MI_CHECK_ARG(a.M <= 0x7fffffffLL, "layer_norm_backward: too many rows");
+      hipLaunchKernelGGL((ln_bwd_row_kernel<Tag>), dim3((unsigned)a.M), dim3(kLnBlock), 0, stream,
+                         a);
+      MI_RETURN_IF(check_launch("layer_norm_backward rows"));
+    }
+    if (cols) {
+      a.rows_per_part = kLnColRows;
+      if ((a.M + kLnColRows - 1) / kLnColRows > kLnMaxParts)
+        a.rows_per_part = (a.M + kLnMaxParts - 1) / kLnMaxParts;
+      nparts = (a.M + a.rows_per_part - 1) / a.rows_per_part;
+      MI_RETURN_IF(ws.alloc((size_t)(nparts * 2 * a.N) * sizeof(float), stream));
+      a.part = (float*)ws.get();
+      hipLaunchKernelGGL((ln_bwd_col_kernel<Tag>), dim3(ceil_div_u(a.N, kLnBlock), (unsigned)nparts),
+                         dim3(kLnBlock), 0, stream, a);
+      MI_RETURN_IF(check_launch("layer_norm_backward columns"));
+    }
+  }
+  if (cols) {
+    hipLaunchKernelGGL(ln_bwd_finish_kernel, dim3(ceil_div_u(a.N, kFinCols)),
+                       dim3(kFinCols * kFinGroups), 0, stream,
+                       (const float*)a.part, nparts, a.N, dw, dw_dt, db, db_dt);
+    MI_RETURN_IF(check_launch("layer_norm_backward finish"));
+  }
+  return MI_OK;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" mi_status_t mi_layer_norm_backward(
+    const mi_tensor_t* grad_input, const mi_tensor_t* grad_weight, const mi_tensor_t* grad_bias,
+    const mi_tensor_t* grad_out, const mi_tensor_t* input, const mi_tensor_t* mean,
+    const mi_tensor_t* rstd, const mi_tensor_t* weight, int64_t normalized_numel,
+    mi_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = (hipStream_t)stream_;
+  MI_RETURN_IF(validate(grad_out, "grad_out"));
+  MI_RETURN_IF(validate(input, "input"));
+  MI_RETURN_IF(validate(mean, "mean"));
+  MI_RETURN_IF(validate(rstd, "rstd"));
+  const int dt = input->dtype;
+  MI_CHECK_ARG(dt == MI_F32 || dt == MI_BF16 || dt == MI_F16,
+               "layer_norm_backward: input dtype %s unsupported", dtype_name(dt));
+  MI_CHECK_ARG(grad_out->dtype == dt, "layer_norm_backward: grad_out must have input's dtype");
+  MI_CHECK_ARG(is_contiguous(*input) && is_contiguous(*grad_out),
+               "layer_norm_backward: input and grad_out must be contiguous");
+  const int64_t total = numel(*input);
+  MI_CHECK_ARG(numel(*grad_out) == total, "layer_norm_backward: grad_out size mismatch");
+  const int64_t N = normalized_numel;
+  MI_CHECK_ARG(N >= 1 && total % N == 0, "layer_norm_backward: %lld elements do not form rows of %lld",
+               (long long)total, (long long)N);
+  const int64_t M = total / N;
+  MI_CHECK_ARG(numel(*mean) == M && numel(*rstd) == M && is_contiguous(*mean) && is_contiguous(*rstd),
+               "layer_norm_backward: mean and rstd must be contiguous with %lld elements", (long long)M);
+  MI_CHECK_ARG(mean->dtype == rstd->dtype && (mean->dtype == MI_F32 || mean->dtype == dt),
+               "layer_norm_backward: mean and rstd must be fp32 or the input's dtype");
+  const bool has_w = weight != nullptr && weight->data != nullptr;
+  if (has_w) {
+    MI_RETURN_IF(validate(weight, "weight"));
+    MI_CHECK_ARG(numel(*weight) == N && is_contiguous(*weight) &&
+                     (weight->dtype == dt || weight->dtype == MI_F32),
+                 "layer_norm_backward: weight must be contiguous with %lld elements of the input's "
+                 "dtype or fp32", (long long)N);
+  }
+  const bool need_dx = grad_input != nullptr && grad_input->data != nullptr;
+  const bool need_dw = grad_weight != nullptr && grad_weight->data != nullptr;
+  const bool need_db = grad_bias != nullptr && grad_bias->data != nullptr;
+  if (need_dx) {
+    MI_RETURN_IF(validate(grad_input, "grad_input"));
+    MI_CHECK_ARG(grad_input->dtype == dt && numel(*grad_input) == total && is_contiguous(*grad_input),
+                 "layer_norm_backward: grad_input must be contiguous like input");
+  }
+  if (need_dw) {
+    MI_RETURN_IF(validate(grad_weight, "grad_weight"));
+    MI_CHECK_ARG(numel(*grad_weight) == N && is_contiguous(*grad_weight) &&
+                     (grad_weight->dtype == MI_F32 || grad_weight->dtype == MI_BF16 ||
+                      grad_weight->dtype == MI_F16),
+                 "layer_norm_backward: grad_weight must be contiguous with %lld elements", (long long)N);
+  }
+  if (need_db) {
+    MI_RETURN_IF(validate(grad_bias, "grad_bias"));
+    MI_CHECK_ARG(numel(*grad_bias) == N && is_contiguous(*grad_bias) &&
+                     (grad_bias->dtype == MI_F32 || grad_bias->dtype == MI_BF16 ||
+                      grad_bias->dtype == MI_F16),
+                 "layer_norm_backward: grad_bias must be contiguous with %lld elements", (long long)N);
+  }
+  if (total == 0) {
+    // no rows: dgamma and dbeta are zero
+    if (need_dw && N > 0) MI_RETURN_IF(mi_fill(grad_weight, mi_scalar_t{0.0, 0, MI_F32, 1}, stream_));
+    if (need_db && N > 0) MI_RETURN_IF(mi_fill(grad_bias, mi_scalar_t{0.0, 0, MI_F32, 1}, stream_));
+    return MI_OK;
+  }
+  if (!need_dx && !need_dw && !need_db) return MI_OK;
+  LnArgs a{};
+  a.dx = need_dx ? grad_input->data : nullptr;
+  a.dy = grad_out->data;
+  a.x = input->data;
+  a.mean = mean->data;
+  a.rstd = rstd->data;
+  a.gamma = has_w ? weight->data : nullptr;
+  a.M = M;
+  a.N = N;
+  a.mean_dt = mean->dtype;
+  a.gamma_dt = has_w ? weight->dtype : MI_F32;
+  a.need_dx = need_dx;
+  a.need_dw = need_dw;
+  a.need_db = need_db;
+  void* dw = need_dw ? grad_weight->data : nullptr;
+  void* db = need_db ? grad_bias->data : nullptr;
+  const int dw_dt = need_dw ? grad_weight->dtype : MI_F32;
+  const int db_dt = need_db ? grad_bias->dtype : MI_F32;
+  switch (dt) {
+    case MI_BF16: return launch_ln_bwd<BF16>(a, dw, dw_dt, db, db_dt, stream);
+    case MI_F16: return launch_ln_bwd<F16>(a, dw, dw_dt, db, db_dt, stream);
+    default: return launch_ln_bwd<float>(a, dw, dw_dt, db, db_dt, stream);
+  }
+}

@@ -288,6 +288,195 @@ mi_status_t launch_t(const mi_tensor_t* out, const mi_tensor_t* self, int dim,
   return check_launch("softmax_col");
 }
 
+// ---- backward ---------------------------------------------------------------
+//   log_softmax: gi = dy - exp(y) * sum(dy)        softmax: gi = y * (dy - sum(dy * y))
+// with y the forward output, the row sums in float (ATen's
+// _log_softmax_backward_data / _softmax_backward_data,
+// aten/src/ATen/native/cpu/SoftMaxKernel.cpp, _vec_log_softmax_backward and
+// _vec_softmax_backward).  Same layouts as the forward: a register-resident
+// row for dense aligned rows, a two-read row kernel, one lane per column.
+template <typename InTag, bool LOG>
+__device__ __forceinline__ float bwd_term(float dy, float y) {
+  return LOG ? dy : dy * y;
+}
+template <typename InTag, bool LOG>
+__device__ __forceinline__ float bwd_out(float dy, float y, float s) {
+  if constexpr (LOG) return dy - kexp<InTag>(y) * s;
+  else return y * (dy - s);
+}
+
+template <typename InTag, typename OutTag, int NTH, int VPT, bool LOG>
+__global__ __launch_bounds__(NTH) void softmax_bwd_reg_kernel(
+    typename ST<OutTag>::storage* __restrict__ gi, const typename ST<InTag>::storage* __restrict__ dy,
+    const typename ST<InTag>::storage* __restrict__ y, int64_t D) {
+  typedef typename ST<InTag>::storage Si;
+  typedef typename ST<OutTag>::storage So;
+  constexpr int VEC = 16 / sizeof(Si);
+  __shared__ float red[NTH / 64];
+  union Vi {
+    uint4 u;
+    Si s[VEC];
+  };
+  // a narrower output (float grads into half) writes 8 bytes per vector
+  constexpr int kBytes = sizeof(So) * VEC;
+  static_assert(kBytes == 8 || kBytes % 16 == 0, "output vector of 8 or 16k bytes");
+  union Vo {
+    So s[VEC];
+    uint2 h[kBytes / 8];
+    uint4 u[(kBytes + 15) / 16];
+  };
+  const int64_t row = blockIdx.x;
+  const Vi* pd = (const Vi*)(dy + row * D);
+  const Vi* py = (const Vi*)(y + row * D);
+  const int nv = (int)(D / VEC);
+  Vi xd[VPT], xy[VPT];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int v = threadIdx.x + k * NTH;
+    if (v < nv) {
+      xd[k] = ld_stream(pd + v);
+      xy[k] = ld_stream(py + v);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    if ((int)threadIdx.x + k * NTH < nv) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        s += bwd_term<InTag, LOG>(ST<InTag>::load(xd[k].s[e]), ST<InTag>::load(xy[k].s[e]));
+    }
+  }
+  s = block_fsum<NTH>(s, red);
+  So* po = gi + row * D;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int v = threadIdx.x + k * NTH;
+    if (v < nv) {
+      Vo o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        o.s[e] = ST<OutTag>::store(
+            bwd_out<InTag, LOG>(ST<InTag>::load(xd[k].s[e]), ST<InTag>::load(xy[k].s[e]), s));
+      if constexpr (kBytes == 8) {
+        *(uint2*)(po + (int64_t)v * VEC) = o.h[0];
+      } else {
+#pragma unroll
+        for (int w = 0; w < kBytes / 16; ++w) st_stream((uint4*)(po + (int64_t)v * VEC) + w, o.u[w]);
+      }
+    }
+  }
+}
+
+template <typename InTag, typename OutTag, bool LOG>
+__global__ __launch_bounds__(kBlock) void softmax_bwd_row_kernel(
+    typename ST<OutTag>::storage* __restrict__ gi, const typename ST<InTag>::storage* __restrict__ dy,
+    const typename ST<InTag>::storage* __restrict__ y, int64_t D) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const typename ST<InTag>::storage* pd = dy + row * D;
+  const typename ST<InTag>::storage* py = y + row * D;
+  float s = 0.f;
+  for (int64_t j = threadIdx.x; j < D; j += kBlock)
+    s += bwd_term<InTag, LOG>(ST<InTag>::load(pd[j]), ST<InTag>::load(py[j]));
+  s = block_sum_f(s, red);
+  typename ST<OutTag>::storage* po = gi + row * D;
+  for (int64_t j = threadIdx.x; j < D; j += kBlock)
+    po[j] = ST<OutTag>::store(bwd_out<InTag, LOG>(ST<InTag>::load(pd[j]), ST<InTag>::load(py[j]), s));
+}
+
+template <typename InTag, typename OutTag, bool LOG>
+__global__ __launch_bounds__(kBlock) void softmax_bwd_col_kernel(
+    typename ST<OutTag>::storage* __restrict__ gi, const typename ST<InTag>::storage* __restrict__ dy,
+    const typename ST<InTag>::storage* __restrict__ y, int64_t outer, int64_t D, int64_t inner) {
+  const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (t >= outer * inner) return;
+  const int64_t o = t / inner, i = t - o * inner;
+  const int64_t base = o * D * inner + i;
+  float s = 0.f;
+  for (int64_t j = 0; j < D; ++j)
+    s += bwd_term<InTag, LOG>(ST<InTag>::load(dy[base + j * inner]), ST<InTag>::load(y[base + j * inner]));
+  for (int64_t j = 0; j < D; ++j) {
+    const int64_t q = base + j * inner;
+    gi[q] = ST<OutTag>::store(bwd_out<InTag, LOG>(ST<InTag>::load(dy[q]), ST<InTag>::load(y[q]), s));
+  }
+}
+
+template <typename InTag, typename OutTag, bool LOG>
+mi_status_t launch_bwd_t(const mi_tensor_t* gi, const mi_tensor_t* dy, const mi_tensor_t* y,
+                         int dim, hipStream_t stream) {
+  typedef typename ST<InTag>::storage Si;
+  typedef typename ST<OutTag>::storage So;
+  const int nd = y->ndim;
+  int64_t outer = 1, inner = 1;
+  const int64_t D = nd == 0 ? 1 : y->sizes[dim];
+  for (int d = 0; d < dim; ++d) outer *= y->sizes[d];
+  for (int d = dim + 1; d < nd; ++d) inner *= y->sizes[d];
+  if (outer * inner == 0 || D == 0) return MI_OK;
+  if (inner == 1) {
+    constexpr int VEC = 16 / sizeof(Si);
+    const bool aligned = (((uintptr_t)dy->data | (uintptr_t)y->data | (uintptr_t)gi->data) % 16 == 0) &&
+                         (D % VEC == 0);
+    const int64_t nv = D / VEC;
+    auto run_reg = [&](auto nth_c, auto vpt_c) -> mi_status_t {
+      constexpr int NTH = decltype(nth_c)::value;
+      constexpr int VPT = decltype(vpt_c)::value;
+      hipLaunchKernelGGL((softmax_bwd_reg_kernel<InTag, OutTag, NTH, VPT, LOG>),
+                         dim3((unsigned)outer), dim3(NTH), 0, stream, (So*)gi->data,
+                         (const Si*)dy->data, (const Si*)y->data, D);
+      return check_launch("softmax_bwd_reg");
+    };
+    typedef std::integral_constant<int, 1> V1;
+    typedef std::integral_constant<int, 1024> N1024;
+    // two row operands in registers: up to 8 vectors of each per lane
+    if (aligned && nv <= 1024 * 8 && outer <= 0x7fffffff) {
+      if (nv <= 256) return run_reg(std::integral_constant<int, 256>(), V1());
+      if (nv <= 512) return run_reg(std::integral_constant<int, 512>(), V1());
+      if (nv <= 1024) return run_reg(N1024(), V1());
+      if (nv <= 2048) return run_reg(N1024(), std::integral_constant<int, 2>());
+      if (nv <= 4096) return run_reg(N1024(), std::integral_constant<int, 4>());
+      return run_reg(N1024(), std::integral_constant<int, 8>());
+    }
+    hipLaunchKernelGGL((softmax_bwd_row_kernel<InTag, OutTag, LOG>), dim3((unsigned)outer),
+                       dim3(kBlock), 0, stream, (So*)gi->data, (const Si*)dy->data,
+                       (const Si*)y->data, D);
+    return check_launch("softmax_bwd_row");
+  }
+  hipLaunchKernelGGL((softmax_bwd_col_kernel<InTag, OutTag, LOG>),
+                     dim3(ceil_div_u(outer * inner, kBlock)), dim3(kBlock), 0, stream,
+                     (So*)gi->data, (const Si*)dy->data, (const Si*)y->data, outer, D, inner);
+  return check_launch("softmax_bwd_col");
+}
+
+template <bool LOG>
+mi_status_t run_softmax_bwd(const mi_tensor_t* gi, const mi_tensor_t* dy, const mi_tensor_t* y,
+                            int64_t dim, hipStream_t stream) {
+  clear_error();
+  MI_RETURN_IF(validate(gi, "grad_input"));
+  MI_RETURN_IF(validate(dy, "grad_output"));
+  MI_RETURN_IF(validate(y, "output"));
+  const int nd = y->ndim;
+  const int lim = nd == 0 ? 1 : nd;
+  if (dim < 0) dim += lim;
+  MI_CHECK_ARG(dim >= 0 && dim < lim, "softmax_backward: dim out of range");
+  MI_CHECK_ARG(gi->ndim == nd && dy->ndim == nd, "softmax_backward: rank mismatch");
+  for (int d = 0; d < nd; ++d)
+    MI_CHECK_ARG(gi->sizes[d] == y->sizes[d] && dy->sizes[d] == y->sizes[d],
+                 "softmax_backward: shape mismatch");
+  if (numel(*y) == 0) return MI_OK;
+  if (!is_contiguous(*gi) || !is_contiguous(*dy) || !is_contiguous(*y))
+    MI_FAIL(MI_ERR_UNSUPPORTED, "softmax_backward: operands must be contiguous");
+  MI_CHECK_ARG(dy->dtype == y->dtype, "softmax_backward: grad_output and output must share a dtype");
+  const int di = y->dtype, dout = gi->dtype;
+  const int d = nd == 0 ? 0 : (int)dim;
+  if (di == MI_BF16 && dout == MI_BF16) return launch_bwd_t<BF16, BF16, LOG>(gi, dy, y, d, stream);
+  if (di == MI_F16 && dout == MI_F16) return launch_bwd_t<F16, F16, LOG>(gi, dy, y, d, stream);
+  if (di == MI_F32 && dout == MI_F32) return launch_bwd_t<float, float, LOG>(gi, dy, y, d, stream);
+  if (di == MI_F32 && dout == MI_BF16) return launch_bwd_t<float, BF16, LOG>(gi, dy, y, d, stream);
+  if (di == MI_F32 && dout == MI_F16) return launch_bwd_t<float, F16, LOG>(gi, dy, y, d, stream);
+  MI_FAIL(MI_ERR_UNSUPPORTED, "softmax_backward: dtype %s -> %s", dtype_name(di), dtype_name(dout));
+}
+
 template <bool LOG>
 mi_status_t run_softmax(const mi_tensor_t* out, const mi_tensor_t* self, int64_t dim,
                         hipStream_t stream) {
@@ -330,6 +519,16 @@ mi_status_t mi_softmax(const mi_tensor_t* out, const mi_tensor_t* self, int64_t 
 mi_status_t mi_log_softmax(const mi_tensor_t* out, const mi_tensor_t* self, int64_t dim,
                            mi_stream_t stream) {
   return run_softmax<true>(out, self, dim, (hipStream_t)stream);
+}
+
+mi_status_t mi_log_softmax_backward(const mi_tensor_t* grad_input, const mi_tensor_t* grad_output,
+                                    const mi_tensor_t* output, int64_t dim, mi_stream_t stream) {
+  return run_softmax_bwd<true>(grad_input, grad_output, output, dim, (hipStream_t)stream);
+}
+
+mi_status_t mi_softmax_backward(const mi_tensor_t* grad_input, const mi_tensor_t* grad_output,
+                                const mi_tensor_t* output, int64_t dim, mi_stream_t stream) {
+  return run_softmax_bwd<false>(grad_input, grad_output, output, dim, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -73,6 +73,10 @@ _SIGNATURES = {
     "mi_copy": ([_T, _T, _S], ctypes.c_int),
     "mi_fill": ([_T, MiScalar, _S], ctypes.c_int),
     "mi_cat": ([_T, ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_int32, _S], ctypes.c_int),
+    "mi_silu_backward": ([_T, _T, _T, _S], ctypes.c_int),
+    "mi_log_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
+    "mi_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
+    "mi_layer_norm_backward": ([_T] * 8 + [ctypes.c_int64, _S], ctypes.c_int),
     "mi_fused_adamw": ([ctypes.POINTER(_T)] * 6 + [ctypes.c_int32, _T, ctypes.POINTER(MiAdamwHparams),
                                                    _T, _T, _S], ctypes.c_int),
     "mi_add": ([_T, _T, _T, MiScalar, _S], ctypes.c_int),
@@ -238,6 +242,33 @@ def fused_adamw(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_ste
     check("mi_fused_adamw", lib().mi_fused_adamw(
         *arrays, n, lr_d, ctypes.byref(hp), gs_d, fi_d,
         stream_of(params[0]) if n else torch.cuda.current_stream().cuda_stream))
+
+
+def silu_backward(grad_input, grad_output, self):
+    check("mi_silu_backward", lib().mi_silu_backward(desc(grad_input), desc(grad_output), desc(self),
+                                                     stream_of(grad_input)))
+    return grad_input
+
+
+def log_softmax_backward(grad_input, grad_output, output, dim):
+    check("mi_log_softmax_backward", lib().mi_log_softmax_backward(
+        desc(grad_input), desc(grad_output), desc(output), dim, stream_of(grad_input)))
+    return grad_input
+
+
+def softmax_backward(grad_input, grad_output, output, dim):
+    check("mi_softmax_backward", lib().mi_softmax_backward(
+        desc(grad_input), desc(grad_output), desc(output), dim, stream_of(grad_input)))
+    return grad_input
+
+
+def layer_norm_backward(grad_input, grad_weight, grad_bias, grad_out, x, mean, rstd, weight,
+                        normalized_numel):
+    """Any of grad_input / grad_weight / grad_bias / weight may be None."""
+    opt = [desc(t) if t is not None else None for t in (grad_input, grad_weight, grad_bias)]
+    check("mi_layer_norm_backward", lib().mi_layer_norm_backward(
+        *opt, desc(grad_out), desc(x), desc(mean), desc(rstd),
+        desc(weight) if weight is not None else None, normalized_numel, stream_of(x)))
 
 
 def fill_(out, value, dtype=None):
