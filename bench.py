@@ -402,6 +402,11 @@ def backward_ops(torch, _abi):
         sets.append({"dy": torch.randn(M, N, generator=gen).bfloat16().cuda(), "x": x,
                      "mean": mean, "rstd": rstd})
     dx = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    mo = torch.empty(M, 1, dtype=torch.bfloat16, device="cuda")
+    ro = torch.empty(M, 1, dtype=torch.bfloat16, device="cuda")
+    res.append(bench_op(torch, "f4.layer_norm fwd bf16 [16384,4096] (out, mean, rstd)", sets,
+                        lambda s: _abi.layer_norm(dx, mo, ro, s["x"], w, w, N, 1e-5),
+                        M * N * 4 + M * 4 + N * 4))
     dw, db = torch.empty_like(w), torch.empty_like(w)
     res.append(bench_op(torch, "f4.layer_norm_backward bf16 [16384,4096] (dx, dgamma, dbeta)", sets,
                         lambda s: _abi.layer_norm_backward(dx, dw, db, s["dy"], s["x"], s["mean"],

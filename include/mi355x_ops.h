@@ -343,6 +343,17 @@ mi_status_t mi_silu_backward(const mi_tensor_t* grad_input,
                              const mi_tensor_t* grad_output,
                              const mi_tensor_t* self, mi_stream_t stream);
 
+/* native_layer_norm over rows of normalized_numel elements: mean, biased
+ * variance and rstd = 1 / sqrt(var + eps) in fp32 (stored in mean / rstd,
+ * fp32 or the input's dtype, one element per row), out = (x - mean) * rstd *
+ * weight + bias with the fp32 statistics; weight and bias optional, fp32 or
+ * the input's dtype.  Contiguous f32 / bf16 / f16 input and out.  Replaces
+ * topsatenNativeLayerNorm (yaml native_layer_norm :481). */
+mi_status_t mi_layer_norm(const mi_tensor_t* out, const mi_tensor_t* mean,
+                          const mi_tensor_t* rstd, const mi_tensor_t* input,
+                          const mi_tensor_t* weight, const mi_tensor_t* bias,
+                          int64_t normalized_numel, double eps, mi_stream_t stream);
+
 /* native_layer_norm_backward over rows of normalized_numel elements: with
  * xh = (x - mean) * rstd and gw = dy * weight,
  *   grad_input  = rstd * (gw - mean_row(gw) - xh * mean_row(gw * xh))

@@ -155,6 +155,32 @@ def test_layer_norm_backward_parity(shape, dt, wdt, affine):
             assert_close(got[2].cpu(), torch.from_numpy(rdb).to(wdt), "bf16", f"dbeta {shape}")
 
 
+_LNF_CASES = [
+    ((16384, 4096), [4096], torch.bfloat16, torch.bfloat16),  # register rows, bf16 statistics
+    ((512, 1000), [1000], torch.float32, torch.float32),
+    ((64, 12288), [12288], torch.bfloat16, torch.float32),   # fp32 parameters: fp32 statistics
+    ((8, 20000), [20000], torch.bfloat16, torch.bfloat16),   # rows read three times
+    ((6, 5, 7), [5, 7], torch.float32, None),                 # two normalized dims, no affine
+]
+
+
+@pytest.mark.parametrize("shape,nshape,dt,wdt", _LNF_CASES)
+def test_layer_norm_forward_parity(shape, nshape, dt, wdt):
+    n = 1
+    for d in nshape:
+        n *= d
+    x = rn(shape, dt, 50, 2.0) + 0.3
+    w = rn(nshape, wdt, 51) if wdt is not None else None
+    b = rn(nshape, wdt, 52) if wdt is not None else None
+    want = aten.layer_norm_forward(x, nshape, w, b, 1e-5)
+    dev = lambda t: None if t is None else t.to("gcu")  # noqa: E731
+    got = torch.native_layer_norm(dev(x), nshape, dev(w), dev(b), 1e-5)
+    for i, name in enumerate(("out", "mean", "rstd")):
+        assert got[i].shape == want[i].shape and got[i].dtype == want[i].dtype, (name, got[i].dtype)
+        assert_close(got[i].cpu(), want[i], bar(want[i].dtype if want[i].dtype != torch.float16
+                                                else torch.bfloat16), f"{name} {shape}")
+
+
 def test_layer_norm_backward_masks_and_no_rows():
     x = rn((256, 512), torch.float32, 30)
     w, b = rn((512,), torch.float32, 31), rn((512,), torch.float32, 32)
@@ -211,5 +237,6 @@ def test_autograd_layer_norm_silu_log_softmax_on_gcu():
     assert_close(gx.cpu(), rx, "fp32", "dx")
     assert_close(gw.cpu(), rw, "fp32", "dgamma")
     assert_close(gb.cpu(), rb, "fp32", "dbeta")
-    for op in ("native_layer_norm_backward", "silu_backward", "_log_softmax_backward_data"):
+    for op in ("native_layer_norm", "native_layer_norm_backward", "silu_backward",
+               "_log_softmax_backward_data"):
         assert stats.get(op, (0, 0))[0] >= 1 and stats.get(op, (0, 0))[1] == 0, (op, stats)

@@ -666,7 +666,12 @@ def test_backward_ops_abi(dtype):
     _abi.softmax_backward(out, dev(dy), dev(p), -1)
     assert_close(out, aten.softmax_backward(dy, p, -1, dtype), kind, "softmax_backward")
     w, b = rand((1024,), dtype, 92), rand((1024,), dtype, 93)
-    _, mean, rstd = aten.layer_norm_forward(x, [1024], w, b, 1e-5)
+    y_ref, mean, rstd = aten.layer_norm_forward(x, [1024], w, b, 1e-5)
+    m_dev, r_dev = torch.empty(300, 1, dtype=dtype, device=DEV), torch.empty(300, 1, dtype=dtype, device=DEV)
+    _abi.layer_norm(out, m_dev, r_dev, dev(x), dev(w), dev(b), 1024, 1e-5)
+    assert_close(out, y_ref, kind, "layer_norm")
+    assert_close(m_dev, mean, kind, "layer_norm mean")
+    assert_close(r_dev, rstd, kind, "layer_norm rstd")
     want = aten.layer_norm_backward(dy, x, [1024], mean, rstd, w, b, [True, True, True])
     dw, db = torch.empty(1024, dtype=dtype, device=DEV), torch.empty(1024, dtype=dtype, device=DEV)
     _abi.layer_norm_backward(out, dw, db, dev(dy), dev(x), dev(mean), dev(rstd), dev(w), 1024)

@@ -1,7 +1,8 @@
 // The training-side backward ops the reference registers natively but sends
 // to CPU on its s60 hardware (codegen/gcu_op_fallback.yaml:22-41):
 // silu_backward, _log_softmax_backward_data / _softmax_backward_data and
-// native_layer_norm_backward.  Shape and dtype rules are ATen's (the
+// native_layer_norm_backward, and the layer-norm forward whose statistics
+// that backward takes (native_layer_norm, yaml :481).  Shape and dtype rules are ATen's (the
 // structured meta functions where the op has one); the arithmetic is the
 // gfx950 kernels'.  dtypes the kernels do not cover run through the CPU
 // fallback, as every unregistered op does.
@@ -134,6 +135,49 @@ at::Tensor& _softmax_backward_data_out(const at::Tensor& grad_output, const at::
         grad_output, output, dim, input_dtype, grad_input);
   softmax_bwd_into(false, grad_output, output, dim, grad_input);
   return grad_input;
+}
+
+// ATen's layer_norm_cpu contract: _check_layer_norm_inputs, mean and rstd
+// fp32 when a 16-bit input meets fp32 parameters ("mixed type") and of the
+// input's dtype otherwise, shaped [leading dims..., 1, ...].
+std::tuple<at::Tensor, at::Tensor, at::Tensor> native_layer_norm(
+    const at::Tensor& input, at::IntArrayRef normalized_shape,
+    const std::optional<at::Tensor>& weight, const std::optional<at::Tensor>& bias, double eps) {
+  const at::Tensor w = weight.has_value() ? *weight : at::Tensor();
+  const at::Tensor b = bias.has_value() ? *bias : at::Tensor();
+  const auto mn = at::native::_check_layer_norm_inputs(input, normalized_shape, w, b);
+  const int64_t N = mn.second;
+  const at::ScalarType dt = input.scalar_type();
+  // a 16-bit input with fp32 weight / bias (ATen's is_mixed_type and
+  // check_mixed_data_type)
+  const bool mixed = (dt == at::kBFloat16 || dt == at::kHalf) &&
+                     ((w.defined() && w.scalar_type() == at::kFloat) ||
+                      (b.defined() && b.scalar_type() == at::kFloat));
+  if (mixed)
+    TORCH_CHECK((!w.defined() || w.scalar_type() == at::kFloat) &&
+                    (!b.defined() || b.scalar_type() == at::kFloat),
+                "mixed dtype (CPU): all inputs must share same datatype.");
+  auto param_ok = [&](const at::Tensor& t) {
+    return !t.defined() || t.scalar_type() == dt || t.scalar_type() == at::kFloat;
+  };
+  if (!float_kernel_dtype(dt) || !param_ok(w) || !param_ok(b))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP(native_layer_norm)>::call(
+        input, normalized_shape, weight, bias, eps);
+  const at::Tensor x = input.contiguous();
+  at::Tensor out = at::empty_like(x, at::MemoryFormat::Contiguous);
+  const int64_t axis = input.dim() - (int64_t)normalized_shape.size();
+  std::vector<int64_t> stat_shape;
+  for (int64_t i = 0; i < input.dim(); ++i) stat_shape.push_back(i < axis ? input.size(i) : 1);
+  const at::ScalarType sdt = mixed ? at::kFloat : dt;
+  at::Tensor mean = at::empty(stat_shape, x.options().dtype(sdt));
+  at::Tensor rstd = at::empty(stat_shape, x.options().dtype(sdt));
+  const at::Tensor gamma = w.defined() ? w.contiguous() : w, beta = b.defined() ? b.contiguous() : b;
+  const mi_tensor_t o = desc(out), m = desc(mean), r = desc(rstd), dx = desc(x), dw = desc(gamma),
+                    db = desc(beta);
+  check_mi(mi_layer_norm(&o, &m, &r, &dx, gamma.defined() ? &dw : nullptr,
+                         beta.defined() ? &db : nullptr, N, eps, mi_stream(x)),
+           "native_layer_norm");
+  return {out, mean, rstd};
 }
 
 // ATen's layer_norm_backward_cpu contract: the checks of

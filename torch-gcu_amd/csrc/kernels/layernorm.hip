@@ -1,3 +1,4 @@
+// native_layer_norm (forward, at the end of this file) and
 // native_layer_norm_backward over the last N elements (normalized_shape
 // flattened): with xh = (x - mean) * rstd and gw = dy * gamma (dy without a
 // weight), per row
@@ -29,6 +30,7 @@ constexpr int kLnRows = 32;       // rows per block (at least), fused path
 constexpr int kLnMaxVpl = 4;      // 16-byte vectors per lane and row (512 lanes), fused path
 constexpr int kLnColRows = 64;    // rows per partial (at least), column pass
 constexpr int64_t kLnMaxParts = 2048;  // partial rows: at most 2048 x 2N floats
+constexpr int kLnFwdRows = 16;         // rows per block, forward
 
 struct LnArgs {
   void* dx;
@@ -356,10 +358,236 @@ mi_status_t launch_ln_bwd(LnArgs& a, void* dw, int dw_dt, void* db, int db_dt,
   return MI_OK;
 }
 
+// ---- forward -------------------------------------------------------------------
+// out = (x - mean) * rstd * gamma + beta over rows of N, mean and
+// rstd = 1 / sqrt(var + eps) (biased variance, two passes over the row held
+// in registers) in fp32, stored in mean_dt; out uses the unrounded fp32 values
+// (ATen's LayerNormKernelImpl does the same with y = x * scale + shift,
+// aten/src/ATen/native/cpu/layer_norm_kernel.cpp).  Rows of up to 2048
+// 16-byte vectors stay in registers, kLnFwdRows rows per block; longer or
+// unaligned rows take one block each and are read three times.
+struct LnFwdArgs {
+  void* out;
+  void* mean;
+  void* rstd;
+  const void* x;
+  const void* gamma;
+  const void* beta;
+  int64_t M, N;
+  float eps;
+  int mean_dt, gamma_dt, beta_dt;
+};
+
+// NT lanes own fixed 16-byte column pieces of every row: gamma and beta are
+// read once per block into registers; rows go RS at a time (their loads in
+// flight together, their sums in one block reduction, two per step: the
+// mean, then the squared deviations).
+template <typename Tag, int VPL, int RS, int NT>
+__global__ __launch_bounds__(NT) void ln_fwd_reg_kernel(LnFwdArgs a) {
+  typedef typename Num<Tag>::storage St;
+  constexpr int VEC = 16 / sizeof(St);
+  union V {
+    uint4 u;
+    St s[VEC];
+  };
+  __shared__ float red[2 * RS * NT / 64];
+  const int64_t nv = a.N / VEC;
+  const float invN = 1.0f / (float)a.N;
+  float gam[VPL][VEC], bet[VPL][VEC];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int64_t v = threadIdx.x + (int64_t)k * NT;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      gam[k][e] = (a.gamma != nullptr && v < nv) ? load_as<float>(a.gamma, v * VEC + e, a.gamma_dt) : 1.0f;
+      bet[k][e] = (a.beta != nullptr && v < nv) ? load_as<float>(a.beta, v * VEC + e, a.beta_dt) : 0.0f;
+    }
+  }
+  const int64_t r0 = (int64_t)blockIdx.x * kLnFwdRows;
+  const int64_t r1 = r0 + kLnFwdRows < a.M ? r0 + kLnFwdRows : a.M;
+  for (int64_t rb = r0; rb < r1; rb += RS) {
+    V vx[RS][VPL];
+    float s1[RS], s2[RS];
+#pragma unroll
+    for (int q = 0; q < RS; ++q) {
+      s1[q] = 0.f;
+      s2[q] = 0.f;
+      if (rb + q < r1) {
+        const V* px = (const V*)((const St*)a.x + (rb + q) * a.N);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+          const int64_t v = threadIdx.x + (int64_t)k * NT;
+          if (v < nv) vx[q][k] = ld_stream(px + v);
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RS; ++q)
+      if (rb + q < r1)
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+          if (threadIdx.x + (int64_t)k * NT < nv)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) s1[q] += Num<Tag>::load(vx[q][k].s[e]);
+    block_sums<RS, NT>(s1, s2, red);
+    float mu[RS];
+#pragma unroll
+    for (int q = 0; q < RS; ++q) {
+      mu[q] = s1[q] * invN;
+      s1[q] = 0.f;
+      s2[q] = 0.f;
+      if (rb + q < r1)
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+          if (threadIdx.x + (int64_t)k * NT < nv)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+              const float d = Num<Tag>::load(vx[q][k].s[e]) - mu[q];
+              s1[q] += d * d;
+            }
+    }
+    block_sums<RS, NT>(s1, s2, red);
+#pragma unroll
+    for (int q = 0; q < RS; ++q) {
+      const int64_t r = rb + q;
+      if (r < r1) {
+        const float rs = 1.0f / sqrtf(s1[q] * invN + a.eps);
+        V* po = (V*)((St*)a.out + r * a.N);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+          const int64_t v = threadIdx.x + (int64_t)k * NT;
+          if (v < nv) {
+            V o;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+              o.s[e] = Num<Tag>::store((Num<Tag>::load(vx[q][k].s[e]) - mu[q]) * rs * gam[k][e] +
+                                       bet[k][e]);
+            st_stream(po + v, o);
+          }
+        }
+        if (threadIdx.x == 0) {
+          store_as<float>(a.mean, r, a.mean_dt, mu[q]);
+          store_as<float>(a.rstd, r, a.mean_dt, rs);
+        }
+      }
+    }
+  }
+}
+
+template <typename Tag>
+__global__ __launch_bounds__(kLnBlock) void ln_fwd_row_kernel(LnFwdArgs a) {
+  typedef typename Num<Tag>::storage St;
+  __shared__ float red[2 * kLnBlock / 64];
+  const int64_t r = blockIdx.x;
+  const St* x = (const St*)a.x + r * a.N;
+  float s = 0.f;
+  for (int64_t j = threadIdx.x; j < a.N; j += kLnBlock) s += Num<Tag>::load(x[j]);
+  const float mu = block_sum2(s, 0.f, red).x / (float)a.N;
+  float q = 0.f;
+  for (int64_t j = threadIdx.x; j < a.N; j += kLnBlock) {
+    const float d = Num<Tag>::load(x[j]) - mu;
+    q += d * d;
+  }
+  const float rs = 1.0f / sqrtf(block_sum2(q, 0.f, red).x / (float)a.N + a.eps);
+  St* o = (St*)a.out + r * a.N;
+  for (int64_t j = threadIdx.x; j < a.N; j += kLnBlock) {
+    float y = (Num<Tag>::load(x[j]) - mu) * rs;
+    if (a.gamma != nullptr) y *= load_as<float>(a.gamma, j, a.gamma_dt);
+    if (a.beta != nullptr) y += load_as<float>(a.beta, j, a.beta_dt);
+    o[j] = Num<Tag>::store(y);
+  }
+  if (threadIdx.x == 0) {
+    store_as<float>(a.mean, r, a.mean_dt, mu);
+    store_as<float>(a.rstd, r, a.mean_dt, rs);
+  }
+}
+
+template <typename Tag>
+mi_status_t launch_ln_fwd(const LnFwdArgs& a, hipStream_t stream) {
+  typedef typename Num<Tag>::storage St;
+  constexpr int VEC = 16 / sizeof(St);
+  const int64_t nv = a.N / VEC;
+  MI_CHECK_ARG(a.M <= 0x7fffffffLL, "layer_norm: too many rows");
+  const bool reg = a.N % VEC == 0 && (((uintptr_t)a.x | (uintptr_t)a.out) % 16) == 0 &&
+                   nv <= (int64_t)512 * 4;
+  if (reg) {
+    const unsigned blocks = (unsigned)((a.M + kLnFwdRows - 1) / kLnFwdRows);
+    if (nv <= 256)
+      hipLaunchKernelGGL((ln_fwd_reg_kernel<Tag, 1, 2, 256>), dim3(blocks), dim3(256), 0, stream, a);
+    else if (nv <= 512)
+      hipLaunchKernelGGL((ln_fwd_reg_kernel<Tag, 1, 2, 512>), dim3(blocks), dim3(512), 0, stream, a);
+    else if (nv <= 1024)
+      hipLaunchKernelGGL((ln_fwd_reg_kernel<Tag, 2, 2, 512>), dim3(blocks), dim3(512), 0, stream, a);
+    else
+      hipLaunchKernelGGL((ln_fwd_reg_kernel<Tag, 4, 1, 512>), dim3(blocks), dim3(512), 0, stream, a);
+    return check_launch("layer_norm");
+  }
+  hipLaunchKernelGGL((ln_fwd_row_kernel<Tag>), dim3((unsigned)a.M), dim3(kLnBlock), 0, stream, a);
+  return check_launch("layer_norm rows");
+}
+
 }  // namespace
 }  // namespace mi
 
 using namespace mi;
+
+extern "C" mi_status_t mi_layer_norm(const mi_tensor_t* out, const mi_tensor_t* mean,
+                                     const mi_tensor_t* rstd, const mi_tensor_t* input,
+                                     const mi_tensor_t* weight, const mi_tensor_t* bias,
+                                     int64_t normalized_numel, double eps, mi_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = (hipStream_t)stream_;
+  MI_RETURN_IF(validate(out, "out"));
+  MI_RETURN_IF(validate(mean, "mean"));
+  MI_RETURN_IF(validate(rstd, "rstd"));
+  MI_RETURN_IF(validate(input, "input"));
+  const int dt = input->dtype;
+  MI_CHECK_ARG(dt == MI_F32 || dt == MI_BF16 || dt == MI_F16, "layer_norm: input dtype %s unsupported",
+               dtype_name(dt));
+  MI_CHECK_ARG(out->dtype == dt && is_contiguous(*out) && is_contiguous(*input) &&
+                   numel(*out) == numel(*input),
+               "layer_norm: input and out must be contiguous, of one dtype and size");
+  const int64_t total = numel(*input), N = normalized_numel;
+  MI_CHECK_ARG(N >= 1 && total % N == 0, "layer_norm: %lld elements do not form rows of %lld",
+               (long long)total, (long long)N);
+  const int64_t M = total / N;
+  MI_CHECK_ARG(numel(*mean) == M && numel(*rstd) == M && is_contiguous(*mean) &&
+                   is_contiguous(*rstd) && mean->dtype == rstd->dtype &&
+                   (mean->dtype == dt || mean->dtype == MI_F32),
+               "layer_norm: mean and rstd must be contiguous with %lld elements, fp32 or the input's "
+               "dtype", (long long)M);
+  LnFwdArgs a{};
+  for (int i = 0; i < 2; ++i) {
+    const mi_tensor_t* p = i == 0 ? weight : bias;
+    if (p != nullptr && p->data != nullptr) {
+      MI_RETURN_IF(validate(p, i == 0 ? "weight" : "bias"));
+      MI_CHECK_ARG(numel(*p) == N && is_contiguous(*p) && (p->dtype == dt || p->dtype == MI_F32),
+                   "layer_norm: weight and bias must be contiguous with %lld elements of the input's "
+                   "dtype or fp32", (long long)N);
+      if (i == 0) {
+        a.gamma = p->data;
+        a.gamma_dt = p->dtype;
+      } else {
+        a.beta = p->data;
+        a.beta_dt = p->dtype;
+      }
+    }
+  }
+  if (total == 0) return MI_OK;
+  a.out = out->data;
+  a.mean = mean->data;
+  a.rstd = rstd->data;
+  a.x = input->data;
+  a.M = M;
+  a.N = N;
+  a.eps = (float)eps;
+  a.mean_dt = mean->dtype;
+  switch (dt) {
+    case MI_BF16: return launch_ln_fwd<BF16>(a, stream);
+    case MI_F16: return launch_ln_fwd<F16>(a, stream);
+    default: return launch_ln_fwd<float>(a, stream);
+  }
+}
 
 extern "C" mi_status_t mi_layer_norm_backward(
     const mi_tensor_t* grad_input, const mi_tensor_t* grad_weight, const mi_tensor_t* grad_bias,

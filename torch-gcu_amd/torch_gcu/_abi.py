@@ -77,6 +77,7 @@ _SIGNATURES = {
     "mi_log_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_layer_norm_backward": ([_T] * 8 + [ctypes.c_int64, _S], ctypes.c_int),
+    "mi_layer_norm": ([_T] * 6 + [ctypes.c_int64, ctypes.c_double, _S], ctypes.c_int),
     "mi_fused_adamw": ([ctypes.POINTER(_T)] * 6 + [ctypes.c_int32, _T, ctypes.POINTER(MiAdamwHparams),
                                                    _T, _T, _S], ctypes.c_int),
     "mi_add": ([_T, _T, _T, MiScalar, _S], ctypes.c_int),
@@ -260,6 +261,14 @@ def softmax_backward(grad_input, grad_output, output, dim):
     check("mi_softmax_backward", lib().mi_softmax_backward(
         desc(grad_input), desc(grad_output), desc(output), dim, stream_of(grad_input)))
     return grad_input
+
+
+def layer_norm(out, mean, rstd, x, weight, bias, normalized_numel, eps):
+    """weight and bias may be None."""
+    check("mi_layer_norm", lib().mi_layer_norm(
+        desc(out), desc(mean), desc(rstd), desc(x), desc(weight) if weight is not None else None,
+        desc(bias) if bias is not None else None, normalized_numel, eps, stream_of(x)))
+    return out
 
 
 def layer_norm_backward(grad_input, grad_weight, grad_bias, grad_out, x, mean, rstd, weight,
