@@ -363,9 +363,10 @@ mi_status_t launch_ln_bwd(LnArgs& a, void* dw, int dw_dt, void* db, int db_dt,
 // rstd = 1 / sqrt(var + eps) (biased variance, two passes over the row held
 // in registers) in fp32, stored in mean_dt; out uses the unrounded fp32 values
 // (ATen's LayerNormKernelImpl does the same with y = x * scale + shift,
-// aten/src/ATen/native/cpu/layer_norm_kernel.cpp).  Rows of up to 2048
-// 16-byte vectors stay in registers, kLnFwdRows rows per block; longer or
-// unaligned rows take one block each and are read three times.
+// aten/src/ATen/native/cpu/layer_norm_kernel.cpp).  Rows of up to 1024
+// 16-byte vectors: one wave per row; up to 2048: kLnFwdRows rows per 512-lane
+// block; longer or unaligned rows take one block each and are read three
+// times.
 struct LnFwdArgs {
   void* out;
   void* mean;
@@ -502,6 +503,99 @@ __global__ __launch_bounds__(kLnBlock) void ln_fwd_row_kernel(LnFwdArgs a) {
   }
 }
 
+// One wave per row (four rows per 256-lane block): the row in registers,
+// both sums by wave shuffles, no block barrier; gamma / beta pieces read per
+// row (they stay in L2).  WF32: the parameters are fp32 (mixed type).
+template <typename Tag, int VPL, bool WF32>
+__global__ __launch_bounds__(256) void ln_fwd_wave_kernel(LnFwdArgs a) {
+  typedef typename Num<Tag>::storage St;
+  constexpr int VEC = 16 / sizeof(St);
+  union V {
+    uint4 u;
+    St s[VEC];
+  };
+  union P {  // VEC fp32 parameters
+    uint4 u[VEC / 4];
+    float f[VEC];
+  };
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= a.M) return;
+  const int64_t nv = a.N / VEC;
+  const V* px = (const V*)((const St*)a.x + row * a.N);
+  V v[VPL];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int64_t i = lane + (int64_t)k * 64;
+    if (i < nv) {
+      v[k] = ld_stream(px + i);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += Num<Tag>::load(v[k].s[e]);
+    }
+  }
+  const float mu = wave_sum(s) / (float)a.N;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k)
+    if (lane + (int64_t)k * 64 < nv)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = Num<Tag>::load(v[k].s[e]) - mu;
+        q += d * d;
+      }
+  const float rs = 1.0f / sqrtf(wave_sum(q) / (float)a.N + a.eps);
+  V* po = (V*)((St*)a.out + row * a.N);
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int64_t i = lane + (int64_t)k * 64;
+    if (i < nv) {
+      float g[VEC], b[VEC];
+      if (a.gamma != nullptr) {
+        if constexpr (WF32) {
+          P pg;
+#pragma unroll
+          for (int w = 0; w < VEC / 4; ++w) pg.u[w] = ((const uint4*)((const float*)a.gamma + i * VEC))[w];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) g[e] = pg.f[e];
+        } else {
+          const V pg = ((const V*)a.gamma)[i];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) g[e] = Num<Tag>::load(pg.s[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) g[e] = 1.0f;
+      }
+      if (a.beta != nullptr) {
+        if constexpr (WF32) {
+          P pb;
+#pragma unroll
+          for (int w = 0; w < VEC / 4; ++w) pb.u[w] = ((const uint4*)((const float*)a.beta + i * VEC))[w];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) b[e] = pb.f[e];
+        } else {
+          const V pb = ((const V*)a.beta)[i];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) b[e] = Num<Tag>::load(pb.s[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) b[e] = 0.0f;
+      }
+      V o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        o.s[e] = Num<Tag>::store((Num<Tag>::load(v[k].s[e]) - mu) * rs * g[e] + b[e]);
+      st_stream(po + i, o);
+    }
+  }
+  if (lane == 0) {
+    store_as<float>(a.mean, row, a.mean_dt, mu);
+    store_as<float>(a.rstd, row, a.mean_dt, rs);
+  }
+}
+
 template <typename Tag>
 mi_status_t launch_ln_fwd(const LnFwdArgs& a, hipStream_t stream) {
   typedef typename Num<Tag>::storage St;
@@ -510,6 +604,28 @@ mi_status_t launch_ln_fwd(const LnFwdArgs& a, hipStream_t stream) {
   MI_CHECK_ARG(a.M <= 0x7fffffffLL, "layer_norm: too many rows");
   const bool reg = a.N % VEC == 0 && (((uintptr_t)a.x | (uintptr_t)a.out) % 16) == 0 &&
                    nv <= (int64_t)512 * 4;
+  // parameters of one dtype (both fp32, or both the input's) for the wave kernel
+  const int pdt = a.gamma != nullptr ? a.gamma_dt : (a.beta != nullptr ? a.beta_dt : -1);
+  const bool params_ok = (a.gamma == nullptr || a.gamma_dt == pdt) &&
+                          (a.beta == nullptr || a.beta_dt == pdt) &&
+                          ((((uintptr_t)a.gamma | (uintptr_t)a.beta) % 16) == 0);
+  if (reg && params_ok && nv <= 64 * 16 && (a.M + 3) / 4 <= 0x7fffffffLL) {
+    const bool wf32 = pdt == MI_F32 && !std::is_same<Tag, float>::value;
+    const unsigned grid = (unsigned)((a.M + 3) / 4);
+    auto go = [&](auto vpl_c) -> mi_status_t {
+      constexpr int VPL = decltype(vpl_c)::value;
+      if (wf32)
+        hipLaunchKernelGGL((ln_fwd_wave_kernel<Tag, VPL, true>), dim3(grid), dim3(256), 0, stream, a);
+      else
+        hipLaunchKernelGGL((ln_fwd_wave_kernel<Tag, VPL, false>), dim3(grid), dim3(256), 0, stream, a);
+      return check_launch("layer_norm");
+    };
+    if (nv <= 64) return go(std::integral_constant<int, 1>());
+    if (nv <= 128) return go(std::integral_constant<int, 2>());
+    if (nv <= 256) return go(std::integral_constant<int, 4>());
+    if (nv <= 512) return go(std::integral_constant<int, 8>());
+    return go(std::integral_constant<int, 16>());
+  }
   if (reg) {
     const unsigned blocks = (unsigned)((a.M + kLnFwdRows - 1) / kLnFwdRows);
     if (nv <= 256)
