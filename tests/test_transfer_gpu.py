@@ -272,3 +272,21 @@ def test_cat_rules_and_out_variant():
     buf = torch.zeros(8, 3, device="gcu")
     with pytest.raises(RuntimeError, match="memory location"):
         torch.cat([buf[:4], buf[4:]], 0, out=buf)
+
+
+def test_stack_and_split_cat_run_natively():
+    """torch.stack (a cat of unsqueezed views) and re-joining torch.chunk
+    pieces reach the native cat; results equal CPU ATen's."""
+    xs = [rand((7, 33), torch.bfloat16, 60 + i) for i in range(5)]
+    C._set_op_debug_config("op_statistics=true")
+    C._clear_op_statistics()
+    try:
+        st = torch.stack([x.to("gcu") for x in xs], 1)
+        big = rand((12, 40), torch.float32, 70).to("gcu")
+        rejoined = torch.cat(torch.chunk(big, 3, 1)[::-1], 1)
+        stats = C._op_statistics()
+    finally:
+        C._set_op_debug_config("")
+    assert_exact(st.cpu(), torch.stack(xs, 1), "stack")
+    assert_exact(rejoined.cpu(), torch.cat(torch.chunk(big.cpu(), 3, 1)[::-1], 1), "chunk + cat")
+    assert stats.get("cat", (0, 0))[0] >= 2 and stats.get("cat", (0, 0))[1] == 0, stats
