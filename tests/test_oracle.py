@@ -344,6 +344,36 @@ def test_golden_fixtures(name):
         assert_close(got, want, "fp32", name)
 
 
+def test_golden_training_fixtures():
+    """CPU ATen on the committed float64 fixtures of the training-side ops and
+    cat (tests/golden/make_golden.py)."""
+    d = np.load(os.path.join(GOLDEN, "adamw.npz"))
+    hp = d["hp"]
+    t = lambda k: torch.from_numpy(d[k])  # noqa: E731
+    out = aten.fused_adamw([t("p")], [t("g")], [t("m")], [t("v")], [], [torch.tensor(float(hp[5]))],
+                           lr=float(hp[0]), beta1=float(hp[1]), beta2=float(hp[2]),
+                           weight_decay=float(hp[3]), eps=float(hp[4]), amsgrad=False,
+                           maximize=False, grad_scale=torch.tensor(float(hp[6])))
+    for k, name in enumerate(("param", "grad", "exp_avg", "exp_avg_sq")):
+        assert_close(out[k][0], torch.from_numpy(d["expected"][k]), "fp32", f"adamw {name}")
+    d = np.load(os.path.join(GOLDEN, "layer_norm.npz"))
+    x, w, b, dy = (torch.from_numpy(d[k]) for k in ("x", "w", "b", "dy"))
+    y, mean, rstd = aten.layer_norm_forward(x, [48], w, b, float(d["eps"]))
+    assert_close(y, torch.from_numpy(d["out"]), "fp32", "layer_norm out")
+    assert_close(mean, torch.from_numpy(d["mean"]), "fp32", "layer_norm mean")
+    assert_close(rstd, torch.from_numpy(d["rstd"]), "fp32", "layer_norm rstd")
+    dx, dw, db = aten.layer_norm_backward(dy, x, [48], mean, rstd, w, b, [True, True, True])
+    for got, k in ((dx, "dx"), (dw, "dw"), (db, "db")):
+        assert_close(got, torch.from_numpy(d[k]), "fp32", f"layer_norm {k}")
+    d = np.load(os.path.join(GOLDEN, "log_softmax_backward.npz"))
+    assert_close(aten.log_softmax_backward(torch.from_numpy(d["dy"]), torch.from_numpy(d["y"]), -1,
+                                           torch.float32),
+                 torch.from_numpy(d["expected"]), "fp32", "log_softmax_backward")
+    d = np.load(os.path.join(GOLDEN, "cat.npz"))
+    assert_exact(aten.cat([torch.from_numpy(d[k]) for k in ("a", "b", "c")], 1),
+                 torch.from_numpy(d["expected"]), "cat")
+
+
 def test_planted_mistakes_are_caught():
     """Mutated oracles must fail the same pins."""
     q = torch.randn(8, 2, 16, generator=g(15))
