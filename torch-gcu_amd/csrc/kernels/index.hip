@@ -18,11 +18,14 @@ __device__ __forceinline__ int64_t read_index(const IdxT* idx, int64_t i, int64_
   return (int64_t)idx[i * istride];
 }
 
-// Dense rows, moved as 16-byte (W = uint4) or 8/4/2/1-byte words, one word
-// per lane: the four lanes of a 64-byte row share its index load, and the
-// grid covers every word once, so each lane's index -> row load chain is
-// its only work.  When the words per row are a power of two (LOG2 >= 0) the
-// row and word come from a shift and a mask instead of a division.
+// Dense rows, moved as 16-byte (W = uint4) or 8/4/2/1-byte words.  A lane
+// takes kGatherU words a grid apart and issues their index loads, then their
+// row loads, then their stores, so four index -> row chains are in flight
+// per lane (the four lanes of a 64-byte row share its index load).  When the
+// words per row are a power of two (LOG2 >= 0) the row and word come from a
+// shift and a mask instead of a division.
+constexpr int kGatherU = 4;  // words per lane: their index loads, then row loads, in flight
+
 template <typename W, typename IdxT>
 __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
     W* __restrict__ out, const W* __restrict__ self, const IdxT* __restrict__ idx,
@@ -31,36 +34,50 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
   const int64_t total = outer * n_idx * words_per_row;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   const bool small = total < 0x7fffffffLL;
-  for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
-    int64_t row, w, o, i;
+  int64_t tt[kGatherU], row[kGatherU], w[kGatherU], o[kGatherU], s[kGatherU];
+#pragma unroll
+  for (int u = 0; u < kGatherU; ++u) {
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x + u * stride;
+    tt[u] = t;
+    int64_t rr, ww, i;
     if (log2_wpr >= 0) {
-      row = t >> log2_wpr;
-      w = t & (words_per_row - 1);
+      rr = t >> log2_wpr;
+      ww = t & (words_per_row - 1);
     } else if (small) {  // 32-bit division is several times cheaper
       const uint32_t r32 = (uint32_t)t / (uint32_t)words_per_row;
-      w = (uint32_t)t - r32 * (uint32_t)words_per_row;
-      row = r32;
+      ww = (uint32_t)t - r32 * (uint32_t)words_per_row;
+      rr = r32;
     } else {
-      row = t / words_per_row;
-      w = t - row * words_per_row;
+      rr = t / words_per_row;
+      ww = t - rr * words_per_row;
     }
     if (outer == 1) {
-      o = 0;
-      i = row;
+      o[u] = 0;
+      i = rr;
     } else {
-      o = row / n_idx;
-      i = row - o * n_idx;
+      o[u] = rr / n_idx;
+      i = rr - o[u] * n_idx;
     }
-    const int64_t s = read_index(idx, i, istride);
-    W v;
-    if (s >= 0 && s < src_rows) {
-      v = self[(o * src_rows + s) * words_per_row + w];
-    } else {
-      v = W{};
-    }
-    if constexpr (sizeof(W) == 16) st_stream(out + t, v);
-    else out[t] = v;
+    row[u] = i;
+    w[u] = ww;
+    s[u] = t < total ? read_index(idx, i, istride) : 0;
   }
+  W v[kGatherU];
+#pragma unroll
+  for (int u = 0; u < kGatherU; ++u) {
+    if (tt[u] < total && s[u] >= 0 && s[u] < src_rows)
+      v[u] = self[(o[u] * src_rows + s[u]) * words_per_row + w[u]];
+    else
+      v[u] = W{};
+  }
+#pragma unroll
+  for (int u = 0; u < kGatherU; ++u) {
+    if (tt[u] < total) {
+      if constexpr (sizeof(W) == 16) st_stream(out + tt[u], v[u]);
+      else out[tt[u]] = v[u];
+    }
+  }
+  (void)row;
 }
 
 // General layout: iterate over out elements; coordinates decoded per element.
@@ -118,7 +135,9 @@ mi_status_t launch_rows(const mi_tensor_t* out, const mi_tensor_t* self, const I
       log2_wpr = 0;
       while ((int64_t(1) << log2_wpr) < wpr) ++log2_wpr;
     }
-    hipLaunchKernelGGL((gather_rows_kernel<W, IdxT>), dim3(grid_for(total)), dim3(kBlock), 0,
+    const int64_t nb = (total + (int64_t)kBlock * kGatherU - 1) / ((int64_t)kBlock * kGatherU);
+    MI_CHECK_ARG(nb <= 0x7fffffffLL, "index_select: too many rows");
+    hipLaunchKernelGGL((gather_rows_kernel<W, IdxT>), dim3((unsigned)nb), dim3(kBlock), 0,
                        stream, (W*)out->data, (const W*)self->data, idx, istride, outer, n_idx,
                        src_rows, wpr, log2_wpr);
     return check_launch("index_select rows");
