@@ -290,3 +290,23 @@ def test_stack_and_split_cat_run_natively():
     assert_exact(st.cpu(), torch.stack(xs, 1), "stack")
     assert_exact(rejoined.cpu(), torch.cat(torch.chunk(big.cpu(), 3, 1)[::-1], 1), "chunk + cat")
     assert stats.get("cat", (0, 0))[0] >= 2 and stats.get("cat", (0, 0))[1] == 0, stats
+
+
+def test_dataloader_pin_memory_batches_come_from_the_host_allocator():
+    """DataLoader(pin_memory=True) pins its batches through the gcu host
+    allocator (the current accelerator is gcu); the batches reach the device
+    with non-blocking copies and equal their sources."""
+    data = torch.randn(64, 8, generator=g(80))
+    labels = torch.arange(64)
+    dl = torch.utils.data.DataLoader(torch.utils.data.TensorDataset(data, labels), batch_size=16,
+                                     pin_memory=True, num_workers=0)
+    before = torch.gcu.host_memory_stats()["num_host_alloc"] + torch.gcu.host_memory_stats()["num_cache_hits"]
+    outs = []
+    for xb, yb in dl:
+        assert xb.is_pinned() and yb.is_pinned()
+        outs.append((xb.to("gcu", non_blocking=True), yb.to("gcu", non_blocking=True)))
+    torch.gcu.synchronize()
+    after = torch.gcu.host_memory_stats()["num_host_alloc"] + torch.gcu.host_memory_stats()["num_cache_hits"]
+    assert after - before >= 8  # two pinned tensors per batch
+    assert torch.equal(torch.cat([x.cpu() for x, _ in outs]), data)
+    assert torch.equal(torch.cat([y.cpu() for _, y in outs]), labels)
