@@ -196,6 +196,14 @@ mi_status_t mi_fused_adamw(const mi_tensor_t* const* params,
                            const mi_tensor_t* grad_scale,
                            const mi_tensor_t* found_inf, mi_stream_t stream);
 
+/* Every tensor of the list += value, in place (the sum in fp32, fp64 for
+ * f64, rounded once): n_tensors dense tensors of one dtype (f32, bf16, f16,
+ * f64).  The optimizer's step-count advance before a fused step.  Replaces
+ * topsatenForeachAdd (yaml _foreach_add_.Scalar :47). */
+mi_status_t mi_foreach_add_scalar(const mi_tensor_t* const* tensors,
+                                  int32_t n_tensors, double value,
+                                  mi_stream_t stream);
+
 /* ---- indexing ---------------------------------------------------------- */
 
 /* out = self.index_select(dim, index); index is 1-D (or 0-D) int32/int64;

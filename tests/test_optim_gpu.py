@@ -129,4 +129,27 @@ def test_optim_adamw_fused_trains_on_gcu():
     for dp_, cp_ in zip(dparams, cparams):
         assert_close(dp_.detach().cpu(), cp_.detach(), "fp32", "AdamW(fused=True) params")
     assert stats.get("_fused_adamw_", (0, 0))[0] == 4, stats
-    assert stats.get("_fused_adamw_", (0, 0))[1] == 0, stats
+    # the step-count advance is native too: nothing of the step falls back to CPU
+    assert stats.get("_foreach_add_.Scalar", (0, 0))[0] == 4, stats
+    assert all(v[1] == 0 for v in stats.values()), stats
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
+def test_foreach_add_scalar_parity(dtype):
+    """_foreach_add_.Scalar over 70 tensors (two launches) of several sizes,
+    including an empty one and a misaligned view, equals CPU ATen's."""
+    shapes = [(7,), (), (0,), (33, 65), (5000,)] * 14
+    base = torch.randn(1 + 513, generator=g(600)).to(dtype)
+    ts = [torch.randn(s, generator=g(601 + i)).to(dtype) for i, s in enumerate(shapes)] + [base[1:]]
+    dbase = base.to("gcu")
+    dts = [t.to("gcu") for t in ts[:-1]] + [dbase[1:]]
+    torch._foreach_add_(dts, 0.3)
+    want = [t.clone() for t in ts]
+    torch._foreach_add_(want, 0.3)
+    for a, b in zip(dts, want):
+        assert_close(a.cpu(), b, "fp32" if dtype in (torch.float32, torch.float64) else "bf16", "foreach_add_")
+    assert float(dbase[0].cpu()) == float(base[0])
+    # an integer list takes the per-tensor path
+    ints = [torch.arange(5).to("gcu"), torch.arange(3).to("gcu")]
+    torch._foreach_add_(ints, 2)
+    assert torch.equal(ints[0].cpu(), torch.arange(5) + 2) and torch.equal(ints[1].cpu(), torch.arange(3) + 2)

@@ -146,5 +146,31 @@ void _fused_adamw__tensor_lr(at::TensorList self, at::TensorList grads, at::Tens
               beta2, weight_decay, eps, amsgrad, maximize, grad_scale, found_inf);
 }
 
+// t += scalar for every tensor of the list (the reference's generated
+// _foreach_add_.Scalar, yaml :47): one multi-tensor launch when the list is
+// dense and of one float dtype with a real scalar, else ATen's per-tensor
+// add_ (which runs on the native elementwise kernel).
+void _foreach_add__Scalar(at::TensorList self, const at::Scalar& scalar) {
+  if (self.empty()) return;
+  const at::ScalarType dt = self[0].scalar_type();
+  bool fast = kernel_dtype(dt) && !scalar.isComplex() && !scalar.isBoolean();
+  for (const at::Tensor& t : self)
+    fast = fast && t.scalar_type() == dt && t.device() == self[0].device() &&
+           (t.numel() == 0 || t.is_non_overlapping_and_dense());
+  if (!fast) {
+    for (const at::Tensor& t : self) const_cast<at::Tensor&>(t).add_(scalar);
+    return;
+  }
+  c10::DeviceGuard g(self[0].device());
+  std::vector<mi_tensor_t> d;
+  d.reserve(self.size());
+  for (const at::Tensor& t : self) d.push_back(desc(t));
+  std::vector<const mi_tensor_t*> ptr;
+  for (const auto& x : d) ptr.push_back(&x);
+  check_mi(mi_foreach_add_scalar(ptr.data(), (int32_t)ptr.size(), scalar.toDouble(),
+                                 mi_stream(self[0])),
+           "_foreach_add_");
+}
+
 }  // namespace aotops
 }  // namespace torch_gcu

@@ -235,10 +235,102 @@ mi_status_t launch_adam(AdamArgs& a, bool ams, hipStream_t s, int64_t blocks) {
   return check_launch("fused_adamw");
 }
 
+// _foreach_add_.Scalar: every tensor of a list += value, in place (the
+// optimizer's step-count advance).  One launch per kForeachMax tensors, the
+// table in kernel arguments as for AdamW; the sum in fp32 (fp64 for fp64),
+// rounded once.
+constexpr int kForeachMax = 64;
+constexpr int kForeachChunk = 1024;  // elements per block
+
+struct ForeachTensor {
+  void* p;
+  int64_t n;
+  int64_t first_block;
+};
+
+struct ForeachArgs {
+  ForeachTensor t[kForeachMax];
+  int32_t count;
+  double value;
+};
+
+template <typename Tag>
+__global__ __launch_bounds__(256) void foreach_add_scalar_kernel(ForeachArgs a) {
+  typedef typename Num<Tag>::storage St;
+  typedef typename Num<Tag>::acc Acc;
+  int lo = 0, hi = a.count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)blockIdx.x >= a.t[mid].first_block) lo = mid;
+    else hi = mid - 1;
+  }
+  const ForeachTensor& t = a.t[lo];
+  St* p = (St*)t.p;
+  const Acc v = (Acc)a.value;
+  const int64_t base = ((int64_t)blockIdx.x - t.first_block) * kForeachChunk;
+  for (int k = threadIdx.x; k < kForeachChunk; k += 256) {
+    const int64_t i = base + k;
+    if (i >= t.n) break;
+    p[i] = Num<Tag>::store(Num<Tag>::load(p[i]) + v);
+  }
+}
+
+template <typename Tag>
+mi_status_t launch_foreach(ForeachArgs& a, int64_t blocks, hipStream_t s) {
+  hipLaunchKernelGGL((foreach_add_scalar_kernel<Tag>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return check_launch("foreach_add_scalar");
+}
+
 }  // namespace
 }  // namespace mi
 
 using namespace mi;
+
+extern "C" mi_status_t mi_foreach_add_scalar(const mi_tensor_t* const* tensors, int32_t n_tensors,
+                                             double value, mi_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = (hipStream_t)stream_;
+  MI_CHECK_ARG(n_tensors >= 0 && (n_tensors == 0 || tensors != nullptr),
+               "foreach_add_scalar: bad tensor list");
+  if (n_tensors == 0) return MI_OK;
+  const int dt = tensors[0] != nullptr ? tensors[0]->dtype : -1;
+  MI_CHECK_ARG(dt == MI_F32 || dt == MI_BF16 || dt == MI_F16 || dt == MI_F64,
+               "foreach_add_scalar: tensors must be float32, bfloat16, float16 or float64");
+  ForeachArgs a{};
+  a.value = value;
+  int k = 0;
+  int64_t blocks = 0;
+  auto flush = [&]() -> mi_status_t {
+    if (k == 0) return MI_OK;
+    a.count = k;
+    mi_status_t st;
+    switch (dt) {
+      case MI_F32: st = launch_foreach<float>(a, blocks, stream); break;
+      case MI_BF16: st = launch_foreach<BF16>(a, blocks, stream); break;
+      case MI_F16: st = launch_foreach<F16>(a, blocks, stream); break;
+      default: st = launch_foreach<double>(a, blocks, stream); break;
+    }
+    k = 0;
+    blocks = 0;
+    return st;
+  };
+  for (int i = 0; i < n_tensors; ++i) {
+    const mi_tensor_t* t = tensors[i];
+    MI_RETURN_IF(validate(t, "tensor"));
+    MI_CHECK_ARG(t->dtype == dt, "foreach_add_scalar: tensor %d is %s, tensor 0 is %s", i,
+                 dtype_name(t->dtype), dtype_name(dt));
+    const int64_t n = numel(*t);
+    if (n == 0) continue;
+    MI_CHECK_ARG(dense_any_order(*t), "foreach_add_scalar: tensor %d is not dense", i);
+    a.t[k].p = t->data;
+    a.t[k].n = n;
+    a.t[k].first_block = blocks;
+    blocks += (n + kForeachChunk - 1) / kForeachChunk;
+    MI_CHECK_ARG(blocks <= 0x7fffffffLL, "foreach_add_scalar: too many blocks");
+    if (++k == kForeachMax) MI_RETURN_IF(flush());
+  }
+  return flush();
+}
 
 extern "C" mi_status_t mi_fused_adamw(
     const mi_tensor_t* const* params, const mi_tensor_t* const* grads,

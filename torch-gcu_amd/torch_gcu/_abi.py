@@ -74,6 +74,7 @@ _SIGNATURES = {
     "mi_fill": ([_T, MiScalar, _S], ctypes.c_int),
     "mi_cat": ([_T, ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_int32, _S], ctypes.c_int),
     "mi_silu_backward": ([_T, _T, _T, _S], ctypes.c_int),
+    "mi_foreach_add_scalar": ([ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_double, _S], ctypes.c_int),
     "mi_log_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_layer_norm_backward": ([_T] * 8 + [ctypes.c_int64, _S], ctypes.c_int),
@@ -243,6 +244,15 @@ def fused_adamw(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_ste
     check("mi_fused_adamw", lib().mi_fused_adamw(
         *arrays, n, lr_d, ctypes.byref(hp), gs_d, fi_d,
         stream_of(params[0]) if n else torch.cuda.current_stream().cuda_stream))
+
+
+def foreach_add_scalar_(tensors, value):
+    """Every tensor += value, in place, through mi_foreach_add_scalar."""
+    ds = [desc(t) for t in tensors]
+    arr = (_T * max(1, len(ds)))(*[ctypes.pointer(d) for d in ds])
+    check("mi_foreach_add_scalar", lib().mi_foreach_add_scalar(
+        arr, len(ds), value, stream_of(tensors[0]) if tensors else torch.cuda.current_stream().cuda_stream))
+    return tensors
 
 
 def silu_backward(grad_input, grad_output, self):
