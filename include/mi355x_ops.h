@@ -204,6 +204,16 @@ mi_status_t mi_foreach_add_scalar(const mi_tensor_t* const* tensors,
                                   int32_t n_tensors, double value,
                                   mi_stream_t stream);
 
+/* Mixed-precision grad unscaling: every element of the n_tensors dense
+ * tensors (one dtype: f32, bf16, f16, f64) *= inv_scale in place (left as it
+ * is when inv_scale is 1), and found_inf is set to 1 when any element is inf
+ * or NaN (it is never cleared here).  found_inf and inv_scale are one-element
+ * float32 tensors read on the device.  Replaces the generated
+ * _amp_foreach_non_finite_check_and_unscale_ (yaml :15). */
+mi_status_t mi_amp_unscale(const mi_tensor_t* const* tensors, int32_t n_tensors,
+                           const mi_tensor_t* found_inf,
+                           const mi_tensor_t* inv_scale, mi_stream_t stream);
+
 /* ---- indexing ---------------------------------------------------------- */
 
 /* out = self.index_select(dim, index); index is 1-D (or 0-D) int32/int64;

@@ -153,3 +153,25 @@ def test_foreach_add_scalar_parity(dtype):
     ints = [torch.arange(5).to("gcu"), torch.arange(3).to("gcu")]
     torch._foreach_add_(ints, 2)
     assert torch.equal(ints[0].cpu(), torch.arange(5) + 2) and torch.equal(ints[1].cpu(), torch.arange(3) + 2)
+
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_amp_unscale_parity(dtype):
+    """_amp_foreach_non_finite_check_and_unscale_ over 70 tensors: the grads
+    are multiplied by inv_scale as CPU ATen does, found_inf stays 0 for finite
+    grads, becomes 1 with an inf or a NaN anywhere, and inv_scale = 1 leaves
+    the values as they are."""
+    shapes = [(7,), (0,), (33, 65), (5000,), ()] * 14
+    grads = [(torch.randn(s, generator=g(700 + i)) * 512).to(dtype) for i, s in enumerate(shapes)]
+    for inv, poison in ((1.0 / 512, None), (1.0 / 512, float("inf")), (1.0, float("nan"))):
+        cg = [t.clone() for t in grads]
+        if poison is not None:
+            cg[23].view(-1)[17] = poison
+        dg = [t.to("gcu") for t in cg]
+        fi, dfi = torch.zeros(1), torch.zeros(1, device="gcu")
+        torch._amp_foreach_non_finite_check_and_unscale_(cg, fi, torch.tensor([inv]))
+        torch._amp_foreach_non_finite_check_and_unscale_(dg, dfi, torch.tensor([inv], device="gcu"))
+        assert float(dfi.cpu()) == float(fi) == (0.0 if poison is None else 1.0)
+        for a, b in zip(dg, cg):
+            assert_close(a.cpu(), b, "fp32" if dtype == torch.float32 else "bf16", f"unscale {inv}")

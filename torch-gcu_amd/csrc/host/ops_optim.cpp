@@ -172,5 +172,36 @@ void _foreach_add__Scalar(at::TensorList self, const at::Scalar& scalar) {
            "_foreach_add_");
 }
 
+// GradScaler's unscale step (the reference's generated
+// _amp_foreach_non_finite_check_and_unscale_, yaml :15): one multi-tensor
+// launch per list of one float dtype; other lists go to CPU ATen.
+void _amp_foreach_non_finite_check_and_unscale_(at::TensorList self, at::Tensor& found_inf,
+                                                const at::Tensor& inv_scale) {
+  TORCH_CHECK(inv_scale.numel() == 1, "inv_scale must be a 1-element tensor.");
+  TORCH_CHECK(found_inf.numel() == 1, "found_inf must be a 1-element tensor.");
+  TORCH_CHECK(inv_scale.scalar_type() == at::ScalarType::Float, "inv_scale must be a float tensor.");
+  TORCH_CHECK(found_inf.scalar_type() == at::ScalarType::Float, "found_inf must be a float tensor.");
+  if (self.empty()) return;
+  const at::ScalarType dt = self[0].scalar_type();
+  bool fast = kernel_dtype(dt) && found_inf.device() == self[0].device() &&
+              inv_scale.device() == self[0].device();
+  for (const at::Tensor& t : self)
+    fast = fast && t.scalar_type() == dt && t.device() == self[0].device() &&
+           (t.numel() == 0 || t.is_non_overlapping_and_dense());
+  if (!fast)
+    return at::native::call_fallback_fn<&gcu_cpu_fallback,
+                                        ATEN_OP(_amp_foreach_non_finite_check_and_unscale_)>::call(
+        self, found_inf, inv_scale);
+  c10::DeviceGuard g(self[0].device());
+  std::vector<mi_tensor_t> d;
+  d.reserve(self.size());
+  for (const at::Tensor& t : self) d.push_back(desc(t));
+  std::vector<const mi_tensor_t*> ptr;
+  for (const auto& x : d) ptr.push_back(&x);
+  const mi_tensor_t fi = desc(found_inf), is = desc(inv_scale);
+  check_mi(mi_amp_unscale(ptr.data(), (int32_t)ptr.size(), &fi, &is, mi_stream(self[0])),
+           "_amp_foreach_non_finite_check_and_unscale_");
+}
+
 }  // namespace aotops
 }  // namespace torch_gcu

@@ -275,10 +275,92 @@ __global__ __launch_bounds__(256) void foreach_add_scalar_kernel(ForeachArgs a) 
   }
 }
 
+// _amp_foreach_non_finite_check_and_unscale_: every element *= inv_scale
+// (left as it is when inv_scale is 1), and found_inf = 1 when any element
+// was inf or NaN.  Every block that saw one stores the same 1.0, so the
+// stores need no ordering.
 template <typename Tag>
-mi_status_t launch_foreach(ForeachArgs& a, int64_t blocks, hipStream_t s) {
+__global__ __launch_bounds__(256) void amp_unscale_kernel(ForeachArgs a, float* found_inf,
+                                                          const float* inv_scale) {
+  typedef typename Num<Tag>::storage St;
+  typedef typename Num<Tag>::acc Acc;
+  int lo = 0, hi = a.count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)blockIdx.x >= a.t[mid].first_block) lo = mid;
+    else hi = mid - 1;
+  }
+  const ForeachTensor& t = a.t[lo];
+  St* p = (St*)t.p;
+  const float sc = *inv_scale;
+  bool bad = false;
+  const int64_t base = ((int64_t)blockIdx.x - t.first_block) * kForeachChunk;
+  for (int k = threadIdx.x; k < kForeachChunk; k += 256) {
+    const int64_t i = base + k;
+    if (i >= t.n) break;
+    const Acc v = Num<Tag>::load(p[i]);
+    if (!isfinite(v)) bad = true;
+    if (sc != 1.0f) p[i] = Num<Tag>::store(v * (Acc)sc);
+  }
+  if (bad) *found_inf = 1.0f;
+}
+
+template <typename Tag>
+mi_status_t launch_foreach(ForeachArgs& a, int64_t blocks, hipStream_t s, float* found_inf,
+                           const float* inv_scale) {
+  if (found_inf != nullptr) {
+    hipLaunchKernelGGL((amp_unscale_kernel<Tag>), dim3((unsigned)blocks), dim3(256), 0, s, a,
+                       found_inf, inv_scale);
+    return check_launch("amp_unscale");
+  }
   hipLaunchKernelGGL((foreach_add_scalar_kernel<Tag>), dim3((unsigned)blocks), dim3(256), 0, s, a);
   return check_launch("foreach_add_scalar");
+}
+
+// The multi-tensor walk shared by both list ops: found_inf == NULL means
+// "add value", else "unscale and check".
+mi_status_t foreach_run(const mi_tensor_t* const* tensors, int32_t n_tensors, double value,
+                        float* found_inf, const float* inv_scale, const char* what,
+                        hipStream_t stream) {
+  MI_CHECK_ARG(n_tensors >= 0 && (n_tensors == 0 || tensors != nullptr), "%s: bad tensor list", what);
+  if (n_tensors == 0) return MI_OK;
+  const int dt = tensors[0] != nullptr ? tensors[0]->dtype : -1;
+  MI_CHECK_ARG(dt == MI_F32 || dt == MI_BF16 || dt == MI_F16 || dt == MI_F64,
+               "%s: tensors must be float32, bfloat16, float16 or float64", what);
+  ForeachArgs a{};
+  a.value = value;
+  int k = 0;
+  int64_t blocks = 0;
+  auto flush = [&]() -> mi_status_t {
+    if (k == 0) return MI_OK;
+    a.count = k;
+    mi_status_t st;
+    switch (dt) {
+      case MI_F32: st = launch_foreach<float>(a, blocks, stream, found_inf, inv_scale); break;
+      case MI_BF16: st = launch_foreach<BF16>(a, blocks, stream, found_inf, inv_scale); break;
+      case MI_F16: st = launch_foreach<F16>(a, blocks, stream, found_inf, inv_scale); break;
+      default: st = launch_foreach<double>(a, blocks, stream, found_inf, inv_scale); break;
+    }
+    k = 0;
+    blocks = 0;
+    return st;
+  };
+  for (int i = 0; i < n_tensors; ++i) {
+    const mi_tensor_t* t = tensors[i];
+    MI_RETURN_IF(validate(t, "tensor"));
+    MI_CHECK_ARG(t->dtype == dt, "%s: tensor %d is %s, tensor 0 is %s", what, i,
+                 dtype_name(t->dtype), dtype_name(dt));
+    const int64_t n = numel(*t);
+    if (n == 0) continue;
+    MI_CHECK_ARG(dense_any_order(*t), "%s: tensor %d is not dense", what, i);
+    a.t[k].p = t->data;
+    a.t[k].n = n;
+    a.t[k].first_block = blocks;
+    blocks += (n + kForeachChunk - 1) / kForeachChunk;
+    MI_CHECK_ARG(blocks <= 0x7fffffffLL, "%s: too many blocks", what);
+    if (++k == kForeachMax) MI_RETURN_IF(flush());
+  }
+  return flush();
 }
 
 }  // namespace
@@ -289,47 +371,22 @@ using namespace mi;
 extern "C" mi_status_t mi_foreach_add_scalar(const mi_tensor_t* const* tensors, int32_t n_tensors,
                                              double value, mi_stream_t stream_) {
   clear_error();
-  hipStream_t stream = (hipStream_t)stream_;
-  MI_CHECK_ARG(n_tensors >= 0 && (n_tensors == 0 || tensors != nullptr),
-               "foreach_add_scalar: bad tensor list");
-  if (n_tensors == 0) return MI_OK;
-  const int dt = tensors[0] != nullptr ? tensors[0]->dtype : -1;
-  MI_CHECK_ARG(dt == MI_F32 || dt == MI_BF16 || dt == MI_F16 || dt == MI_F64,
-               "foreach_add_scalar: tensors must be float32, bfloat16, float16 or float64");
-  ForeachArgs a{};
-  a.value = value;
-  int k = 0;
-  int64_t blocks = 0;
-  auto flush = [&]() -> mi_status_t {
-    if (k == 0) return MI_OK;
-    a.count = k;
-    mi_status_t st;
-    switch (dt) {
-      case MI_F32: st = launch_foreach<float>(a, blocks, stream); break;
-      case MI_BF16: st = launch_foreach<BF16>(a, blocks, stream); break;
-      case MI_F16: st = launch_foreach<F16>(a, blocks, stream); break;
-      default: st = launch_foreach<double>(a, blocks, stream); break;
-    }
-    k = 0;
-    blocks = 0;
-    return st;
-  };
-  for (int i = 0; i < n_tensors; ++i) {
-    const mi_tensor_t* t = tensors[i];
-    MI_RETURN_IF(validate(t, "tensor"));
-    MI_CHECK_ARG(t->dtype == dt, "foreach_add_scalar: tensor %d is %s, tensor 0 is %s", i,
-                 dtype_name(t->dtype), dtype_name(dt));
-    const int64_t n = numel(*t);
-    if (n == 0) continue;
-    MI_CHECK_ARG(dense_any_order(*t), "foreach_add_scalar: tensor %d is not dense", i);
-    a.t[k].p = t->data;
-    a.t[k].n = n;
-    a.t[k].first_block = blocks;
-    blocks += (n + kForeachChunk - 1) / kForeachChunk;
-    MI_CHECK_ARG(blocks <= 0x7fffffffLL, "foreach_add_scalar: too many blocks");
-    if (++k == kForeachMax) MI_RETURN_IF(flush());
-  }
-  return flush();
+  return foreach_run(tensors, n_tensors, value, nullptr, nullptr, "foreach_add_scalar",
+                     (hipStream_t)stream_);
+}
+
+extern "C" mi_status_t mi_amp_unscale(const mi_tensor_t* const* tensors, int32_t n_tensors,
+                                      const mi_tensor_t* found_inf, const mi_tensor_t* inv_scale,
+                                      mi_stream_t stream_) {
+  clear_error();
+  MI_RETURN_IF(validate(found_inf, "found_inf"));
+  MI_RETURN_IF(validate(inv_scale, "inv_scale"));
+  MI_CHECK_ARG(numel(*found_inf) == 1 && found_inf->dtype == MI_F32,
+               "amp_unscale: found_inf must be a one-element float32 tensor");
+  MI_CHECK_ARG(numel(*inv_scale) == 1 && inv_scale->dtype == MI_F32,
+               "amp_unscale: inv_scale must be a one-element float32 tensor");
+  return foreach_run(tensors, n_tensors, 0.0, (float*)found_inf->data,
+                     (const float*)inv_scale->data, "amp_unscale", (hipStream_t)stream_);
 }
 
 extern "C" mi_status_t mi_fused_adamw(

@@ -75,6 +75,7 @@ _SIGNATURES = {
     "mi_cat": ([_T, ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_int32, _S], ctypes.c_int),
     "mi_silu_backward": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_foreach_add_scalar": ([ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_double, _S], ctypes.c_int),
+    "mi_amp_unscale": ([ctypes.POINTER(_T), ctypes.c_int32, _T, _T, _S], ctypes.c_int),
     "mi_log_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_layer_norm_backward": ([_T] * 8 + [ctypes.c_int64, _S], ctypes.c_int),
@@ -252,6 +253,15 @@ def foreach_add_scalar_(tensors, value):
     arr = (_T * max(1, len(ds)))(*[ctypes.pointer(d) for d in ds])
     check("mi_foreach_add_scalar", lib().mi_foreach_add_scalar(
         arr, len(ds), value, stream_of(tensors[0]) if tensors else torch.cuda.current_stream().cuda_stream))
+    return tensors
+
+
+def amp_unscale_(tensors, found_inf, inv_scale):
+    """GradScaler's unscale and inf / NaN check through mi_amp_unscale."""
+    ds = [desc(t) for t in tensors]
+    arr = (_T * max(1, len(ds)))(*[ctypes.pointer(d) for d in ds])
+    check("mi_amp_unscale", lib().mi_amp_unscale(arr, len(ds), desc(found_inf), desc(inv_scale),
+                                                 stream_of(found_inf)))
     return tensors
 
 
