@@ -214,6 +214,18 @@ mi_status_t mi_amp_unscale(const mi_tensor_t* const* tensors, int32_t n_tensors,
                            const mi_tensor_t* found_inf,
                            const mi_tensor_t* inv_scale, mi_stream_t stream);
 
+/* GradScaler's scale update in place: when found_inf is nonzero the scale is
+ * multiplied by backoff_factor and growth_tracker set to 0; otherwise
+ * growth_tracker counts up, and on reaching growth_interval the scale is
+ * multiplied by growth_factor (kept only if finite) and the count restarts.
+ * scale and found_inf are one-element float32, growth_tracker one-element
+ * int32, all device tensors.  Replaces the generated _amp_update_scale_
+ * (yaml :16). */
+mi_status_t mi_amp_update_scale(const mi_tensor_t* scale, const mi_tensor_t* growth_tracker,
+                                const mi_tensor_t* found_inf, double growth_factor,
+                                double backoff_factor, int64_t growth_interval,
+                                mi_stream_t stream);
+
 /* ---- indexing ---------------------------------------------------------- */
 
 /* out = self.index_select(dim, index); index is 1-D (or 0-D) int32/int64;

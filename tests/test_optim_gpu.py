@@ -175,3 +175,55 @@ def test_amp_unscale_parity(dtype):
         assert float(dfi.cpu()) == float(fi) == (0.0 if poison is None else 1.0)
         for a, b in zip(dg, cg):
             assert_close(a.cpu(), b, "fp32" if dtype == torch.float32 else "bf16", f"unscale {inv}")
+
+
+def test_amp_update_scale_parity():
+    """_amp_update_scale_ follows CPU ATen's over a sequence of clean and
+    overflowing steps: growth after growth_interval clean steps, back-off and
+    a restarted count on inf, and a growth that would overflow fp32 is not
+    taken."""
+    for start in (65536.0, 3.0e38):
+        cs, ct = torch.tensor([start]), torch.tensor([0], dtype=torch.int32)
+        ds, dt = cs.to("gcu"), ct.to("gcu")
+        for k, bad in enumerate([0, 0, 0, 1, 0, 0, 0, 0, 1, 1, 0, 0, 0]):
+            cf = torch.tensor([float(bad)])
+            torch._amp_update_scale_(cs, ct, cf, 2.0, 0.5, 3)
+            torch._amp_update_scale_(ds, dt, cf.to("gcu"), 2.0, 0.5, 3)
+            assert float(ds.cpu()) == float(cs) and int(dt.cpu()) == int(ct), (start, k)
+
+
+def test_grad_scaler_with_fused_adamw_on_gcu():
+    """torch.amp.GradScaler over AdamW(fused=True): the unscale check, the
+    fused step with grad_scale / found_inf and the scale update all run
+    natively, an overflowing step is skipped, and the parameters and scale
+    follow the same loop on CPU."""
+    torch.manual_seed(0)
+    ref = [torch.randn(64, 32) * 0.1, torch.randn(64) * 0.1]
+    res = {}
+    C._set_op_debug_config("op_statistics=true")
+    C._clear_op_statistics()
+    try:
+        for dev in ("gcu", "cpu"):
+            ps = [torch.nn.Parameter(t.clone().to(dev)) for t in ref]
+            opt = torch.optim.AdamW(ps, lr=1e-2, fused=True)
+            scaler = torch.amp.GradScaler(dev, init_scale=1024.0, growth_interval=2)
+            for it in range(5):
+                x = torch.randn(16, 32, generator=g(800 + it)).to(dev)
+                loss = torch.nn.functional.linear(x, ps[0], ps[1]).pow(2).mean()
+                if it == 2:
+                    loss = loss * float("inf")
+                opt.zero_grad()
+                scaler.scale(loss).backward()
+                scaler.step(opt)
+                scaler.update()
+            res[dev] = ([p.detach().cpu() for p in ps], float(scaler.get_scale()))
+            if dev == "gcu":
+                torch.gcu.synchronize()
+                stats = C._op_statistics()
+    finally:
+        C._set_op_debug_config("")
+    for a, b in zip(res["gcu"][0], res["cpu"][0]):
+        assert_close(a, b, "fp32", "GradScaler + AdamW(fused=True) params")
+    assert res["gcu"][1] == res["cpu"][1]
+    for op in ("_amp_foreach_non_finite_check_and_unscale_", "_amp_update_scale_", "_fused_adamw_"):
+        assert stats.get(op, (0, 0))[0] >= 4 and stats[op][1] == 0, (op, stats.get(op))

@@ -203,5 +203,27 @@ void _amp_foreach_non_finite_check_and_unscale_(at::TensorList self, at::Tensor&
            "_amp_foreach_non_finite_check_and_unscale_");
 }
 
+// GradScaler's scale update (the reference's generated _amp_update_scale_,
+// yaml :16) on the device; tensors on another device or of other dtypes go
+// to CPU ATen, which raises ATen's own errors for them.
+at::Tensor& _amp_update_scale_(at::Tensor& self, at::Tensor& growth_tracker,
+                               const at::Tensor& found_inf, double scale_growth_factor,
+                               double scale_backoff_factor, int64_t growth_interval) {
+  const bool fast = self.numel() == 1 && self.scalar_type() == at::kFloat &&
+                    growth_tracker.numel() == 1 && growth_tracker.scalar_type() == at::kInt &&
+                    found_inf.numel() == 1 && found_inf.scalar_type() == at::kFloat &&
+                    growth_tracker.device() == self.device() && found_inf.device() == self.device();
+  if (!fast)
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP(_amp_update_scale_)>::call(
+        self, growth_tracker, found_inf, scale_growth_factor, scale_backoff_factor,
+        growth_interval);
+  c10::DeviceGuard g(self.device());
+  const mi_tensor_t s = desc(self), gt = desc(growth_tracker), fi = desc(found_inf);
+  check_mi(mi_amp_update_scale(&s, &gt, &fi, scale_growth_factor, scale_backoff_factor,
+                               growth_interval, mi_stream(self)),
+           "_amp_update_scale_");
+  return self;
+}
+
 }  // namespace aotops
 }  // namespace torch_gcu

@@ -389,6 +389,51 @@ extern "C" mi_status_t mi_amp_unscale(const mi_tensor_t* const* tensors, int32_t
                      (const float*)inv_scale->data, "amp_unscale", (hipStream_t)stream_);
 }
 
+// GradScaler's scale update, one lane: on inf / NaN the scale backs off and
+// the growth count restarts; after growth_interval clean steps the scale
+// grows (kept only when the grown value is finite).  The products are taken
+// in fp64 and rounded once to fp32.
+__global__ __launch_bounds__(64) void amp_update_scale_kernel(float* scale, int32_t* tracker,
+                                                              const float* found_inf,
+                                                              double growth, double backoff,
+                                                              int64_t interval) {
+  if (threadIdx.x != 0) return;
+  if (*found_inf != 0.0f) {
+    *scale = (float)((double)*scale * backoff);
+    *tracker = 0;
+    return;
+  }
+  const int64_t good = (int64_t)*tracker + 1;
+  if (good == interval) {
+    const float grown = (float)((double)*scale * growth);
+    if (isfinite(grown)) *scale = grown;
+    *tracker = 0;
+  } else {
+    *tracker = (int32_t)good;
+  }
+}
+
+extern "C" mi_status_t mi_amp_update_scale(const mi_tensor_t* scale,
+                                           const mi_tensor_t* growth_tracker,
+                                           const mi_tensor_t* found_inf, double growth_factor,
+                                           double backoff_factor, int64_t growth_interval,
+                                           mi_stream_t stream_) {
+  clear_error();
+  MI_RETURN_IF(validate(scale, "scale"));
+  MI_RETURN_IF(validate(growth_tracker, "growth_tracker"));
+  MI_RETURN_IF(validate(found_inf, "found_inf"));
+  MI_CHECK_ARG(numel(*scale) == 1 && scale->dtype == MI_F32,
+               "amp_update_scale: current_scale must be a one-element float32 tensor");
+  MI_CHECK_ARG(numel(*growth_tracker) == 1 && growth_tracker->dtype == MI_I32,
+               "amp_update_scale: growth_tracker must be a one-element int32 tensor");
+  MI_CHECK_ARG(numel(*found_inf) == 1 && found_inf->dtype == MI_F32,
+               "amp_update_scale: found_inf must be a one-element float32 tensor");
+  hipLaunchKernelGGL(amp_update_scale_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream_,
+                     (float*)scale->data, (int32_t*)growth_tracker->data,
+                     (const float*)found_inf->data, growth_factor, backoff_factor, growth_interval);
+  return check_launch("amp_update_scale");
+}
+
 extern "C" mi_status_t mi_fused_adamw(
     const mi_tensor_t* const* params, const mi_tensor_t* const* grads,
     const mi_tensor_t* const* exp_avgs, const mi_tensor_t* const* exp_avg_sqs,

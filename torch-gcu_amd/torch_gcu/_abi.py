@@ -76,6 +76,8 @@ _SIGNATURES = {
     "mi_silu_backward": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_foreach_add_scalar": ([ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_double, _S], ctypes.c_int),
     "mi_amp_unscale": ([ctypes.POINTER(_T), ctypes.c_int32, _T, _T, _S], ctypes.c_int),
+    "mi_amp_update_scale": ([_T, _T, _T, ctypes.c_double, ctypes.c_double, ctypes.c_int64, _S],
+                            ctypes.c_int),
     "mi_log_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_softmax_backward": ([_T, _T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_layer_norm_backward": ([_T] * 8 + [ctypes.c_int64, _S], ctypes.c_int),
@@ -263,6 +265,14 @@ def amp_unscale_(tensors, found_inf, inv_scale):
     check("mi_amp_unscale", lib().mi_amp_unscale(arr, len(ds), desc(found_inf), desc(inv_scale),
                                                  stream_of(found_inf)))
     return tensors
+
+
+def amp_update_scale_(scale, growth_tracker, found_inf, growth_factor, backoff_factor, interval):
+    """GradScaler's scale update through mi_amp_update_scale."""
+    check("mi_amp_update_scale", lib().mi_amp_update_scale(
+        desc(scale), desc(growth_tracker), desc(found_inf), float(growth_factor),
+        float(backoff_factor), int(interval), stream_of(scale)))
+    return scale
 
 
 def silu_backward(grad_input, grad_output, self):
