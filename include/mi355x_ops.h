@@ -204,6 +204,14 @@ mi_status_t mi_foreach_add_scalar(const mi_tensor_t* const* tensors,
                                   int32_t n_tensors, double value,
                                   mi_stream_t stream);
 
+/* Every tensor of the list *= one value, in place: `scalar` (a one-element
+ * float32 device tensor read by the kernel) when it is non-NULL, else
+ * `value`.  The list is dense tensors of one float dtype, as for
+ * mi_foreach_add_scalar.  Replaces the generated _foreach_mul_.Scalar and
+ * _foreach_mul_.Tensor (yaml :131, :133). */
+mi_status_t mi_foreach_mul_scalar(const mi_tensor_t* const* tensors, int32_t n_tensors,
+                                  double value, const mi_tensor_t* scalar, mi_stream_t stream);
+
 /* Mixed-precision grad unscaling: every element of the n_tensors dense
  * tensors (one dtype: f32, bf16, f16, f64) *= inv_scale in place (left as it
  * is when inv_scale is 1), and found_inf is set to 1 when any element is inf

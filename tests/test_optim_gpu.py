@@ -227,3 +227,53 @@ def test_grad_scaler_with_fused_adamw_on_gcu():
     assert res["gcu"][1] == res["cpu"][1]
     for op in ("_amp_foreach_non_finite_check_and_unscale_", "_amp_update_scale_", "_fused_adamw_"):
         assert stats.get(op, (0, 0))[0] >= 4 and stats[op][1] == 0, (op, stats.get(op))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
+def test_foreach_mul_parity(dtype):
+    """_foreach_mul_ by a Python scalar, by a 0-dim fp32 scalar on the device
+    (read by the kernel, as gradient clipping passes it) and by a CPU scalar
+    tensor, over 70 tensors with an empty one and a misaligned view, equals
+    CPU ATen's; an integer list takes the per-tensor path."""
+    shapes = [(7,), (), (0,), (33, 65), (5000,)] * 14
+    bar = "fp32" if dtype in (torch.float32, torch.float64) else "bf16"
+    for k, other in enumerate((0.37, torch.tensor(0.37), torch.tensor(-1.75))):
+        base = torch.randn(1 + 513, generator=g(900 + k)).to(dtype)
+        ts = [torch.randn(s, generator=g(910 + k * 100 + i)).to(dtype) for i, s in enumerate(shapes)]
+        ts.append(base[1:])
+        dbase = base.to("gcu")
+        dts = [t.to("gcu") for t in ts[:-1]] + [dbase[1:]]
+        want = [t.clone() for t in ts]
+        torch._foreach_mul_(want, other)
+        dother = other.to("gcu") if (isinstance(other, torch.Tensor) and k == 1) else other
+        torch._foreach_mul_(dts, dother)
+        for a, b in zip(dts, want):
+            assert_close(a.cpu(), b, bar, f"foreach_mul_ {k}")
+        assert float(dbase[0].cpu()) == float(base[0])
+    ints = [torch.arange(5).to("gcu")]
+    torch._foreach_mul_(ints, 3)
+    assert torch.equal(ints[0].cpu(), torch.arange(5) * 3)
+
+
+def test_clip_grad_norm_foreach_on_gcu():
+    """torch.nn.utils.clip_grad_norm_(foreach=True) scales gcu gradients with
+    the native _foreach_mul_.Tensor and matches the CPU result."""
+    grads = [torch.randn(s, generator=g(990 + i)) * 3 for i, s in enumerate([(64, 32), (64,), (7, 5)])]
+    cps = [torch.nn.Parameter(torch.zeros(gr.shape)) for gr in grads]
+    dps = [torch.nn.Parameter(torch.zeros(gr.shape, device="gcu")) for gr in grads]
+    for c, d, gr in zip(cps, dps, grads):
+        c.grad, d.grad = gr.clone(), gr.to("gcu")
+    C._set_op_debug_config("op_statistics=true")
+    C._clear_op_statistics()
+    try:
+        dn = torch.nn.utils.clip_grad_norm_(dps, 1.0, foreach=True)
+        torch.gcu.synchronize()
+        stats = C._op_statistics()
+    finally:
+        C._set_op_debug_config("")
+    cn = torch.nn.utils.clip_grad_norm_(cps, 1.0, foreach=True)
+    assert_close(dn.cpu(), cn, "fp32", "total norm")
+    for c, d in zip(cps, dps):
+        assert_close(d.grad.cpu(), c.grad, "fp32", "clipped grad")
+    st = stats.get("_foreach_mul_.Tensor", (0, 0))
+    assert st[0] == 1 and st[1] == 0, stats

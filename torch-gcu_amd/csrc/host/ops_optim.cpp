@@ -150,26 +150,81 @@ void _fused_adamw__tensor_lr(at::TensorList self, at::TensorList grads, at::Tens
 // _foreach_add_.Scalar, yaml :47): one multi-tensor launch when the list is
 // dense and of one float dtype with a real scalar, else ATen's per-tensor
 // add_ (which runs on the native elementwise kernel).
-void _foreach_add__Scalar(at::TensorList self, const at::Scalar& scalar) {
-  if (self.empty()) return;
+namespace {
+
+// One multi-tensor launch when the list is dense and of one float dtype on
+// one device; false when the caller must take ATen's per-tensor path.
+bool foreach_fast(at::TensorList self) {
   const at::ScalarType dt = self[0].scalar_type();
-  bool fast = kernel_dtype(dt) && !scalar.isComplex() && !scalar.isBoolean();
+  bool fast = kernel_dtype(dt);
   for (const at::Tensor& t : self)
     fast = fast && t.scalar_type() == dt && t.device() == self[0].device() &&
            (t.numel() == 0 || t.is_non_overlapping_and_dense());
-  if (!fast) {
-    for (const at::Tensor& t : self) const_cast<at::Tensor&>(t).add_(scalar);
-    return;
-  }
+  return fast;
+}
+
+template <typename F>
+void foreach_launch(at::TensorList self, const char* what, F&& call) {
   c10::DeviceGuard g(self[0].device());
   std::vector<mi_tensor_t> d;
   d.reserve(self.size());
   for (const at::Tensor& t : self) d.push_back(desc(t));
   std::vector<const mi_tensor_t*> ptr;
   for (const auto& x : d) ptr.push_back(&x);
-  check_mi(mi_foreach_add_scalar(ptr.data(), (int32_t)ptr.size(), scalar.toDouble(),
-                                 mi_stream(self[0])),
-           "_foreach_add_");
+  check_mi(call(ptr.data(), (int32_t)ptr.size(), mi_stream(self[0])), what);
+}
+
+bool real_scalar(const at::Scalar& s) { return !s.isComplex() && !s.isBoolean(); }
+
+}  // namespace
+
+void _foreach_add__Scalar(at::TensorList self, const at::Scalar& scalar) {
+  if (self.empty()) return;
+  if (!foreach_fast(self) || !real_scalar(scalar)) {
+    for (const at::Tensor& t : self) const_cast<at::Tensor&>(t).add_(scalar);
+    return;
+  }
+  foreach_launch(self, "_foreach_add_", [&](const mi_tensor_t* const* p, int32_t n, mi_stream_t s) {
+    return mi_foreach_add_scalar(p, n, scalar.toDouble(), s);
+  });
+}
+
+// _foreach_mul_.Scalar (yaml :131): the same launch with a product.
+void _foreach_mul__Scalar(at::TensorList self, const at::Scalar& scalar) {
+  if (self.empty()) return;
+  if (!foreach_fast(self) || !real_scalar(scalar)) {
+    for (const at::Tensor& t : self) const_cast<at::Tensor&>(t).mul_(scalar);
+    return;
+  }
+  foreach_launch(self, "_foreach_mul_", [&](const mi_tensor_t* const* p, int32_t n, mi_stream_t s) {
+    return mi_foreach_mul_scalar(p, n, scalar.toDouble(), nullptr, s);
+  });
+}
+
+// _foreach_mul_.Tensor (yaml :133), as gradient clipping calls it: a 0-dim
+// fp32 scalar on the list's device is read by the kernel (no host sync); a
+// CPU scalar is read on the host; other scalars take ATen's per-tensor mul_.
+void _foreach_mul__Tensor(at::TensorList self, const at::Tensor& other) {
+  TORCH_CHECK(other.dim() == 0, "scalar tensor expected to be 0 dim but it has ", other.dim(),
+              " dimensions and ", other.numel(), " elements.");
+  if (self.empty()) return;
+  const bool on_dev = other.device() == self[0].device() && other.scalar_type() == at::kFloat;
+  if (!foreach_fast(self) || !(on_dev || (other.is_cpu() && !other.is_complex() &&
+                                          other.scalar_type() != at::kBool))) {
+    for (const at::Tensor& t : self) const_cast<at::Tensor&>(t).mul_(other);
+    return;
+  }
+  if (on_dev) {
+    const mi_tensor_t sd = desc(other);
+    foreach_launch(self, "_foreach_mul_", [&](const mi_tensor_t* const* p, int32_t n, mi_stream_t s) {
+      return mi_foreach_mul_scalar(p, n, 0.0, &sd, s);
+    });
+    return;
+  }
+  const double v = other.item<double>();
+  foreach_launch(self, "_foreach_mul_", [&](const mi_tensor_t* const* p, int32_t n, mi_stream_t s) {
+    return mi_foreach_mul_scalar(p, n, v, nullptr, s);
+  });
 }
 
 // GradScaler's unscale step (the reference's generated

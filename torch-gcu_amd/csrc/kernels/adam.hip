@@ -235,10 +235,12 @@ mi_status_t launch_adam(AdamArgs& a, bool ams, hipStream_t s, int64_t blocks) {
   return check_launch("fused_adamw");
 }
 
-// _foreach_add_.Scalar: every tensor of a list += value, in place (the
-// optimizer's step-count advance).  One launch per kForeachMax tensors, the
-// table in kernel arguments as for AdamW; the sum in fp32 (fp64 for fp64),
-// rounded once.
+// _foreach_add_.Scalar / _foreach_mul_.Scalar / _foreach_mul_.Tensor: every
+// tensor of a list += or *= one value, in place (the optimizer's step-count
+// advance, gradient clipping's scale).  One launch per kForeachMax tensors,
+// the table in kernel arguments as for AdamW; the value is a host double or
+// a one-element fp32 device tensor read by the kernel; the arithmetic in fp32
+// (fp64 for fp64), rounded once.
 constexpr int kForeachMax = 64;
 constexpr int kForeachChunk = 1024;  // elements per block
 
@@ -254,8 +256,10 @@ struct ForeachArgs {
   double value;
 };
 
-template <typename Tag>
-__global__ __launch_bounds__(256) void foreach_add_scalar_kernel(ForeachArgs a) {
+enum ForeachOp { FE_ADD = 0, FE_MUL = 1 };
+
+template <typename Tag, int OP>
+__global__ __launch_bounds__(256) void foreach_scalar_kernel(ForeachArgs a, const float* dev_value) {
   typedef typename Num<Tag>::storage St;
   typedef typename Num<Tag>::acc Acc;
   int lo = 0, hi = a.count - 1;
@@ -266,12 +270,13 @@ __global__ __launch_bounds__(256) void foreach_add_scalar_kernel(ForeachArgs a) 
   }
   const ForeachTensor& t = a.t[lo];
   St* p = (St*)t.p;
-  const Acc v = (Acc)a.value;
+  const Acc v = dev_value != nullptr ? (Acc)*dev_value : (Acc)a.value;
   const int64_t base = ((int64_t)blockIdx.x - t.first_block) * kForeachChunk;
   for (int k = threadIdx.x; k < kForeachChunk; k += 256) {
     const int64_t i = base + k;
     if (i >= t.n) break;
-    p[i] = Num<Tag>::store(Num<Tag>::load(p[i]) + v);
+    const Acc x = Num<Tag>::load(p[i]);
+    p[i] = Num<Tag>::store(OP == FE_ADD ? x + v : x * v);
   }
 }
 
@@ -306,22 +311,27 @@ __global__ __launch_bounds__(256) void amp_unscale_kernel(ForeachArgs a, float* 
 }
 
 template <typename Tag>
-mi_status_t launch_foreach(ForeachArgs& a, int64_t blocks, hipStream_t s, float* found_inf,
-                           const float* inv_scale) {
+mi_status_t launch_foreach(ForeachArgs& a, int64_t blocks, hipStream_t s, int op,
+                           const float* dev_value, float* found_inf, const float* inv_scale) {
   if (found_inf != nullptr) {
     hipLaunchKernelGGL((amp_unscale_kernel<Tag>), dim3((unsigned)blocks), dim3(256), 0, s, a,
                        found_inf, inv_scale);
     return check_launch("amp_unscale");
   }
-  hipLaunchKernelGGL((foreach_add_scalar_kernel<Tag>), dim3((unsigned)blocks), dim3(256), 0, s, a);
-  return check_launch("foreach_add_scalar");
+  if (op == FE_MUL)
+    hipLaunchKernelGGL((foreach_scalar_kernel<Tag, FE_MUL>), dim3((unsigned)blocks), dim3(256), 0,
+                       s, a, dev_value);
+  else
+    hipLaunchKernelGGL((foreach_scalar_kernel<Tag, FE_ADD>), dim3((unsigned)blocks), dim3(256), 0,
+                       s, a, dev_value);
+  return check_launch("foreach_scalar");
 }
 
-// The multi-tensor walk shared by both list ops: found_inf == NULL means
-// "add value", else "unscale and check".
-mi_status_t foreach_run(const mi_tensor_t* const* tensors, int32_t n_tensors, double value,
-                        float* found_inf, const float* inv_scale, const char* what,
-                        hipStream_t stream) {
+// The multi-tensor walk shared by the list ops: found_inf == NULL means
+// "add or multiply by the value", else "unscale and check".
+mi_status_t foreach_run(const mi_tensor_t* const* tensors, int32_t n_tensors, double value, int op,
+                        const float* dev_value, float* found_inf, const float* inv_scale,
+                        const char* what, hipStream_t stream) {
   MI_CHECK_ARG(n_tensors >= 0 && (n_tensors == 0 || tensors != nullptr), "%s: bad tensor list", what);
   if (n_tensors == 0) return MI_OK;
   const int dt = tensors[0] != nullptr ? tensors[0]->dtype : -1;
@@ -336,10 +346,10 @@ mi_status_t foreach_run(const mi_tensor_t* const* tensors, int32_t n_tensors, do
     a.count = k;
     mi_status_t st;
     switch (dt) {
-      case MI_F32: st = launch_foreach<float>(a, blocks, stream, found_inf, inv_scale); break;
-      case MI_BF16: st = launch_foreach<BF16>(a, blocks, stream, found_inf, inv_scale); break;
-      case MI_F16: st = launch_foreach<F16>(a, blocks, stream, found_inf, inv_scale); break;
-      default: st = launch_foreach<double>(a, blocks, stream, found_inf, inv_scale); break;
+      case MI_F32: st = launch_foreach<float>(a, blocks, stream, op, dev_value, found_inf, inv_scale); break;
+      case MI_BF16: st = launch_foreach<BF16>(a, blocks, stream, op, dev_value, found_inf, inv_scale); break;
+      case MI_F16: st = launch_foreach<F16>(a, blocks, stream, op, dev_value, found_inf, inv_scale); break;
+      default: st = launch_foreach<double>(a, blocks, stream, op, dev_value, found_inf, inv_scale); break;
     }
     k = 0;
     blocks = 0;
@@ -371,8 +381,23 @@ using namespace mi;
 extern "C" mi_status_t mi_foreach_add_scalar(const mi_tensor_t* const* tensors, int32_t n_tensors,
                                              double value, mi_stream_t stream_) {
   clear_error();
-  return foreach_run(tensors, n_tensors, value, nullptr, nullptr, "foreach_add_scalar",
-                     (hipStream_t)stream_);
+  return foreach_run(tensors, n_tensors, value, FE_ADD, nullptr, nullptr, nullptr,
+                     "foreach_add_scalar", (hipStream_t)stream_);
+}
+
+extern "C" mi_status_t mi_foreach_mul_scalar(const mi_tensor_t* const* tensors, int32_t n_tensors,
+                                             double value, const mi_tensor_t* scalar,
+                                             mi_stream_t stream_) {
+  clear_error();
+  const float* dev = nullptr;
+  if (scalar != nullptr) {
+    MI_RETURN_IF(validate(scalar, "scalar"));
+    MI_CHECK_ARG(numel(*scalar) == 1 && scalar->dtype == MI_F32,
+                 "foreach_mul_scalar: scalar must be a one-element float32 tensor");
+    dev = (const float*)scalar->data;
+  }
+  return foreach_run(tensors, n_tensors, value, FE_MUL, dev, nullptr, nullptr,
+                     "foreach_mul_scalar", (hipStream_t)stream_);
 }
 
 extern "C" mi_status_t mi_amp_unscale(const mi_tensor_t* const* tensors, int32_t n_tensors,
@@ -385,7 +410,7 @@ extern "C" mi_status_t mi_amp_unscale(const mi_tensor_t* const* tensors, int32_t
                "amp_unscale: found_inf must be a one-element float32 tensor");
   MI_CHECK_ARG(numel(*inv_scale) == 1 && inv_scale->dtype == MI_F32,
                "amp_unscale: inv_scale must be a one-element float32 tensor");
-  return foreach_run(tensors, n_tensors, 0.0, (float*)found_inf->data,
+  return foreach_run(tensors, n_tensors, 0.0, FE_MUL, nullptr, (float*)found_inf->data,
                      (const float*)inv_scale->data, "amp_unscale", (hipStream_t)stream_);
 }
 

@@ -75,6 +75,8 @@ _SIGNATURES = {
     "mi_cat": ([_T, ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_int32, _S], ctypes.c_int),
     "mi_silu_backward": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_foreach_add_scalar": ([ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_double, _S], ctypes.c_int),
+    "mi_foreach_mul_scalar": ([ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_double, _T, _S],
+                              ctypes.c_int),
     "mi_amp_unscale": ([ctypes.POINTER(_T), ctypes.c_int32, _T, _T, _S], ctypes.c_int),
     "mi_amp_update_scale": ([_T, _T, _T, ctypes.c_double, ctypes.c_double, ctypes.c_int64, _S],
                             ctypes.c_int),
@@ -255,6 +257,16 @@ def foreach_add_scalar_(tensors, value):
     arr = (_T * max(1, len(ds)))(*[ctypes.pointer(d) for d in ds])
     check("mi_foreach_add_scalar", lib().mi_foreach_add_scalar(
         arr, len(ds), value, stream_of(tensors[0]) if tensors else torch.cuda.current_stream().cuda_stream))
+    return tensors
+
+
+def foreach_mul_scalar_(tensors, value=0.0, scalar=None):
+    """Every tensor *= value (or the one-element fp32 device tensor `scalar`)."""
+    ds = [desc(t) for t in tensors]
+    arr = (_T * max(1, len(ds)))(*[ctypes.pointer(d) for d in ds])
+    sd = desc(scalar) if scalar is not None else None
+    check("mi_foreach_mul_scalar", lib().mi_foreach_mul_scalar(
+        arr, len(ds), float(value), sd, stream_of(tensors[0]) if tensors else None))
     return tensors
 
 
