@@ -246,6 +246,23 @@ mi_status_t mi_index_select(const mi_tensor_t* out, const mi_tensor_t* self,
                             int64_t dim, const mi_tensor_t* index,
                             mi_stream_t stream);
 
+/* out = self[indices] (advanced indexing, ATen's index.Tensor rules).
+ * indices has n_indices <= self.ndim entries, one per leading dim of self:
+ * NULL takes that dim whole, otherwise an int32 or int64 index tensor.  The
+ * defined index tensors must already be broadcast to one shape B (stride 0
+ * where broadcast).  When the indexed dims are adjacent,
+ * out.shape = self.shape[:first] + B + self.shape[last+1:]; otherwise
+ * out.shape = B + the other dims of self in order.  out is contiguous, of
+ * self's dtype.  int32 indices are read as int32 (no widening to int64).
+ * Negative indices count from the end of their dim; an index still out of
+ * range writes its out row as zeros (the kernel never reads outside self;
+ * the host layer raises the IndexError for host-side indices).  Replaces
+ * topsatenIndex behind device_int32_indices_index
+ * (torch_gcu/csrc/efficient_ops/ops.cpp:335-342, bridge_topsatenIndex_out1). */
+mi_status_t mi_index(const mi_tensor_t* out, const mi_tensor_t* self,
+                     const mi_tensor_t* const* indices, int32_t n_indices,
+                     mi_stream_t stream);
+
 /* ---- reductions ----------------------------------------------------------
  * dims lists the reduced dimensions of self (empty = all).  out holds
  * self's shape with reduced dims removed (keepdim=0) or set to 1
@@ -261,6 +278,7 @@ mi_status_t mi_amax(const mi_tensor_t* out, const mi_tensor_t* self,
 mi_status_t mi_mean(const mi_tensor_t* out, const mi_tensor_t* self,
                     const int64_t* dims, int32_t ndims, int32_t keepdim,
                     mi_stream_t stream);
+
 
 /* ---- softmax family -------------------------------------------------------
  * out = softmax / log_softmax of self along dim, computed in float; out may

@@ -257,3 +257,55 @@ def layer_norm_backward(grad_out, x, normalized_shape, mean, rstd, weight, bias,
     numpy_ref.layer_norm_backward64 and central differences of layer norm."""
     return torch.ops.aten.native_layer_norm_backward(grad_out, x, normalized_shape, mean, rstd,
                                                      weight, bias, mask)
+
+
+def foreach_add_scalar(tensors, value):
+    """aten::_foreach_add_.Scalar -> the generated foreach add
+    (codegen/gcu_native_functions.yaml:47): CPU ATen on clones; each element
+    plus the scalar in the op-math type (float for 16-bit inputs), rounded
+    once.  Pinned by the numpy float32 sum rounded to the dtype and by
+    x + 0 == x."""
+    c = [t.clone() for t in tensors]
+    torch._foreach_add_(c, value)
+    return c
+
+
+def foreach_mul(tensors, other):
+    """aten::_foreach_mul_.Scalar / .Tensor (codegen/gcu_native_functions.yaml:131,
+    :133): CPU ATen on clones.  Pinned by the numpy float32 product rounded to
+    the dtype, x * 1 == x and x * -1 == -x."""
+    c = [t.clone() for t in tensors]
+    torch._foreach_mul_(c, other)
+    return c
+
+
+def amp_unscale(grads, found_inf, inv_scale):
+    """aten::_amp_foreach_non_finite_check_and_unscale_
+    (codegen/gcu_native_functions.yaml:15): CPU ATen on clones; returns
+    (unscaled grads, found_inf).  Pinned by the numpy float32 product
+    rounded to the dtype, the inv_scale == 1 identity, and found_inf being 1
+    exactly when some element is inf or NaN."""
+    c = [t.clone() for t in grads]
+    fi = found_inf.clone()
+    torch._amp_foreach_non_finite_check_and_unscale_(c, fi, inv_scale)
+    return c, fi
+
+
+def amp_update_scale(scale, growth_tracker, found_inf, growth_factor, backoff_factor,
+                     growth_interval):
+    """aten::_amp_update_scale_ (codegen/gcu_native_functions.yaml:16): CPU ATen
+    on clones; returns (scale, growth_tracker).  Pinned by the state machine
+    of numpy_ref.amp_update_scale_ref and hand-worked step sequences."""
+    s, t = scale.clone(), growth_tracker.clone()
+    torch._amp_update_scale_(s, t, found_inf, growth_factor, backoff_factor, growth_interval)
+    return s, t
+
+
+def int32_indices_index(self, indices):
+    """The efficient op device_int32_indices_index
+    (torch_gcu/csrc/efficient_ops/ops.cpp:335-342; gcu/efficient/op.py:8-16):
+    CPU ATen's aten::index with the int32 indices widened to int64 (the same
+    values).  Pinned by numpy advanced indexing (which places the broadcast
+    index dims by the same adjacent / non-adjacent rule) and by a brute-force
+    walk over output positions."""
+    return torch.ops.aten.index(self, [None if i is None else i.long() for i in indices])

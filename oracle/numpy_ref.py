@@ -214,3 +214,96 @@ def central_difference(f, x, eps=1e-6):
         xm[i] -= eps
         g[i] = ((f(xp) * c).sum() - (f(xm) * c).sum()) / (2 * eps)
     return g, c
+
+
+def round_to(x: np.ndarray, kind: str) -> np.ndarray:
+    """float32 values rounded once to 'f32', 'bf16' or 'f16' (as float32)."""
+    x = np.asarray(x, dtype=np.float32)
+    if kind == "bf16":
+        return round_bf16(x)
+    if kind == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    return x
+
+
+def foreach_binary32(x, value, op: str, kind: str, round_scalar: bool = True) -> np.ndarray:
+    """x (op) value in float32, rounded once to `kind`: the foreach add / mul
+    of 16- and 32-bit floats.  A Python-number operand is first rounded to
+    the list's dtype (round_scalar); a 0-dim float32 tensor operand is not."""
+    a = np.asarray(x, dtype=np.float32)
+    v = round_to(np.float32(value), kind) if round_scalar else np.float32(value)
+    r = a + v if op == "add" else a * v
+    return round_to(r, kind)
+
+
+def amp_unscale_ref(grads, inv_scale: float, kind: str):
+    """(grads * inv_scale in float32 rounded to `kind`, 1.0 if any element of
+    the input grads is inf or NaN else 0.0); inv_scale == 1 leaves values as
+    they are."""
+    found = 0.0
+    out = []
+    for g in grads:
+        g = np.asarray(g, dtype=np.float32)
+        if not np.all(np.isfinite(g)):
+            found = 1.0
+        out.append(g.copy() if inv_scale == 1.0 else round_to(g * np.float32(inv_scale), kind))
+    return out, found
+
+
+def amp_update_scale_ref(scale: float, tracker: int, found_inf: float, growth: float,
+                         backoff: float, interval: int):
+    """One GradScaler update (torch.amp.GradScaler's documented rule): on inf
+    the scale backs off and the count restarts; otherwise the count grows and,
+    at `interval`, the scale grows (kept only if the float32 result is
+    finite) and the count restarts.  Products in float64, rounded to float32."""
+    if found_inf:
+        return float(np.float32(scale * backoff)), 0
+    tracker += 1
+    if tracker == interval:
+        grown = np.float32(scale * growth)
+        if np.isfinite(grown):
+            scale = float(grown)
+        return scale, 0
+    return scale, tracker
+
+
+def adv_index(arr: np.ndarray, indices) -> np.ndarray:
+    """numpy advanced indexing: arr[i0, :, i2, ...] with None for ':'."""
+    key = tuple(slice(None) if i is None else np.asarray(i) for i in indices)
+    return arr[key]
+
+
+def adv_index_brute(arr: np.ndarray, indices) -> np.ndarray:
+    """The same by explicit loops over output positions: the defined indices
+    broadcast to one shape B; B replaces the indexed dims in place when they
+    are adjacent, else comes first; negative indices count from the end."""
+    import itertools
+
+    idx = list(indices) + [None] * (arr.ndim - len(indices))
+    kdims = [d for d, i in enumerate(idx) if i is not None]
+    bs = np.broadcast_arrays(*[np.asarray(idx[d]) for d in kdims])
+    bshape = bs[0].shape
+    adjacent = kdims == list(range(kdims[0], kdims[-1] + 1))
+    rest = [d for d in range(arr.ndim) if idx[d] is None]
+    if adjacent:
+        before = [d for d in rest if d < kdims[0]]
+        after = [d for d in rest if d > kdims[-1]]
+        layout = [("s", d) for d in before] + [("b", j) for j in range(len(bshape))] + \
+                 [("s", d) for d in after]
+    else:
+        layout = [("b", j) for j in range(len(bshape))] + [("s", d) for d in rest]
+    oshape = tuple(arr.shape[x] if kind == "s" else bshape[x] for kind, x in layout)
+    out = np.empty(oshape, dtype=arr.dtype)
+    for pos in itertools.product(*[range(n) for n in oshape]):
+        src = [0] * arr.ndim
+        bpos = [0] * len(bshape)
+        for (kind, x), c in zip(layout, pos):
+            if kind == "s":
+                src[x] = c
+            else:
+                bpos[x] = c
+        for k, d in enumerate(kdims):
+            v = int(bs[k][tuple(bpos)])
+            src[d] = v + arr.shape[d] if v < 0 else v
+        out[pos] = arr[tuple(src)]
+    return out

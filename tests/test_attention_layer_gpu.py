@@ -144,3 +144,110 @@ def test_decoder_layer_graph_replay_equals_eager():
     torch.gcu.synchronize()
     assert_exact(out.cpu(), dl.forward(w, ids, SMALL, pos).cpu(), "replay with new ids")
     graph.reset()
+
+
+# ---- config 5 at its configured shape -------------------------------------------
+
+C5 = dl.LayerConfig()  # hidden 4096, 32 heads x 128, FFN 11008, vocab 32000
+C5_B, C5_S = 8, 2048
+
+
+@pytest.fixture(scope="module")
+def c5_layer():
+    """The config-5 layer (random-init bf16 weights) over B8 x S2048 token ids,
+    run once on gcu: (weights on CPU, fp32 weights, ids, weights on gcu,
+    the gcu output on the host)."""
+    w = dl.init_weights(C5, seed=20261205)
+    w32 = {k: v.float() for k, v in w.items()}
+    ids = torch.randint(0, C5.vocab, (C5_B, C5_S), generator=g(20261206))
+    wg = {k: v.to("gcu") for k, v in w.items()}
+    out = dl.forward(wg, ids.to("gcu"), C5).cpu()
+    return w, w32, ids, wg, out
+
+
+@pytest.mark.parametrize("b", range(C5_B))
+def test_config5_layer_full_shape_matches_cpu_per_sequence(c5_layer, b):
+    """Sequences of a causal layer are independent, so row block b of the
+    full-batch gcu output must match the CPU ATen layer run on sequence b
+    alone: every projection, the attention and the FFN at their config-5
+    shapes ([16384, 4096] x [4096, 11008] and the rest) are checked through
+    the output they produce."""
+    w, w32, ids, _, out = c5_layer
+    rows = slice(b * C5_S, (b + 1) * C5_S)
+    ref = dl.forward(w, ids[b:b + 1], C5)       # CPU ATen, bf16
+    truth = dl.forward(w32, ids[b:b + 1], C5)   # the same chain in fp32
+    assert out[rows].shape == ref.shape
+    assert torch.isfinite(out[rows].float()).all()
+    assert_composed_close(out[rows], ref, truth, f"config-5 layer, sequence {b}")
+
+
+def test_config5_layer_full_shape_graph_replay_equals_eager(c5_layer):
+    """GCUGraph capture of the full-shape layer: every replay equals eager
+    execution bit for bit, and eager execution is deterministic (equal to
+    the fixture's run)."""
+    _, _, ids, wg, out = c5_layer
+    idg = ids.to("gcu")
+    pos = dl.positions(C5_B, C5_S, "gcu")
+    eager = dl.forward(wg, idg, C5, pos)
+    assert_exact(eager.cpu(), out, "eager run-to-run")
+    graph = torch.gcu.GCUGraph()
+    torch.gcu.synchronize()
+    with torch.gcu.graph(graph):
+        gout = dl.forward(wg, idg, C5, pos)
+    for k in range(2):
+        graph.replay()
+        torch.gcu.synchronize()
+        assert_exact(gout.cpu(), out, f"full-shape replay {k}")
+    graph.reset()
+
+
+# ---- SDPA under autograd and the grouped-query rule --------------------------------
+
+def test_sdpa_backward_on_gcu_matches_cpu():
+    """With q/k/v requiring grad the math path runs (the flash kernel is
+    forward only); gradients match CPU ATen's."""
+    B, H, S, D = 2, 4, 96, 64
+    q0, k0, v0 = rn((B, H, S, D), 21), rn((B, H, S, D), 22), rn((B, H, S, D), 23)
+    dout = rn((B, H, S, D), 24)
+
+    def grads(dev, dtype):
+        q, k, v = (t.detach().to(dtype).to(dev).clone().requires_grad_() for t in (q0, k0, v0))
+        o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        o.backward(dout.to(dtype).to(dev))
+        return [o.detach().cpu()] + [t.grad.cpu() for t in (q, k, v)]
+
+    torch_gcu._C._set_op_debug_config("op_statistics=true")
+    torch_gcu._C._clear_op_statistics()
+    try:
+        gcu = grads("gcu", torch.bfloat16)
+        stats = torch_gcu._C._op_statistics()
+    finally:
+        torch_gcu._C._set_op_debug_config("")
+    assert "_scaled_dot_product_fused_attention_overrideable" not in stats, stats
+    cpu = grads("cpu", torch.bfloat16)
+    f32 = grads("cpu", torch.float32)
+    for name, a, c, t in zip(("out", "dq", "dk", "dv"), gcu, cpu, f32):
+        assert_composed_close(a, c, t, f"sdpa backward {name}")
+    # without grad the flash kernel still runs
+    with torch.no_grad():
+        out = F.scaled_dot_product_attention(q0.to("gcu"), k0.to("gcu"), v0.to("gcu"),
+                                             is_causal=True)
+    assert_close(out.cpu(), ref_attention(q0, k0, v0, True)[0], "bf16", "sdpa no_grad")
+
+
+def test_sdpa_grouped_query_heads_follow_enable_gqa():
+    q, k, v = rn((1, 8, 64, 128), 31), rn((1, 2, 64, 128), 32), rn((1, 2, 64, 128), 33)
+    with pytest.raises(RuntimeError) as cpu_err:
+        F.scaled_dot_product_attention(q, k, v)
+    with pytest.raises(RuntimeError):
+        F.scaled_dot_product_attention(q.to("gcu"), k.to("gcu"), v.to("gcu"))
+    assert cpu_err.value is not None
+    out = F.scaled_dot_product_attention(q.to("gcu"), k.to("gcu"), v.to("gcu"), enable_gqa=True)
+    ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), enable_gqa=True)
+    assert_close(out.cpu(), ref.to(torch.bfloat16), "bf16", "sdpa enable_gqa")
+    # a k/v batch of 1 broadcast by the math path, not handed to the kernel
+    kb, vb = rn((1, 8, 64, 128), 34), rn((1, 8, 64, 128), 35)
+    q2 = rn((2, 8, 64, 128), 36)
+    out2 = F.scaled_dot_product_attention(q2.to("gcu"), kb.to("gcu"), vb.to("gcu"))
+    ref2 = F.scaled_dot_product_attention(q2.float(), kb.float(), vb.float())
+    assert_close(out2.cpu(), ref2.to(torch.bfloat16), "bf16", "sdpa broadcast batch")

@@ -212,3 +212,86 @@ def test_graph_capture_rejects_default_stream_and_cpu_fallback():
         with torch.gcu.graph(gr2):
             torch.cos(x)
     torch.gcu.synchronize()
+
+
+# ---- memory overlap -----------------------------------------------------------------
+
+OVERLAP_CASES = {
+    "partial in-place add": lambda x: x[1:].add_(x[:-1]),
+    "in-place add into an expanded tensor": lambda x: x[:1].expand(4).add_(1),
+    "add.out into an overlapping view": lambda x: torch.add(x[:-1], 1, out=x[1:]),
+    "mul.out into an expanded out": lambda x: torch.mul(x[:4], 2, out=x[:1].expand(4)),
+    "copy_ between overlapping views": lambda x: x[1:].copy_(x[:-1]),
+    "copy_ into an expanded tensor": lambda x: x[:1].expand(4).copy_(x[1:5]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(OVERLAP_CASES))
+def test_overlapping_writes_raise_like_cpu(case):
+    """Elementwise writes whose output shares memory with an input (other
+    than element for element) or with itself raise as CPU ATen's do, rather
+    than racing in the kernel."""
+    fn = OVERLAP_CASES[case]
+    x = torch.arange(8, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="unsupported operation") as cpu_err:
+        fn(x.clone())
+    xg = x.to("gcu")
+    with pytest.raises(RuntimeError, match="unsupported operation") as gcu_err:
+        fn(xg)
+    assert str(cpu_err.value).split(".")[0] in str(gcu_err.value)
+    torch.gcu.synchronize()
+    assert_exact(xg.cpu(), x, f"{case}: gcu tensor unchanged")
+    # element-for-element in place is allowed on both
+    y = x.clone().to("gcu")
+    y.add_(y)
+    y.copy_(y)
+    assert_exact(y.cpu(), x * 2, "full-overlap in place")
+
+
+# ---- graphs sharing a memory pool ----------------------------------------------------
+
+def test_two_graphs_share_one_pool():
+    """Two captures into one graph_pool_handle() pool (the reference's
+    graph_pool_handle and capture_begin(pool), gcu_graph.cpp:24-31,170-185):
+    the second capture's allocations reuse blocks the first capture freed
+    (no new segment), live outputs of the first are not handed out again,
+    and replaying both in capture order reproduces eager execution."""
+    n = 1 << 20  # 4 MiB fp32 tensors: large-pool blocks
+    x = torch.randn(n, generator=g(40)).to("gcu")
+    eager1 = torch.log_softmax((x * 2).view(256, -1), -1)
+    eager2 = (eager1 + 1) * 3
+    pool = torch.gcu.graph_pool_handle()
+    g1, g2 = torch.gcu.GCUGraph(), torch.gcu.GCUGraph()
+    torch.gcu.synchronize()
+    with torch.gcu.graph(g1, pool=pool):
+        y1 = torch.log_softmax((x * 2).view(256, -1), -1)  # x * 2 is freed inside
+    # graph() empties the cache on entry; do it here too so that the
+    # comparison sees only the pools' own segments
+    torch.gcu.synchronize()
+    torch.gcu.empty_cache()
+    reserved_after_g1 = torch_gcu._C._memory_stats(0)["reserved_bytes.all.current"]
+    with torch.gcu.graph(g2, pool=pool):
+        y2 = (y1 + 1) * 3
+    reserved_after_g2 = torch_gcu._C._memory_stats(0)["reserved_bytes.all.current"]
+    assert reserved_after_g2 == reserved_after_g1, (reserved_after_g1, reserved_after_g2)
+    assert y2.data_ptr() != y1.data_ptr()
+    assert g1.pool() == g2.pool()
+    for k in range(3):
+        x.copy_(torch.randn(n, generator=g(41 + k)).to("gcu"))
+        g1.replay()
+        g2.replay()
+        torch.gcu.synchronize()
+        e1 = torch.log_softmax((x * 2).view(256, -1), -1)
+        assert_exact(y1.cpu(), e1.cpu(), f"shared pool replay {k}: first graph")
+        assert_exact(y2.cpu(), ((e1 + 1) * 3).cpu(), f"shared pool replay {k}: second graph")
+    # a third capture into its own pool takes new memory
+    g3 = torch.gcu.GCUGraph()
+    with torch.gcu.graph(g3):
+        y3 = (y1 + 1) * 3
+    assert torch_gcu._C._memory_stats(0)["reserved_bytes.all.current"] > reserved_after_g2
+    g3.replay()
+    torch.gcu.synchronize()
+    assert_exact(y3.cpu(), y2.cpu(), "separate pool")
+    del eager1, eager2
+    for gr in (g1, g2, g3):
+        gr.reset()

@@ -418,3 +418,136 @@ def test_planted_mistakes_are_caught():
     _, mu, rs = npr.layer_norm64(xs, None, None, 1e-5)
     dropped = rs * (c - c.sum(-1, keepdims=True) / 5)
     assert np.abs(num - dropped).max() > 1e-2
+
+
+# ---- foreach and mixed-precision grad scaling ------------------------------------------
+
+KIND = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_foreach_add_mul_vs_float32_closed_form(dtype):
+    ts = [torch.randn(s, generator=g(60 + i)).to(dtype) for i, s in enumerate([(7,), (33, 5), ()])]
+    for value in (0.3, -1.75, 1e-3):
+        got = aten.foreach_add_scalar(ts, value)
+        for a, t in zip(got, ts):
+            want = npr.foreach_binary32(t.float().numpy(), value, "add", KIND[dtype])
+            assert_exact(a.float(), torch.from_numpy(np.asarray(want)).reshape(t.shape),
+                         f"foreach_add {dtype} {value}")
+        got = aten.foreach_mul(ts, value)
+        for a, t in zip(got, ts):
+            want = npr.foreach_binary32(t.float().numpy(), value, "mul", KIND[dtype])
+            assert_exact(a.float(), torch.from_numpy(np.asarray(want)).reshape(t.shape),
+                         f"foreach_mul {dtype} {value}")
+    # a 0-dim float32 tensor factor keeps its float value (not rounded to the
+    # list's dtype as a Python number is)
+    for a, t in zip(aten.foreach_mul(ts, torch.tensor(0.37)), ts):
+        want = npr.foreach_binary32(t.float().numpy(), 0.37, "mul", KIND[dtype], round_scalar=False)
+        assert_exact(a.float(), torch.from_numpy(np.asarray(want)).reshape(t.shape),
+                     f"foreach_mul tensor factor {dtype}")
+    # identities
+    for a, t in zip(aten.foreach_add_scalar(ts, 0.0), ts):
+        assert_exact(a, t, "x + 0")
+    for a, t in zip(aten.foreach_mul(ts, -1.0), ts):
+        assert_exact(a, -t, "x * -1")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_amp_unscale_vs_float32_closed_form(dtype):
+    grads = [(torch.randn(s, generator=g(70 + i)) * 512).to(dtype)
+             for i, s in enumerate([(9,), (4, 6), ()])]
+    for inv, poison in ((1.0 / 512, None), (1.0 / 3, float("inf")), (1.0, float("nan")),
+                        (0.25, float("-inf"))):
+        gs = [t.clone() for t in grads]
+        if poison is not None:
+            gs[1].view(-1)[5] = poison
+        got, fi = aten.amp_unscale(gs, torch.zeros(1), torch.tensor([inv]))
+        want, found = npr.amp_unscale_ref([t.float().numpy() for t in gs], inv, KIND[dtype])
+        assert float(fi) == found == (0.0 if poison is None else 1.0)
+        for a, w in zip(got, want):
+            a32, w32 = a.float(), torch.from_numpy(np.asarray(w, dtype=np.float32)).reshape(a.shape)
+            same = (a32 == w32) | (torch.isnan(a32) & torch.isnan(w32))
+            assert bool(same.all()), f"unscale {dtype} inv={inv}"
+        if inv == 1.0:
+            for a, t in zip(got, gs):
+                assert_exact(a, t, "inv_scale 1 leaves values")
+
+
+def test_amp_update_scale_vs_state_machine_and_worked_steps():
+    # hand-worked: growth 2, backoff 0.5, interval 3 from 65536
+    steps = [0, 0, 0, 1, 0, 0, 0, 0, 1, 1]
+    worked = [(65536.0, 1), (65536.0, 2), (131072.0, 0), (65536.0, 0), (65536.0, 1),
+              (65536.0, 2), (131072.0, 0), (131072.0, 1), (65536.0, 0), (32768.0, 0)]
+    for start, table in ((65536.0, worked), (3.0e38, None), (1.0, None)):
+        s, t = torch.tensor([start]), torch.tensor([0], dtype=torch.int32)
+        rs, rt = float(np.float32(start)), 0
+        for k, bad in enumerate(steps):
+            s, t = aten.amp_update_scale(s, t, torch.tensor([float(bad)]), 2.0, 0.5, 3)
+            rs, rt = npr.amp_update_scale_ref(rs, rt, float(bad), 2.0, 0.5, 3)
+            assert (float(s), int(t)) == (rs, rt), (start, k)
+            if table is not None:
+                assert (float(s), int(t)) == table[k], (start, k)
+    # a growth that overflows float32 is not taken, but the count restarts
+    s, t = aten.amp_update_scale(torch.tensor([3.0e38]), torch.tensor([2], dtype=torch.int32),
+                                 torch.tensor([0.0]), 2.0, 0.5, 3)
+    assert float(s) == float(np.float32(3.0e38)) and int(t) == 0
+
+
+def test_planted_mistakes_in_grad_scaling_are_caught():
+    # a back-off that forgets to reset the count, and a growth taken even
+    # when it overflows, each leave the worked sequence
+    def forgetful(scale, tracker, found, growth, backoff, interval):
+        if found:
+            return float(np.float32(scale * backoff)), tracker
+        return npr.amp_update_scale_ref(scale, tracker, found, growth, backoff, interval)
+
+    s, t, s2, t2 = 65536.0, 0, 65536.0, 0
+    diverged = False
+    for bad in [0, 0, 1, 0, 0, 0]:
+        s, t = npr.amp_update_scale_ref(s, t, bad, 2.0, 0.5, 3)
+        s2, t2 = forgetful(s2, t2, bad, 2.0, 0.5, 3)
+        diverged |= (s, t) != (s2, t2)
+    assert diverged
+    grown = float(np.float32(3.0e38) * np.float32(2.0))
+    assert not math.isfinite(grown)
+    assert npr.amp_update_scale_ref(3.0e38, 2, 0.0, 2.0, 0.5, 3)[0] != grown
+    # unscaling with the scale instead of its inverse misses the closed form
+    g0 = [np.array([512.0, -1024.0], dtype=np.float32)]
+    assert not np.array_equal(npr.amp_unscale_ref(g0, 1 / 512, "f32")[0][0], g0[0] * 512)
+
+
+# ---- int32 advanced index ------------------------------------------------------------
+
+INDEX_CASES = [
+    ("rows", (7, 5), lambda r: [r.integers(-7, 7, (4,))]),
+    ("2-D index", (6, 4, 3), lambda r: [r.integers(0, 6, (2, 3))]),
+    ("middle dim", (3, 8, 2), lambda r: [None, r.integers(-8, 8, (5,))]),
+    ("two broadcast", (5, 6, 2), lambda r: [r.integers(0, 5, (3, 1)), r.integers(0, 6, (4,))]),
+    ("non-adjacent", (4, 3, 5, 2), lambda r: [r.integers(0, 4, (2, 2)), None, r.integers(0, 5, (2,))]),
+    ("0-dim index", (5, 3), lambda r: [np.array(3)]),
+    ("last dim", (2, 3, 9), lambda r: [None, None, r.integers(0, 9, (4,))]),
+]
+
+
+@pytest.mark.parametrize("name", [c[0] for c in INDEX_CASES])
+def test_int32_indices_index_vs_numpy_and_brute_force(name):
+    _, shape, mk = next(c for c in INDEX_CASES if c[0] == name)
+    rng = np.random.default_rng(abs(hash(name)) % 1000)
+    arr = rng.integers(-2**62, 2**62, shape)
+    idx = mk(rng)
+    t_idx = [None if i is None else torch.from_numpy(np.asarray(i, dtype=np.int32)) for i in idx]
+    got = aten.int32_indices_index(torch.from_numpy(arr), t_idx)
+    assert np.array_equal(got.numpy(), npr.adv_index(arr, idx)), name
+    assert np.array_equal(got.numpy(), npr.adv_index_brute(arr, idx)), name
+
+
+def test_int32_indices_index_planted_mistake_non_adjacent_order():
+    # placing B in the position of the first indexed dim even when the
+    # indexed dims are not adjacent gives another shape than the brute force
+    arr = np.arange(4 * 3 * 5).reshape(4, 3, 5)
+    idx = [np.array([0, 1]), None, np.array([2, 4])]
+    want = npr.adv_index_brute(arr, idx)
+    assert want.shape == (2, 3)
+    wrong = np.stack([arr[idx[0][j], :, idx[2][j]] for j in range(2)], 0)  # same here...
+    wrong_layout = np.moveaxis(wrong, 0, 1)  # ...but B placed second
+    assert wrong_layout.shape != want.shape or not np.array_equal(wrong_layout, want)

@@ -7,7 +7,10 @@
 // in a GCUGraph and shows up in profiles.  The fused ops are new (RMSNorm,
 // RoPE, SiLU-mul); int32_indices_index keeps the reference's op.
 #include <ATen/ATen.h>
+#include <ATen/ExpandUtils.h>
 #include <torch/library.h>
+
+#include <sstream>
 
 #include "dispatch_util.h"
 #include "efficient_ops.h"
@@ -121,28 +124,117 @@ at::Tensor int8_linear(const at::Tensor& x, const at::Tensor& weight, const at::
 }
 
 // Advanced index with int32 indices (torch_gcu/csrc/efficient_ops/ops.cpp:221-342):
-// one index tensor selecting along dim 0 is an index_select; other patterns
-// run through aten::index after the indices are widened.
+// the reference's make_info rules -- index tensors long, int, byte or bool
+// (ops.cpp:135-159), masks expanded to their nonzero positions (:101-133),
+// the index tensors broadcast together (:230-240), and every one of them int32
+// (:266-272), so a mask or an int64 index raises as in the reference -- then
+// one mi_index gather that reads the int32 indices as they are.  Index
+// tensors on the CPU are range-checked on the host and copied to the device;
+// device indices are not (that would need a synchronising read), and an
+// out-of-range one writes its out row as zeros.
 at::Tensor int32_indices_index(const at::Tensor& self,
                                const c10::List<std::optional<at::Tensor>>& indices) {
   TORCH_CHECK(is_gcu(self), "int32_indices_index: self must be a gcu tensor");
+  TORCH_CHECK_INDEX(indices.size() <= (size_t)self.dim(), "too many indices for tensor of dimension ",
+                    self.dim(), " (got ", indices.size(), ")");
+  const c10::DeviceGuard g(self.device());
+  std::vector<at::Tensor> idx;
   for (const auto& oi : indices) {
     const std::optional<at::Tensor> i = oi;
-    if (i.has_value() && i->defined())
-      TORCH_CHECK(i->scalar_type() == at::kInt,
-                  "int32_indices_index: indices must be int32 tensors, got ", i->scalar_type());
+    if (!i.has_value() || !i->defined()) {
+      idx.emplace_back();
+      continue;
+    }
+    const auto st = i->scalar_type();
+    TORCH_CHECK_INDEX(st == at::kLong || st == at::kInt || st == at::kByte || st == at::kBool,
+                      "tensors used as indices must be long, int, byte or bool tensors");
+    TORCH_CHECK(i->is_cpu() || i->device() == self.device(),
+                "indices should be either on the same device as the indexed tensor (",
+                self.device(), ")");
+    if (st == at::kByte || st == at::kBool) {
+      // a mask: its nonzero positions, one long index per mask dim
+      for (int64_t j = 0; j < i->dim(); ++j) {
+        const int64_t src_dim = (int64_t)idx.size() + j;
+        TORCH_CHECK_INDEX(src_dim < self.dim() && i->size(j) == self.size(src_dim),
+                          "The shape of the mask ", i->sizes(), " at index ", j,
+                          " does not match the shape of the indexed tensor ", self.sizes(),
+                          " at index ", src_dim);
+      }
+      const at::Tensor nz = i->nonzero();
+      for (int64_t j = 0; j < i->dim(); ++j) idx.push_back(nz.select(1, j));
+    } else {
+      idx.push_back(*i);
+    }
   }
-  if (indices.size() == 1) {
-    const std::optional<at::Tensor> i0 = indices.get(0);
-    if (i0.has_value() && i0->defined() && i0->dim() == 1)
-      return at::index_select(self, 0, *i0);
+  TORCH_CHECK_INDEX(idx.size() <= (size_t)self.dim(), "too many indices for tensor of dimension ",
+                    self.dim(), " (got ", idx.size(), ")");
+  std::vector<at::Tensor> defined;
+  for (const at::Tensor& t : idx)
+    if (t.defined()) defined.push_back(t);
+  TORCH_CHECK_INDEX(!defined.empty(), "int32_indices_index: at least one index tensor is needed");
+  std::vector<at::Tensor> bcast;
+  try {
+    bcast = at::expand_outplace(defined);
+  } catch (const std::exception&) {
+    std::ostringstream os;
+    for (size_t k = 0; k < defined.size(); ++k) os << (k ? ", " : "") << defined[k].sizes();
+    TORCH_CHECK_INDEX(false, "shape mismatch: indexing tensors could not be broadcast together "
+                      "with shapes ", os.str());
   }
-  c10::List<std::optional<at::Tensor>> wide;
-  for (const auto& oi : indices) {
-    const std::optional<at::Tensor> i = oi;
-    wide.push_back(i.has_value() && i->defined() ? std::optional<at::Tensor>(i->to(at::kLong)) : i);
+  for (const at::Tensor& t : bcast)
+    TORCH_CHECK_INDEX(t.scalar_type() == at::kInt, "indice error, should be int in gcu_index ",
+                      "but got ", t.scalar_type());
+  // the device view of each index; CPU indices range-checked here
+  std::vector<at::Tensor> dev(idx.size());
+  std::vector<int64_t> kdim;
+  for (size_t d = 0, k = 0; d < idx.size(); ++d) {
+    if (!idx[d].defined()) continue;
+    at::Tensor t = bcast[k++];
+    if (t.is_cpu() && t.numel() > 0) {
+      const int64_t n = self.size((int64_t)d);
+      const int64_t lo = t.min().item<int64_t>(), hi = t.max().item<int64_t>();
+      const int64_t bad = lo < -n ? lo : hi;
+      TORCH_CHECK_INDEX(lo >= -n && hi < n, "index ", bad, " is out of bounds for dimension ", d,
+                        " with size ", n);
+    }
+    dev[d] = t.is_cpu() ? t.contiguous().to(self.device()) : t;
+    kdim.push_back((int64_t)d);
   }
-  return at::index(self, wide);
+  // out shape: B in place of adjacent indexed dims, else in front
+  bool adjacent = true;
+  for (size_t k = 1; k < kdim.size(); ++k) adjacent = adjacent && kdim[k] == kdim[k - 1] + 1;
+  const auto bshape = bcast[0].sizes();
+  std::vector<int64_t> shape;
+  if (!adjacent) shape.insert(shape.end(), bshape.begin(), bshape.end());
+  for (int64_t d = 0; d < self.dim(); ++d) {
+    const bool indexed = d < (int64_t)idx.size() && idx[d].defined();
+    if (!indexed) {
+      shape.push_back(self.size(d));
+    } else if (adjacent && d == kdim[0]) {
+      shape.insert(shape.end(), bshape.begin(), bshape.end());
+    }
+  }
+  TORCH_CHECK((int64_t)shape.size() <= MI_MAX_DIMS, "int32_indices_index: result has ",
+              shape.size(), " dims, at most ", MI_MAX_DIMS, " are supported");
+  at::Tensor out = at::empty(shape, self.options());
+  if (out.numel() == 0) {
+    for (int64_t d : kdim)
+      TORCH_CHECK_INDEX(self.size(d) > 0 || bcast[0].numel() == 0,
+                        "index is out of bounds for dimension with size 0");
+    return out;
+  }
+  const mi_tensor_t od = desc(out), sd = desc(self);
+  std::vector<mi_tensor_t> descs(idx.size());
+  std::vector<const mi_tensor_t*> ptrs(idx.size(), nullptr);
+  for (size_t d = 0; d < idx.size(); ++d) {
+    if (!dev[d].defined()) continue;
+    descs[d] = desc(dev[d]);
+    ptrs[d] = &descs[d];
+  }
+  check_mi(mi_index(&od, &sd, ptrs.data(), (int32_t)ptrs.size(), mi_stream(out)),
+           "int32_indices_index");
+  after_op();
+  return out;
 }
 
 }  // namespace efficient

@@ -54,15 +54,25 @@ void GCUGraph::capture_end() {
   hipGraph_t g = nullptr;
   const hipError_t e = hipStreamEndCapture(capture_stream_, &g);
   allocator::end_allocate_to_pool(device_, mempool_);
-  TORCH_CHECK(e == hipSuccess && g != nullptr,
-              "GCU graph capture failed (an operation in the captured region is not "
-              "capturable, or the capture was invalidated): ", hipGetErrorString(e));
+  if (e != hipSuccess || g == nullptr) {
+    // nothing will replay: the pool's blocks go back to the caching allocator
+    if (g != nullptr) (void)hipGraphDestroy(g);
+    abandon_capture();
+    TORCH_CHECK(false, "GCU graph capture failed (an operation in the captured region is not "
+                "capturable, or the capture was invalidated): ", hipGetErrorString(e));
+  }
   graph_ = g;
   has_graph_ = true;
   size_t n = 0;
-  GCU_HIP_CHECK(hipGraphGetNodes(graph_, nullptr, &n));
+  hipError_t ie = hipGraphGetNodes(graph_, nullptr, &n);
+  if (ie == hipSuccess) ie = hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0);
+  if (ie != hipSuccess) {
+    (void)hipGraphDestroy(graph_);
+    has_graph_ = false;
+    abandon_capture();
+    TORCH_CHECK(false, "GCU graph instantiation failed: ", hipGetErrorString(ie));
+  }
   num_nodes_ = (int64_t)n;
-  GCU_HIP_CHECK(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0));
   has_exec_ = true;
   if (!debug_) {
     GCU_HIP_CHECK(hipGraphDestroy(graph_));
@@ -74,6 +84,14 @@ void GCUGraph::replay() {
   TORCH_CHECK(has_exec_, "Called GCUGraph::replay without a preceding successful capture.");
   const c10::DeviceGuard guard(c10::Device(kGCU, (c10::DeviceIndex)device_));
   GCU_HIP_CHECK(hipGraphLaunch(exec_, current_hip_stream(device_)));
+}
+
+// A capture that produced no executable graph: releases the private pool
+// (its blocks return to the allocator once their last uses on the device
+// complete) and returns the object to its initial state.
+void GCUGraph::abandon_capture() {
+  allocator::release_pool(device_, mempool_);
+  capture_stream_ = nullptr;
 }
 
 void GCUGraph::reset() {

@@ -31,6 +31,8 @@ class GCUGraph {
   int64_t num_nodes() const { return num_nodes_; }
 
  private:
+  void abandon_capture();
+
   hipGraph_t graph_ = nullptr;
   hipGraphExec_t exec_ = nullptr;
   bool has_graph_ = false;

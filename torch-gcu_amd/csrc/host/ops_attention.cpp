@@ -9,6 +9,7 @@
 // _scaled_dot_product_flash_attention (torch_gcu/csrc/aten/GCUNativeFunctions.cpp:49-102,
 // gcu_attention.cpp:21-79) both run mi_flash_attention_fwd.
 #include <ATen/SDPBackend.h>
+#include <ATen/core/grad_mode.h>
 #include <ATen/native/DispatchStub.h>
 #include <ATen/native/transformers/attention.h>
 
@@ -22,8 +23,12 @@ namespace aotops {
 
 namespace {
 
+// The shapes the flash kernel takes: 4-D bf16/fp16 q/k/v of one batch size,
+// k and v of one sequence length, head_dim 64 or 128, no mask, no dropout,
+// and either as many k/v heads as query heads or, with enable_gqa, a number
+// that divides them (ATen's math path raises for H != Hk without it).
 bool flash_applies(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                   bool has_mask, double dropout_p) {
+                   bool has_mask, double dropout_p, bool enable_gqa) {
   if (has_mask || dropout_p > 0.0) return false;
   if (q.dim() != 4 || k.dim() != 4 || v.dim() != 4) return false;
   const auto dt = q.scalar_type();
@@ -31,8 +36,18 @@ bool flash_applies(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
     return false;
   const int64_t d = q.size(3);
   if ((d != 64 && d != 128) || k.size(3) != d || v.size(3) != d) return false;
-  if (q.size(1) % k.size(1) != 0 || k.size(1) != v.size(1)) return false;
+  if (q.size(0) != k.size(0) || k.size(0) != v.size(0) || k.size(2) != v.size(2)) return false;
+  if (k.size(1) != v.size(1) || k.size(1) == 0 || q.size(1) % k.size(1) != 0) return false;
+  if (!enable_gqa && q.size(1) != k.size(1)) return false;
   return is_gcu(q) && is_gcu(k) && is_gcu(v);
+}
+
+// The kernel is forward only: when autograd will need gradients of q, k or
+// v, the math path runs instead (its bmm / softmax ops have native backward
+// kernels), as the reference selects by whether the logsumexp must be kept
+// for a backward pass (torch_gcu/csrc/aten/RegisterSPDA.cpp:422-428).
+bool needs_grad(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
+  return at::GradMode::is_enabled() && (q.requires_grad() || k.requires_grad() || v.requires_grad());
 }
 
 // Makes head_dim contiguous and every row 16-byte aligned.
@@ -64,9 +79,8 @@ int64_t gcu_fused_sdp_choice(const at::Tensor& q, const at::Tensor& k, const at:
                              bool is_causal, std::optional<double> scale, bool enable_gqa) {
   (void)is_causal;
   (void)scale;
-  (void)enable_gqa;
   const bool has_mask = attn_mask.has_value() && attn_mask->defined();
-  if (flash_applies(q, k, v, has_mask, dropout_p))
+  if (!needs_grad(q, k, v) && flash_applies(q, k, v, has_mask, dropout_p, enable_gqa))
     return static_cast<int64_t>(at::SDPBackend::overrideable);
   return static_cast<int64_t>(at::SDPBackend::math);
 }
@@ -82,8 +96,11 @@ _scaled_dot_product_fused_attention_overrideable(const at::Tensor& query, const 
                                                  bool return_debug_mask,
                                                  std::optional<double> scale) {
   const bool has_mask = attn_bias.has_value() && attn_bias->defined();
-  TORCH_CHECK(flash_applies(query, key, value, has_mask, dropout_p),
-              "gcu fused attention: needs bf16/fp16 4-D q/k/v with head_dim 64 or 128, no "
+  // called directly (not through the backend choice), grouped k/v heads are
+  // taken as they come, as the fused ops of ATen's other backends take them
+  TORCH_CHECK(flash_applies(query, key, value, has_mask, dropout_p, /*enable_gqa=*/true),
+              "gcu fused attention: needs bf16/fp16 4-D q/k/v of one batch size with head_dim "
+              "64 or 128, k and v of one length, query heads a multiple of k/v heads, no "
               "attention mask and no dropout");
   TORCH_CHECK(!return_debug_mask, "gcu fused attention: return_debug_mask is not supported");
   auto [out, lse] = run_flash(query, key, value, is_causal, scale);

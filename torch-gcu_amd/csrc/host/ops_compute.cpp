@@ -6,6 +6,7 @@
 // topsaten_bridge_define.h:323-336).  A CPU 0-dim operand is handed over by
 // value (codegen/gen_backend_stubs.py:1061-1078), never copied to the device.
 #include <ATen/ExpandUtils.h>
+#include <ATen/MemoryOverlap.h>
 #include <ATen/WrapDimUtils.h>
 #include <ATen/native/ReduceOpsUtils.h>
 #include <ATen/native/Resize.h>
@@ -79,6 +80,16 @@ void run_binary(Bin op, const at::Tensor& out, const at::Tensor& self, const at:
   }
 }
 
+// The checks TensorIterator makes before an elementwise kernel writes
+// (CPU ATen raises the same errors): no element of the written tensor may
+// share memory with another of its elements, and the written tensor and an
+// input may share memory only element for element (in place).
+void check_binary_overlap(const at::Tensor& out, const at::Tensor& self, const at::Tensor& other) {
+  at::assert_no_internal_overlap(out);
+  at::assert_no_partial_overlap(out, self);
+  at::assert_no_partial_overlap(out, other);
+}
+
 at::Device gcu_device(const at::Tensor& a, const at::Tensor& b) {
   if (is_gcu(a)) return a.device();
   TORCH_CHECK(is_gcu(b), "gcu op called without a gcu tensor");
@@ -103,6 +114,7 @@ at::Tensor& binary_out(Bin op, const at::Tensor& self, const at::Tensor& other,
               " can't be cast to the desired output type ", out.scalar_type());
   const auto shape = at::infer_size_dimvector(self.sizes(), other.sizes());
   at::native::resize_output(out, shape);
+  check_binary_overlap(out, self, other);
   run_binary(op, out, self, other, alpha);
   return out;
 }
@@ -116,6 +128,7 @@ at::Tensor& binary_inplace(Bin op, at::Tensor& self, const at::Tensor& other,
   const auto shape = at::infer_size_dimvector(self.sizes(), other.sizes());
   TORCH_CHECK(at::IntArrayRef(shape) == self.sizes(), "output with shape ", self.sizes(),
               " doesn't match the broadcast shape ", at::IntArrayRef(shape));
+  check_binary_overlap(self, self, other);
   run_binary(op, self, self, other, alpha);
   return self;
 }

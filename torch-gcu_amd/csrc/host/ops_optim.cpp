@@ -176,6 +176,15 @@ void foreach_launch(at::TensorList self, const char* what, F&& call) {
 
 bool real_scalar(const at::Scalar& s) { return !s.isComplex() && !s.isBoolean(); }
 
+// The value a Python-number operand of _foreach_add_ / _foreach_mul_ takes:
+// CPU ATen first rounds it to a 16-bit list's own dtype, then computes in
+// float (a 0-dim tensor operand keeps its float value).
+double list_scalar(const at::Scalar& s, at::ScalarType dt) {
+  if (dt == at::kBFloat16) return static_cast<float>(s.to<c10::BFloat16>());
+  if (dt == at::kHalf) return static_cast<float>(s.to<c10::Half>());
+  return s.toDouble();
+}
+
 }  // namespace
 
 void _foreach_add__Scalar(at::TensorList self, const at::Scalar& scalar) {
@@ -185,7 +194,7 @@ void _foreach_add__Scalar(at::TensorList self, const at::Scalar& scalar) {
     return;
   }
   foreach_launch(self, "_foreach_add_", [&](const mi_tensor_t* const* p, int32_t n, mi_stream_t s) {
-    return mi_foreach_add_scalar(p, n, scalar.toDouble(), s);
+    return mi_foreach_add_scalar(p, n, list_scalar(scalar, self[0].scalar_type()), s);
   });
 }
 
@@ -197,7 +206,7 @@ void _foreach_mul__Scalar(at::TensorList self, const at::Scalar& scalar) {
     return;
   }
   foreach_launch(self, "_foreach_mul_", [&](const mi_tensor_t* const* p, int32_t n, mi_stream_t s) {
-    return mi_foreach_mul_scalar(p, n, scalar.toDouble(), nullptr, s);
+    return mi_foreach_mul_scalar(p, n, list_scalar(scalar, self[0].scalar_type()), nullptr, s);
   });
 }
 

@@ -280,6 +280,11 @@ at::Tensor _copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_bl
       return dst;
     }
     c10::DeviceGuard g(dst.device());
+    // at::copy_ hands a gcu copy to _copy_from before its TensorIterator
+    // would check memory overlap, so the checks are made here (CPU ATen
+    // raises the same errors)
+    at::assert_no_internal_overlap(dst);
+    at::assert_no_partial_overlap(dst, self);
     copy_d2d(dst, self);
     return dst;
   }

@@ -276,7 +276,7 @@ __global__ __launch_bounds__(256) void foreach_scalar_kernel(ForeachArgs a, cons
     const int64_t i = base + k;
     if (i >= t.n) break;
     const Acc x = Num<Tag>::load(p[i]);
-    p[i] = Num<Tag>::store(OP == FE_ADD ? x + v : x * v);
+    p[i] = Num<Tag>::store(as_rounded(OP == FE_ADD ? x + v : x * v));
   }
 }
 
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void amp_unscale_kernel(ForeachArgs a, float* 
     if (i >= t.n) break;
     const Acc v = Num<Tag>::load(p[i]);
     if (!isfinite(v)) bad = true;
-    if (sc != 1.0f) p[i] = Num<Tag>::store(v * (Acc)sc);
+    if (sc != 1.0f) p[i] = Num<Tag>::store(as_rounded(v * (Acc)sc));
   }
   if (bad) *found_inf = 1.0f;
 }

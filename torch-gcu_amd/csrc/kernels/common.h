@@ -113,6 +113,17 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// The value as it stands, rounded to its own type: an empty asm the compiler
+// cannot look through, so a following conversion to fp16 is not fused with
+// the arithmetic that produced it into one v_fma_mixlo_f16 that rounds once.
+// CPU ATen rounds the fp32 result first, then converts; ops that promise its
+// bits use this before storing 16-bit results.
+template <typename T>
+__device__ __forceinline__ T as_rounded(T x) {
+  if constexpr (sizeof(T) == 4) asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Storage type tags used by templated kernels.
 struct BF16 {
   typedef uint16_t storage;

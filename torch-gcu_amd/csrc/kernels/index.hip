@@ -200,10 +200,241 @@ mi_status_t index_select_t(const mi_tensor_t* out, const mi_tensor_t* self, int 
   return launch_general<IdxT>(out, self, dim, idx, istride, stream);
 }
 
+// ---- advanced index (aten::index with integer index tensors) ---------------
+//
+// out = self[indices] with ATen's rules: the defined index tensors (already
+// broadcast to one shape B by the caller, stride 0 where broadcast) select
+// along their dims; out is self.shape[:first] + B + self.shape[last+1:]
+// when the indexed dims are adjacent, else B + the other dims in order.
+// out is dense; every out dim maps either to a self dim (a stride into
+// self) or to a dim of B (a stride into each index tensor).  Trailing out
+// dims that run contiguously through self are folded into a row copied in
+// 16/8/4/2/1-byte words.  Negative indices count from the end; an index
+// still out of range selects nothing and its row is written as zeros (the
+// kernel never reads outside self).
+constexpr int kMaxIdx = MI_MAX_DIMS;
+
+struct AdvIndex {
+  int nd;     // out dims decoded per row (the folded inner dims excluded)
+  int n_idx;  // defined index tensors
+  uint32_t idx64;  // bit k: index k is int64 (else int32)
+  int64_t sizes[MI_MAX_DIMS];       // out sizes of the decoded dims
+  int64_t src_bstride[MI_MAX_DIMS]; // self byte stride per decoded dim (0 for dims of B)
+  int64_t idx_stride[kMaxIdx][MI_MAX_DIMS];  // element stride of index k per decoded dim
+  const void* idx[kMaxIdx];
+  int64_t limit[kMaxIdx];           // size of the self dim index k selects
+  int64_t sel_bstride[kMaxIdx];     // byte stride of that self dim
+};
+
+// Byte offset into self of a row (out coordinates decoded from `row`), or -1
+// when an index is out of range.
+__device__ __forceinline__ int64_t adv_row_offset(const AdvIndex& a, int64_t row) {
+  int64_t off = 0;
+  int64_t ioff[kMaxIdx];
+#pragma unroll
+  for (int k = 0; k < kMaxIdx; ++k) ioff[k] = 0;
+  for (int d = a.nd - 1; d >= 0; --d) {
+    const int64_t sz = a.sizes[d];
+    const int64_t q = row / sz;
+    const int64_t c = row - q * sz;
+    row = q;
+    off += c * a.src_bstride[d];
+#pragma unroll
+    for (int k = 0; k < kMaxIdx; ++k)
+      if (k < a.n_idx) ioff[k] += c * a.idx_stride[k][d];
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxIdx; ++k) {
+    if (k < a.n_idx) {
+      int64_t v = ((a.idx64 >> k) & 1) ? ((const int64_t*)a.idx[k])[ioff[k]]
+                                       : (int64_t)((const int32_t*)a.idx[k])[ioff[k]];
+      if (v < 0) v += a.limit[k];
+      if (v < 0 || v >= a.limit[k]) return -1;
+      off += v * a.sel_bstride[k];
+    }
+  }
+  return off;
+}
+
+// Short rows: one word per lane, rows decoded per word.
+template <typename W>
+__global__ __launch_bounds__(kBlock) void adv_index_words_kernel(W* __restrict__ out,
+                                                                 const char* __restrict__ src,
+                                                                 AdvIndex a, int64_t rows,
+                                                                 int64_t wpr) {
+  const int64_t total = rows * wpr;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
+    const int64_t row = wpr == 1 ? t : t / wpr;
+    const int64_t w = t - row * wpr;
+    const int64_t off = adv_row_offset(a, row);
+    out[t] = off >= 0 ? ((const W*)(src + off))[w] : W{};
+  }
+}
+
+// Long rows (64 words or more): a wave per row, the row decoded once and its
+// words moved by the 64 lanes, four loads in flight per lane.
+template <typename W>
+__global__ __launch_bounds__(kBlock) void adv_index_rows_kernel(W* __restrict__ out,
+                                                                const char* __restrict__ src,
+                                                                AdvIndex a, int64_t rows,
+                                                                int64_t wpr) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
+  for (int64_t row = wave; row < rows; row += nwaves) {
+    const int64_t off = adv_row_offset(a, row);
+    const W* s = (const W*)(src + (off >= 0 ? off : 0));
+    W* o = out + row * wpr;
+    for (int64_t w0 = lane; w0 < wpr; w0 += 4 * 64) {
+      W v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t w = w0 + u * 64;
+        v[u] = (off >= 0 && w < wpr) ? s[w] : W{};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t w = w0 + u * 64;
+        if (w < wpr) {
+          if constexpr (sizeof(W) == 16) st_stream(o + w, v[u]);
+          else o[w] = v[u];
+        }
+      }
+    }
+  }
+}
+
+mi_status_t run_adv_index(const mi_tensor_t* out, const mi_tensor_t* self,
+                          const mi_tensor_t* const* indices, int32_t n_indices,
+                          hipStream_t stream) {
+  const int snd = self->ndim;
+  MI_CHECK_ARG(n_indices >= 0 && n_indices <= snd, "index: %d indices for a tensor of %d dims",
+               (int)n_indices, snd);
+  MI_CHECK_ARG(out->dtype == self->dtype, "index: out dtype %s != self dtype %s",
+               dtype_name(out->dtype), dtype_name(self->dtype));
+  // the defined indices, their dims, and the broadcast shape B
+  int kdim[kMaxIdx];
+  const mi_tensor_t* kt[kMaxIdx];
+  int nk = 0;
+  for (int d = 0; d < n_indices; ++d) {
+    if (indices == nullptr || indices[d] == nullptr) continue;
+    MI_RETURN_IF(validate(indices[d], "index"));
+    MI_CHECK_ARG(indices[d]->dtype == MI_I32 || indices[d]->dtype == MI_I64,
+                 "index: index tensors must be int32 or int64, got %s",
+                 dtype_name(indices[d]->dtype));
+    kdim[nk] = d;
+    kt[nk++] = indices[d];
+  }
+  MI_CHECK_ARG(nk > 0, "index: no index tensor given");
+  const mi_tensor_t& b0 = *kt[0];
+  for (int k = 1; k < nk; ++k) {
+    bool same = kt[k]->ndim == b0.ndim;
+    for (int d = 0; same && d < b0.ndim; ++d) same = kt[k]->sizes[d] == b0.sizes[d];
+    MI_CHECK_ARG(same, "index: index tensors must be broadcast to one shape by the caller");
+  }
+  bool adjacent = true;
+  for (int k = 1; k < nk; ++k) adjacent = adjacent && kdim[k] == kdim[k - 1] + 1;
+  // out dims: (self dim or -1 for a dim of B, position in B)
+  int map_self[2 * MI_MAX_DIMS], map_b[2 * MI_MAX_DIMS];
+  int ond = 0;
+  auto push_b = [&]() {
+    for (int j = 0; j < b0.ndim; ++j) {
+      map_self[ond] = -1;
+      map_b[ond++] = j;
+    }
+  };
+  bool is_indexed[MI_MAX_DIMS] = {};
+  for (int k = 0; k < nk; ++k) is_indexed[kdim[k]] = true;
+  if (!adjacent) push_b();
+  for (int d = 0; d < snd; ++d) {
+    if (is_indexed[d]) {
+      if (adjacent && d == kdim[0]) push_b();
+      continue;
+    }
+    map_self[ond] = d;
+    map_b[ond++] = -1;
+  }
+  MI_CHECK_ARG(ond == out->ndim, "index: out has %d dims, expected %d", out->ndim, ond);
+  int64_t bnum = 1;
+  for (int j = 0; j < b0.ndim; ++j) bnum *= b0.sizes[j];
+  for (int d = 0; d < ond; ++d) {
+    const int64_t want = map_self[d] >= 0 ? self->sizes[map_self[d]] : b0.sizes[map_b[d]];
+    MI_CHECK_ARG(out->sizes[d] == want, "index: out size %lld at dim %d, expected %lld",
+                 (long long)out->sizes[d], d, (long long)want);
+  }
+  if (numel(*out) == 0) return MI_OK;
+  for (int k = 0; k < nk; ++k)
+    MI_CHECK_ARG(self->sizes[kdim[k]] > 0 || bnum == 0,
+                 "index: index is out of bounds for dimension with size 0");
+  if (!is_contiguous(*out)) MI_FAIL(MI_ERR_UNSUPPORTED, "index: out must be contiguous");
+  const int64_t es = dtype_size(self->dtype);
+  // fold trailing out dims that run contiguously through self into the row
+  int64_t row_elems = 1;
+  int nd = ond;
+  while (nd > 0 && map_self[nd - 1] >= 0 && self->strides[map_self[nd - 1]] == row_elems) {
+    row_elems *= self->sizes[map_self[nd - 1]];
+    --nd;
+  }
+  AdvIndex a{};
+  a.nd = nd;
+  a.n_idx = nk;
+  uintptr_t align = (uintptr_t)out->data | (uintptr_t)self->data | (uintptr_t)(row_elems * es);
+  int64_t rows = 1;
+  for (int d = 0; d < nd; ++d) {
+    a.sizes[d] = out->sizes[d];
+    rows *= out->sizes[d];
+    if (map_self[d] >= 0) {
+      a.src_bstride[d] = self->strides[map_self[d]] * es;
+      align |= (uintptr_t)a.src_bstride[d];
+    }
+    for (int k = 0; k < nk; ++k)
+      a.idx_stride[k][d] = map_b[d] >= 0 ? kt[k]->strides[map_b[d]] : 0;
+  }
+  for (int k = 0; k < nk; ++k) {
+    a.idx[k] = kt[k]->data;
+    if (kt[k]->dtype == MI_I64) a.idx64 |= 1u << k;
+    a.limit[k] = self->sizes[kdim[k]];
+    a.sel_bstride[k] = self->strides[kdim[k]] * es;
+    align |= (uintptr_t)a.sel_bstride[k];
+  }
+  auto go = [&](auto word) -> mi_status_t {
+    typedef decltype(word) W;
+    const int64_t wpr = row_elems * es / (int64_t)sizeof(W);
+    const int64_t cap = (int64_t)cu_count() * 32;
+    if (wpr >= 64) {
+      const int64_t want = (rows + 3) / 4;  // four waves per block
+      const unsigned grid = (unsigned)(want < cap ? want : cap);
+      hipLaunchKernelGGL((adv_index_rows_kernel<W>), dim3(grid), dim3(kBlock), 0, stream,
+                         (W*)out->data, (const char*)self->data, a, rows, wpr);
+    } else {
+      const int64_t want = (rows * wpr + kBlock - 1) / kBlock;
+      const unsigned grid = (unsigned)(want < cap ? want : cap);
+      hipLaunchKernelGGL((adv_index_words_kernel<W>), dim3(grid), dim3(kBlock), 0, stream,
+                         (W*)out->data, (const char*)self->data, a, rows, wpr);
+    }
+    return check_launch("index");
+  };
+  if (align % 16 == 0) return go(uint4{});
+  if (align % 8 == 0) return go(uint2{});
+  if (align % 4 == 0) return go(uint32_t{});
+  if (align % 2 == 0) return go(uint16_t{});
+  return go(uint8_t{});
+}
+
 }  // namespace
 }  // namespace mi
 
 using namespace mi;
+
+extern "C" mi_status_t mi_index(const mi_tensor_t* out, const mi_tensor_t* self,
+                                const mi_tensor_t* const* indices, int32_t n_indices,
+                                mi_stream_t stream) {
+  clear_error();
+  MI_RETURN_IF(validate(out, "out"));
+  MI_RETURN_IF(validate(self, "self"));
+  return run_adv_index(out, self, indices, n_indices, (hipStream_t)stream);
+}
 
 extern "C" mi_status_t mi_index_select(const mi_tensor_t* out, const mi_tensor_t* self,
                                        int64_t dim, const mi_tensor_t* index,

@@ -94,6 +94,7 @@ _SIGNATURES = {
     "mi_mul_scalar": ([_T, _T, MiScalar, _S], ctypes.c_int),
     "mi_div_scalar": ([_T, _T, MiScalar, _S], ctypes.c_int),
     "mi_index_select": ([_T, _T, ctypes.c_int64, _T, _S], ctypes.c_int),
+    "mi_index": ([_T, _T, ctypes.POINTER(_T), ctypes.c_int32, _S], ctypes.c_int),
     "mi_sum": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
                ctypes.c_int),
     "mi_amax": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
@@ -144,6 +145,23 @@ def lib() -> ctypes.CDLL:
                 fn.restype = res
             _lib = handle
         return _lib
+
+
+def runtime_info() -> dict:
+    """Which HIP runtime the loaded kernel library resolved: the paths of
+    every libamdhip64 mapped into this process (torch's bundled copy and the
+    library share one when they bind to the same file) and that runtime's
+    hipRuntimeGetVersion."""
+    lib()
+    with open("/proc/self/maps") as f:
+        paths = sorted({line.split()[-1] for line in f
+                        if "libamdhip64" in line and line.split()[-1].startswith("/")})
+    version = None
+    if paths:
+        v = ctypes.c_int(0)
+        if ctypes.CDLL(paths[0]).hipRuntimeGetVersion(ctypes.byref(v)) == 0:
+            version = v.value
+    return {"libamdhip64": paths, "hip_runtime_version": version}
 
 
 # ---- descriptors ---------------------------------------------------------------
@@ -367,6 +385,16 @@ def index_select(out, self, dim, index):
     return out
 
 
+def index(out, self, indices):
+    """out = self[indices] through mi_index; indices is a list (one entry per
+    leading dim of self, None for a dim taken whole) of int32/int64 device
+    tensors already broadcast to one shape."""
+    descs = [None if t is None else desc(t) for t in indices]
+    arr = (_T * max(1, len(descs)))(*[None if d is None else ctypes.pointer(d) for d in descs])
+    check("mi_index", lib().mi_index(desc(out), desc(self), arr, len(descs), stream_of(out)))
+    return out
+
+
 def _reduce(name, out, self, dims, keepdim):
     arr, n = _dims(list(dims))
     check(name, getattr(lib(), name)(desc(out), desc(self), arr, n, int(keepdim),
@@ -384,6 +412,7 @@ def amax(out, self, dims: Iterable[int] = (), keepdim=False):
 
 def mean(out, self, dims: Iterable[int] = (), keepdim=False):
     return _reduce("mi_mean", out, self, dims, keepdim)
+
 
 
 def softmax(out, self, dim):
