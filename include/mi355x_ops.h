@@ -279,6 +279,24 @@ mi_status_t mi_mean(const mi_tensor_t* out, const mi_tensor_t* self,
                     const int64_t* dims, int32_t ndims, int32_t keepdim,
                     mi_stream_t stream);
 
+/* Size of the static device scratch of mi_mean_noalloc (per GPU). */
+#define MI_MEAN_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/* mi_mean that allocates nothing.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as mi_mean; the temporary memory mi_mean
+ * takes from the workspace allocator (split-reduction partials; staging
+ * copies for a reduced block that is not dense or an out that is not dense)
+ * comes instead from a static device array of MI_MEAN_NOALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends.  The call makes no hipMalloc /
+ * hipFree and never calls the registered workspace allocator; a call that
+ * would need more scratch than that returns MI_ERR_TOO_LARGE before it
+ * writes out.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (on two streams, or from two threads) race. */
+mi_status_t mi_mean_noalloc(const mi_tensor_t* out, const mi_tensor_t* self,
+                            const int64_t* dims, int32_t ndims,
+                            int32_t keepdim, mi_stream_t stream);
 
 /* ---- softmax family -------------------------------------------------------
  * out = softmax / log_softmax of self along dim, computed in float; out may

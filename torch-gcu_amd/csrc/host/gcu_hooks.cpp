@@ -72,6 +72,13 @@ struct GCUGeneratorImpl : public c10::GeneratorImpl {
   uint64_t offset_ = 0;
 };
 
+// The caching allocator as the kernel library's stream-ordered workspace
+// allocator (gcu_custom_api.cpp:23-31 registers the reference's the same way).
+void register_library_workspace() {
+  mi_set_workspace_allocator(reinterpret_cast<mi_alloc_fn>(&allocator::workspace_alloc),
+                             reinterpret_cast<mi_free_fn>(&allocator::workspace_free), nullptr);
+}
+
 namespace {
 
 std::mutex g_gen_mu;
@@ -88,9 +95,7 @@ struct GCUHooks final : public at::PrivateUse1HooksInterface {
     std::call_once(once, [] {
       g_initialized.store(true);
       allocator::init(device_count());
-      mi_set_workspace_allocator(
-          reinterpret_cast<mi_alloc_fn>(&allocator::workspace_alloc),
-          reinterpret_cast<mi_free_fn>(&allocator::workspace_free), nullptr);
+      register_library_workspace();
     });
   }
 

@@ -14,6 +14,7 @@
 namespace torch_gcu {
 void ensure_initialized();
 bool is_initialized();
+void register_library_workspace();
 }
 
 namespace py = pybind11;
@@ -67,6 +68,9 @@ PYBIND11_MODULE(_C, m) {
 
   m.def("_init", &ensure_initialized);
   m.def("_is_initialized", &is_initialized);
+  // registers the caching allocator with the kernel library again (after a
+  // direct C-ABI caller installed its own workspace allocator)
+  m.def("_register_library_workspace", &register_library_workspace);
   m.def("_device_count", []() { return (int)device_count(); });
   m.def("_current_device", []() { return (int)current_device(); });
   m.def("_set_device", [](int d) { set_device((c10::DeviceIndex)d); });

@@ -45,8 +45,14 @@ mi_status_t check_launch(const char* what) {
   return MI_OK;
 }
 
+namespace {
+thread_local ScratchArena* t_arena = nullptr;
+}
+
+void set_scratch_arena(ScratchArena* arena) { t_arena = arena; }
+
 Workspace::~Workspace() {
-  if (ptr_ != nullptr) {
+  if (ptr_ != nullptr && !from_arena_) {
     mi_free_fn f;
     void* ctx;
     {
@@ -59,6 +65,21 @@ Workspace::~Workspace() {
 }
 
 mi_status_t Workspace::alloc(size_t bytes, hipStream_t stream) {
+  if (t_arena != nullptr) {
+    ScratchArena& ar = *t_arena;
+    const size_t start = (ar.used + 255) & ~(size_t)255;
+    if (start > ar.size || bytes > ar.size - start)
+      MI_FAIL(MI_ERR_TOO_LARGE,
+              "this call needs %zu bytes of scratch (%zu already taken) but the static "
+              "scratch holds %zu bytes",
+              bytes, start, ar.size);
+    ptr_ = ar.base + start;
+    ar.used = start + bytes;
+    if (ar.used > ar.peak) ar.peak = ar.used;
+    stream_ = stream;
+    from_arena_ = true;
+    return MI_OK;
+  }
   mi_alloc_fn a;
   void* ctx;
   {

@@ -43,7 +43,8 @@ mi_status_t check_launch(const char* what);
 
 // ---- workspace ----------------------------------------------------------------
 
-// RAII workspace from the registered allocator.
+// RAII workspace from the registered allocator, or from this thread's
+// scratch arena while one is set.
 class Workspace {
  public:
   Workspace() = default;
@@ -56,7 +57,21 @@ class Workspace {
  private:
   void* ptr_ = nullptr;
   hipStream_t stream_ = nullptr;
+  bool from_arena_ = false;
 };
+
+// A fixed device buffer that Workspace::alloc carves from (256-byte aligned
+// bump allocation, nothing returned until the arena is cleared) while it is
+// set on the calling thread.  An entry point that must not allocate sets one
+// over its static scratch for the duration of the call; a request that does
+// not fit fails with MI_ERR_TOO_LARGE instead of reaching the allocator.
+struct ScratchArena {
+  char* base;
+  size_t size;
+  size_t used;
+  size_t peak;
+};
+void set_scratch_arena(ScratchArena* arena);  // nullptr clears it
 
 int cu_count();
 

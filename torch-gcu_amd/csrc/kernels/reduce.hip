@@ -16,6 +16,7 @@
 // Floating inputs accumulate in float (double for f64), integers in int64.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "iter.h"
@@ -540,12 +541,65 @@ mi_status_t run_reduce(int op, const mi_tensor_t* out, const mi_tensor_t* self,
   return MI_OK;
 }
 
+// ---- static scratch of mi_mean_noalloc ---------------------------------------
+//
+// Device memory of the reductions that take no allocation: the split-row and
+// split-column partials (config 2's fp32 [16384, 4096] mean over dim 0 takes
+// 256 x 4096 floats = 4 MiB), and, for inputs whose reduced dims are not one
+// dense block or an output that is not dense, the staging copies.  Every
+// byte a kernel reads from it was written earlier in the same call, so
+// nothing is cleared between calls.  One copy per GPU, held until the
+// process ends; concurrent calls on one GPU (two streams or two threads)
+// share it and race.
+constexpr size_t kScratchBytes = MI_MEAN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device: the address of `scratch`
+
+// Device address of this GPU's `scratch`, looked up once per device with it
+// current.  Host code never passes `scratch` itself to a kernel: on the host
+// that name is a stand-in, not a device address.
+mi_status_t scratch_on_current_device(char** out) {
+  int dev = 0;
+  const hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess) MI_FAIL(MI_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(de));
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      MI_FAIL(MI_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+              hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = (char*)g_scratch_ptr[dev];
+  return MI_OK;
+}
+
+// Clears the thread's arena on every return path.
+struct ArenaScope {
+  explicit ArenaScope(ScratchArena* a) { set_scratch_arena(a); }
+  ~ArenaScope() { set_scratch_arena(nullptr); }
+};
+
 }  // namespace
 }  // namespace mi
 
 using namespace mi;
 
 extern "C" {
+
+mi_status_t mi_mean_noalloc(const mi_tensor_t* out, const mi_tensor_t* self, const int64_t* dims,
+                            int32_t ndims, int32_t keepdim, mi_stream_t stream) {
+  clear_error();
+  char* base = nullptr;
+  MI_RETURN_IF(scratch_on_current_device(&base));
+  ScratchArena arena{base, kScratchBytes, 0, 0};
+  ArenaScope scope(&arena);
+  return run_reduce(R_MEAN, out, self, dims, ndims, keepdim, (hipStream_t)stream);
+}
 
 mi_status_t mi_sum(const mi_tensor_t* out, const mi_tensor_t* self, const int64_t* dims,
                    int32_t ndims, int32_t keepdim, mi_stream_t stream) {

@@ -101,6 +101,8 @@ _SIGNATURES = {
                 ctypes.c_int),
     "mi_mean": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
                 ctypes.c_int),
+    "mi_mean_noalloc": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32,
+                         _S], ctypes.c_int),
     "mi_softmax": ([_T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_log_softmax": ([_T, _T, ctypes.c_int64, _S], ctypes.c_int),
     "mi_rms_norm": ([_T, _T, _T, ctypes.c_double, _S], ctypes.c_int),
@@ -413,6 +415,11 @@ def amax(out, self, dims: Iterable[int] = (), keepdim=False):
 def mean(out, self, dims: Iterable[int] = (), keepdim=False):
     return _reduce("mi_mean", out, self, dims, keepdim)
 
+
+def mean_noalloc(out, self, dims: Iterable[int] = (), keepdim=False):
+    """mi_mean_noalloc: mean with its temporary memory in the library's
+    static per-GPU scratch (no allocation)."""
+    return _reduce("mi_mean_noalloc", out, self, dims, keepdim)
 
 
 def softmax(out, self, dim):
