@@ -309,3 +309,19 @@ def int32_indices_index(self, indices):
     index dims by the same adjacent / non-adjacent rule) and by a brute-force
     walk over output positions."""
     return torch.ops.aten.index(self, [None if i is None else i.long() for i in indices])
+
+
+def widened_fallback(fn, *args, **kwargs):
+    """The CPU fallback of an op whose CPU kernel lacks a 16-bit float dtype
+    (torch_gcu/csrc/aten/aten_cpu_fallback.cpp:193-340): every tensor of that
+    dtype widened to float32, the op run on CPU ATen, and the tensor results
+    rounded back to the 16-bit dtype.  Pinned by float64 closed forms (a
+    diagonal sum, scipy's erfcx) rounded to the 16-bit dtype."""
+    low = next(a.dtype for a in args
+               if isinstance(a, torch.Tensor) and a.dtype in (torch.float16, torch.bfloat16))
+    wide = [a.float() if isinstance(a, torch.Tensor) and a.dtype == low else a for a in args]
+    out = fn(*wide, **kwargs)
+    if isinstance(out, torch.Tensor):
+        return out.to(low) if out.dtype == torch.float32 else out
+    return type(out)(o.to(low) if isinstance(o, torch.Tensor) and o.dtype == torch.float32 else o
+                     for o in out)

@@ -141,7 +141,7 @@ def test_op_debug_forced_fallback_op_check_and_statistics():
     # different order than CPU's only agrees to about 1e-6 relative, so the
     # run uses the fp32 reduction bar of this build (1e-5) instead of the
     # reference's 1e-6 default
-    C._set_op_debug_config("op_check=all_ops op_check_rtol_fp32=1e-5 op_check_atol_fp32=1e-5")
+    C._set_op_debug_config("op_check=all_ops op_check_tol_fp32=1e-5,1e-5")
     y = (d * 3 + d).sum(0)
     assert_close(y.cpu(), (x * 3 + x).sum(0), "fp32", "op_check run")
 

@@ -551,3 +551,26 @@ def test_int32_indices_index_planted_mistake_non_adjacent_order():
     wrong = np.stack([arr[idx[0][j], :, idx[2][j]] for j in range(2)], 0)  # same here...
     wrong_layout = np.moveaxis(wrong, 0, 1)  # ...but B placed second
     assert wrong_layout.shape != want.shape or not np.array_equal(wrong_layout, want)
+
+
+# ---- the CPU fallback widened to float ------------------------------------------------
+
+@pytest.mark.parametrize("low", [torch.float16, torch.bfloat16])
+def test_widened_fallback_vs_float64_closed_forms(low):
+    import scipy.special
+
+    # integer-valued matrix: the diagonal sum is exact in every precision
+    m = torch.randint(-8, 9, (12, 12), generator=g(80)).to(low)
+    t = aten.widened_fallback(torch.trace, m)
+    assert t.dtype == low and t.dim() == 0
+    assert float(t) == float(np.trace(m.double().numpy()))
+    x = (torch.rand(500, generator=g(81)) * 6 - 2).to(low)
+    got = aten.widened_fallback(torch.special.erfcx, x)
+    assert got.dtype == low
+    ref = torch.from_numpy(scipy.special.erfcx(x.double().numpy())).to(low)
+    # float32 erfcx rounded to 16 bits vs float64 rounded to 16 bits: at most
+    # one unit in the last place apart
+    ulp = (ref.double().abs() * (2.0 ** -10 if low == torch.float16 else 2.0 ** -7)).clamp_min(1e-30)
+    assert bool(((got.double() - ref.double()).abs() <= ulp).all())
+    # a planted mistake: forgetting to round the result back leaves float32
+    assert torch.special.erfcx(x.float()).dtype != low

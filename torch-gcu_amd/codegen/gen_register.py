@@ -12,10 +12,23 @@ Output (into the build directory):
                           reference's generated wrappers do
                           (codegen/wrapper_torch_codegen.py:350-440 and
                           codegen/gen_GCUNativeFunctions_methods.py:145-330):
-                          device check, device guard, forced CPU fallback /
-                          op_check / statistics under ENFLAME_PT_OP_DEBUG_CONFIG,
-                          the native call and the op_sync_mode stream sync;
-                          then ``TORCH_LIBRARY_IMPL(aten, PrivateUse1, m)``.
+                          device check, device guard, the fallback policy of
+                          ``gcu_op_fallback.yaml``, forced CPU fallback /
+                          op_check / input and output dumps / statistics /
+                          calltrace under ENFLAME_PT_OP_DEBUG_CONFIG, the
+                          native call and the op_sync_mode stream sync; then
+                          ``TORCH_LIBRARY_IMPL(aten, PrivateUse1, m)``, which
+                          skips ops the configuration deregisters and records
+                          the policy for introspection.
+
+The fallback policy (codegen/gcu_op_fallback.yaml, the format of the
+reference's file and generator: codegen/gcu_op_fallback.yaml:1-64,
+codegen/gen_op_fallback_register.py:112-176, register_fallback_ops.h:88-105)
+names, for this hardware (the ``mi355x`` key), native ops that run on CPU
+ATen always ("all") or when an argument takes one of the listed values: a
+tensor by its dtype ("self: ComplexFloat"), a ScalarType, string, bool or
+int argument by its value.  The rules become plain comparisons in the
+wrapper, ahead of the native call.
 """
 from __future__ import annotations
 
@@ -27,6 +40,15 @@ import yaml
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 OPS_YAML = os.path.join(HERE, "gcu_native_functions.yaml")
+POLICY_YAML = os.path.join(HERE, "gcu_op_fallback.yaml")
+HARDWARE = "mi355x"
+
+# c10::ScalarType names a policy may list for a tensor or dtype argument
+SCALAR_TYPES = {
+    "Byte", "Char", "Short", "Int", "Long", "Half", "Float", "Double", "ComplexHalf",
+    "ComplexFloat", "ComplexDouble", "Bool", "BFloat16", "UInt16", "UInt32", "UInt64",
+    "Float8_e5m2", "Float8_e4m3fn", "Float8_e5m2fnuz", "Float8_e4m3fnuz",
+}
 
 
 @dataclass
@@ -55,6 +77,91 @@ def load_entries(path: str | None = None) -> list[OpEntry]:
     dup = {n for n in names if names.count(n) > 1}
     assert not dup, f"duplicate ops in {path}: {sorted(dup)}"
     return out
+
+
+def load_policy(path: str | None = None) -> dict[str, object]:
+    """op name -> "all" or [(arg, [values]), ...] for this hardware."""
+    path = path or POLICY_YAML
+    with open(path) as f:
+        doc = yaml.safe_load(f) or {}
+    out: dict[str, object] = {}
+    for e in doc.get("fallback", []) or []:
+        cfg = e.get(HARDWARE)
+        if cfg is None:
+            continue
+        name = e["name"]
+        assert name not in out, f"{path}: {name} listed twice"
+        if cfg == "all":
+            out[name] = "all"
+            continue
+        assert isinstance(cfg, list), f"{path}: {name}: expected 'all' or a list of rules"
+        rules = []
+        for r in cfg:
+            assert isinstance(r, dict) and len(r) == 1, f"{path}: {name}: bad rule {r!r}"
+            (arg, vals), = r.items()
+            values = [v.strip() for v in str(vals).split(",") if v.strip()]
+            assert values, f"{path}: {name}: rule for {arg} has no values"
+            rules.append((arg, values))
+        out[name] = rules
+    return out
+
+
+def _policy_condition(op: str, schema, rules) -> tuple[str, list[str]]:
+    """C++ condition that is true when a call must take the CPU fallback, and
+    the rules as "arg::value" strings."""
+    from torchgen.model import BaseTy, BaseType, ListType, OptionalType
+
+    args = {a.name: a.type for a in schema.arguments.flat_all}
+    terms, strings = [], []
+    for arg, values in rules:
+        assert arg in args, f"fallback policy of {op}: {arg} is not an argument of {schema}"
+        t = args[arg]
+        strings += [f"{arg}::{v}" for v in values]
+        opt = isinstance(t, OptionalType)
+        base = t.elem if opt else t
+
+        def dtypes(expr):
+            for v in values:
+                assert v in SCALAR_TYPES, f"fallback policy of {op}: {v} is not a dtype"
+            return " || ".join(f"{expr} == at::ScalarType::{v}" for v in values)
+
+        if isinstance(base, BaseType) and base.name == BaseTy.Tensor:
+            if opt:
+                terms.append(f"({arg}.has_value() && {arg}->defined() && "
+                             f"({dtypes(f'{arg}->scalar_type()')}))")
+            else:
+                terms.append(f"({arg}.defined() && ({dtypes(f'{arg}.scalar_type()')}))")
+        elif isinstance(base, ListType) and isinstance(base.elem, BaseType) and \
+                base.elem.name == BaseTy.Tensor:
+            lst = ", ".join(f"at::ScalarType::{v}" for v in values)
+            for v in values:
+                assert v in SCALAR_TYPES, f"fallback policy of {op}: {v} is not a dtype"
+            terms.append(f"torch_gcu::any_dtype_in({arg}, {{{lst}}})")
+        elif isinstance(base, BaseType) and base.name == BaseTy.ScalarType:
+            e = f"(*{arg})" if opt else arg
+            cond = f"({dtypes(e)})"
+            terms.append(f"({arg}.has_value() && {cond})" if opt else cond)
+        elif isinstance(base, BaseType) and base.name == BaseTy.str:
+            e = f"(*{arg})" if opt else arg
+            cond = "(" + " || ".join(f'{e} == "{v}"' for v in values) + ")"
+            terms.append(f"({arg}.has_value() && {cond})" if opt else cond)
+        elif isinstance(base, BaseType) and base.name == BaseTy.bool:
+            e = f"(*{arg})" if opt else arg
+            vs = {"true": "true", "1": "true", "false": "false", "0": "false"}
+            cond = "(" + " || ".join(f"{e} == {vs[v.lower()]}" for v in values) + ")"
+            terms.append(f"({arg}.has_value() && {cond})" if opt else cond)
+        elif isinstance(base, BaseType) and base.name in (BaseTy.int, BaseTy.SymInt):
+            e = f"(*{arg})" if opt else arg
+            cond = "(" + " || ".join(f"{e} == {int(v)}" for v in values) + ")"
+            terms.append(f"({arg}.has_value() && {cond})" if opt else cond)
+        elif isinstance(base, BaseType) and base.name == BaseTy.Scalar:
+            e = f"{arg}->type()" if opt else f"{arg}.type()"
+            cond = f"({dtypes(e)})"
+            terms.append(f"({arg}.has_value() && {cond})" if opt else cond)
+        else:
+            raise AssertionError(f"fallback policy of {op}: argument {arg} of type {t} "
+                                 "cannot carry a rule")
+    return " || ".join(terms), strings
 
 
 def native_schemas() -> dict[str, tuple[str, bool, bool]]:
@@ -132,8 +239,10 @@ def _aliased_return_arg(schema):
 
 def generate(out_dir: str) -> list[str]:
     entries = load_entries()
+    policy = load_policy()
+    used_policy: set[str] = set()
     schemas = native_schemas()
-    decls, wrappers, regs = [], [], []
+    decls, wrappers, regs, policy_regs = [], [], [], []
     for e in entries:
         if e.name not in schemas:
             raise KeyError(f"{e.name} is not an ATen operator (native_functions.yaml)")
@@ -163,34 +272,71 @@ def generate(out_dir: str) -> list[str]:
                     guard_expr = " , ".join(f"torch_gcu::gcu_device_of({n})" for n in first)
                     body.append(f"  const c10::OptionalDeviceGuard device_guard("
                                 f"torch_gcu::first_gcu_device({{{guard_expr}}}));")
-        # debug paths (fallback / op_check / statistics)
+        ovl = overload if overload else ""
+        fallback_call = (f"at::native::call_fallback_fn<&torch_gcu::gcu_cpu_fallback, "
+                         f"ATEN_OP2({base}, {ovl})>::call({arg_names})" if overload else
+                         f"at::native::call_fallback_fn<&torch_gcu::gcu_cpu_fallback, "
+                         f"ATEN_OP({base})>::call({arg_names})")
+        # the fallback policy of this hardware (gcu_op_fallback.yaml)
+        pol = policy.get(e.name)
+        if pol is not None:
+            assert e.fallback_cpu, f"{e.name} has a fallback policy but fallback_cpu: false"
+            if pol == "all":
+                body.append(f"  return {fallback_call};  // fallback policy: all")
+                policy_regs.append(f'  torch_gcu::register_fallback_policy("{e.name}", {{"all"}});')
+            else:
+                cond, strings = _policy_condition(e.name, schema, pol)
+                body.append(f"  if ({cond}) return {fallback_call};  // fallback policy")
+                lst = ", ".join(f'"{x}"' for x in strings)
+                policy_regs.append(f'  torch_gcu::register_fallback_policy("{e.name}", {{{lst}}});')
+            used_policy.add(e.name)
+        # debug paths: names / calltrace, forced fallback, op_check,
+        # statistics, input and output dumps
+        boxed_args = f"c10::impl::boxArgs<{', '.join(boxed)}>({arg_names})" if boxed else \
+            "torch::jit::Stack()"
         dbg = []
-        dbg.append(f"    static const std::string kName = \"{e.name}\";")
+        dbg.append(f"    static const std::string kName = \"{e.name}\", kCpp = \"{fn}\";")
         dbg.append("    const auto& cfg = torch_gcu::OpDebugConfig::get();")
+        dbg.append("    if (!torch_gcu::in_op_check()) torch_gcu::trace_call(kName, kCpp);")
         if e.fallback_cpu:
-            ovl = overload if overload else ""
-            dbg.append("    if (cfg.forced_fallback(kName)) {")
-            dbg.append(f"      return at::native::call_fallback_fn<&torch_gcu::gcu_cpu_fallback, "
-                       f"ATEN_OP2({base}, {ovl})>::call({arg_names});"
-                       if overload else
-                       f"      return at::native::call_fallback_fn<&torch_gcu::gcu_cpu_fallback, "
-                       f"ATEN_OP({base})>::call({arg_names});")
+            dbg.append("    if (torch_gcu::forced_fallback(kName, kCpp)) {")
+            dbg.append(f"      return {fallback_call};")
             dbg.append("    }")
+        dbg.append(f"    static const auto op_ = c10::Dispatcher::singleton().findSchemaOrThrow(\"aten::{base}\", \"{overload}\");")
         if e.op_check:
             alias = _aliased_return_arg(schema)
             ret_ok = ret in ("at::Tensor",) or alias is not None
             if ret_ok:
-                dbg.append("    if (cfg.checked(kName) && !torch_gcu::in_op_check()) {")
+                dbg.append("    if (!torch_gcu::in_op_check() && torch_gcu::checked(kName, kCpp)) {")
                 dbg.append("      torch_gcu::OpCheckScope scope_;")
-                dbg.append(f"      static const auto op_ = c10::Dispatcher::singleton().findSchemaOrThrow(\"aten::{base}\", \"{overload}\");")
-                dbg.append(f"      auto stack_ = c10::impl::boxArgs<{', '.join(boxed)}>({arg_names});")
-                dbg.append("      torch_gcu::op_check_boxed(op_, &stack_, c10::DispatchKeySet(c10::DispatchKey::PrivateUse1));")
+                dbg.append(f"      auto stack_ = {boxed_args};")
+                # the native run inside re-enters this wrapper, which records
+                # the call's statistics and dumps
+                dbg.append("      torch_gcu::op_check_boxed(op_, &stack_, c10::DispatchKeySet(c10::DispatchKey::PrivateUse1), kCpp);")
                 if alias is not None:
                     dbg.append(f"      return {alias};")
                 else:
                     dbg.append("      return stack_.back().toTensor();")
                 dbg.append("    }")
-        dbg.append("    if (cfg.statistics) torch_gcu::count_op(kName, false);")
+        dbg.append("    if (cfg.statistics) {")
+        dbg.append(f"      const auto args_ = {boxed_args};")
+        dbg.append("      torch_gcu::count_op(kName, false, &args_, &op_.schema());")
+        dbg.append("    }")
+        dbg.append("    const bool din_ = torch_gcu::dump_inputs(kName, kCpp);")
+        dbg.append("    const bool dout_ = torch_gcu::dump_outputs(kName, kCpp);")
+        dbg.append("    if (din_ || dout_) {")
+        dbg.append(f"      if (din_) torch_gcu::dump_call(kCpp, \"input\", {boxed_args});")
+        if ret == "void":
+            dbg.append(f"      torch_gcu::aotops::{fn}({arg_names});")
+            dbg.append("      torch_gcu::after_op();")
+            dbg.append(f"      if (dout_) torch_gcu::dump_call(kCpp, \"output\", {boxed_args});")
+            dbg.append("      return;")
+        else:
+            dbg.append(f"      {'auto&&' if '&' in ret else 'auto'} d_ = torch_gcu::aotops::{fn}({arg_names});")
+            dbg.append("      torch_gcu::after_op();")
+            dbg.append("      if (dout_) torch_gcu::dump_call(kCpp, \"output\", {c10::IValue(d_)});")
+            dbg.append("      return d_;")
+        dbg.append("    }")
         body.append("  if (C10_UNLIKELY(torch_gcu::op_debug_active())) {")
         body.extend(dbg)
         body.append("  }")
@@ -203,11 +349,15 @@ def generate(out_dir: str) -> list[str]:
             body.append("  torch_gcu::after_op();")
             body.append("  return r_;")
         wrappers.append(f"{ret} wrapper_PrivateUse1_{fn}({decl_args}) {{\n" + "\n".join(body) + "\n}\n")
-        reg = f"m.impl(\"{e.name}\", TORCH_FN(wrapper_PrivateUse1_{fn}));"
+        reg = (f"if (!torch_gcu::deregistered(\"{e.name}\", \"{fn}\")) "
+               f"m.impl(\"{e.name}\", TORCH_FN(wrapper_PrivateUse1_{fn}));")
         if e.env_gate:
-            regs.append(f"  if (torch_gcu::env_true(\"{e.env_gate}\")) {reg}")
+            regs.append(f"  if (torch_gcu::env_true(\"{e.env_gate}\")) {{ {reg} }}")
         else:
             regs.append(f"  {reg}")
+    unused = set(policy) - used_policy
+    assert not unused, (f"fallback policy names ops without a native kernel "
+                        f"(they run on CPU anyway): {sorted(unused)}")
 
     header_text = (
         "// Generated by codegen/gen_register.py from codegen/gcu_native_functions.yaml.\n"
@@ -223,7 +373,7 @@ def generate(out_dir: str) -> list[str]:
         "#include \"op_debug.h\"\n\nnamespace {\n\n"
         + "\n".join(wrappers)
         + "\n}  // namespace\n\nTORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {\n"
-        + "\n".join(regs) + "\n}\n")
+        + "\n".join(policy_regs + regs) + "\n}\n")
     src = os.path.join(out_dir, "RegisterGCU.cpp")
     _write_if_changed(os.path.join(out_dir, "aotops.h"), header_text)
     _write_if_changed(src, src_text)

@@ -14,7 +14,7 @@ thread_local int tls_op_check_depth = 0;
 
 bool op_debug_active() {
   static const OpDebugConfig& c = OpDebugConfig::get();
-  return c.any_debug();
+  return c.any_debug() || any_scope();
 }
 
 bool in_op_check() { return tls_op_check_depth > 0; }

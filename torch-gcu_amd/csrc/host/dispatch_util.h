@@ -44,6 +44,21 @@ inline std::optional<at::Device> first_gcu_device(
   return std::nullopt;
 }
 
+// True when a tensor of the list has one of the dtypes (fallback policy rules
+// on tensor-list arguments).
+inline bool any_dtype_in(const at::ITensorListRef& l, std::initializer_list<at::ScalarType> dts) {
+  for (const at::Tensor& t : l)
+    for (at::ScalarType d : dts)
+      if (t.defined() && t.scalar_type() == d) return true;
+  return false;
+}
+inline bool any_dtype_in(at::TensorList l, std::initializer_list<at::ScalarType> dts) {
+  for (const at::Tensor& t : l)
+    for (at::ScalarType d : dts)
+      if (t.defined() && t.scalar_type() == d) return true;
+  return false;
+}
+
 bool op_debug_active();
 bool in_op_check();
 struct OpCheckScope {

@@ -57,6 +57,21 @@ py::tuple stream_tuple(c10::Stream s) {
   return py::make_tuple(s.id(), (int)s.device_index(), (int)s.device_type());
 }
 
+// The calling Python stack, for op_calltrace (the reference's
+// GetPythonFrame); empty when the interpreter is not running.
+std::string python_stack() {
+  if (!Py_IsInitialized()) return std::string();
+  py::gil_scoped_acquire gil;
+  try {
+    std::string s;
+    for (const auto& line : py::module::import("traceback").attr("format_stack")())
+      s += line.cast<std::string>();
+    return s;
+  } catch (const std::exception& e) {
+    return std::string("  <Python stack unavailable: ") + e.what() + ">\n";
+  }
+}
+
 c10::Stream stream_from(int64_t id, int device) {
   return c10::Stream(c10::Stream::UNSAFE, c10::Device(kGCU, (c10::DeviceIndex)device), id);
 }
@@ -238,12 +253,43 @@ PYBIND11_MODULE(_C, m) {
     return efficient::int32_indices_index(self, l);
   });
 
-  // op debug
+  // op debug (the reference's torch_gcu/csrc/InitGcuBindings.cpp:131-153)
   m.def("_set_op_debug_config", &set_op_debug_config);
+  m.def("_op_debug_config", []() {
+    const OpDebugConfig& c = OpDebugConfig::get();
+    py::dict d;
+    d["dump_path"] = c.dump_path;
+    d["op_check_dump_dir"] = c.check_dump_dir;
+    d["op_dump_dir"] = c.op_dump_dir;
+    d["op_statistics"] = c.statistics;
+    d["op_statistics_dump"] = c.statistics_dump;
+    d["op_check_tol"] = py::make_tuple(py::make_tuple(c.rtol_fp32, c.atol_fp32),
+                                       py::make_tuple(c.rtol_fp16, c.atol_fp16),
+                                       py::make_tuple(c.rtol_bf16, c.atol_bf16));
+    return d;
+  });
   m.def("_op_statistics", []() {
     py::dict d;
     for (const auto& kv : op_statistics()) d[py::str(kv.first)] = py::make_tuple(kv.second.first, kv.second.second);
     return d;
   });
   m.def("_clear_op_statistics", &clear_op_statistics);
+  m.def("_clear_statistics", &clear_op_statistics);
+  m.def("_get_op_statistics_info", &op_statistics_info);
+  m.def("_dump_op_statistics_to_json", &dump_op_statistics_json);
+  m.def("_enter_dump_op_name_scope", []() { set_scope(0, true); });
+  m.def("_exit_print_cpp_name_scope", []() { set_scope(0, false); });
+  m.def("_enter_fallback_cpu_scope", []() { set_scope(1, true); });
+  m.def("_exit_fallback_cpu_scope", []() { set_scope(1, false); });
+  m.def("_enter_op_check_scope", []() { set_scope(2, true); });
+  m.def("_exit_op_check_scope", []() { set_scope(2, false); });
+  m.def("_get_dump_op_name_scope_state", []() { return scope_state(0); });
+  m.def("_get_fallback_cpu_scope_state", []() { return scope_state(1); });
+  m.def("_get_op_check_scope_state", []() { return scope_state(2); });
+  m.def("_fallback_policy", []() {
+    py::dict d;
+    for (const auto& kv : fallback_policy()) d[py::str(kv.first)] = kv.second;
+    return d;
+  });
+  set_python_stack_fn(&python_stack);
 }

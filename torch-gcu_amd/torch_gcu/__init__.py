@@ -31,4 +31,11 @@ _C._init()
 
 from .gcu import efficient  # noqa: E402,F401
 
+if _C._op_debug_config()["op_statistics_dump"]:
+    # op_statistics_dump=true: the statistics are written at exit
+    # (the reference dumps them when its statistics object is destroyed)
+    import atexit as _atexit
+
+    _atexit.register(_C._dump_op_statistics_to_json)
+
 __all__ = ["gcu", "efficient"]

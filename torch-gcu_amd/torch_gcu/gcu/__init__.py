@@ -219,4 +219,4 @@ if hasattr(os, "register_at_fork"):
     os.register_at_fork(after_in_child=_after_fork_in_child)
 
 
-from . import efficient  # noqa: E402,F401
+from . import debug, efficient  # noqa: E402,F401
