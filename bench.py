@@ -102,6 +102,9 @@ def run_config2(torch, _abi, synthetic, steps, warmup):
         "log_softmax": torch.empty(rows, vocab, dtype=torch.bfloat16, device="cuda"),
         "mean": torch.empty(sets[0]["m"].shape[1], dtype=torch.float32, device="cuda"),
     }
+    # the same inputs on the gcu device, for the step through the dispatcher
+    gsets = [{"logits": st["logits"].cpu().to("gcu"), "m": st["m"].cpu().to("gcu")}
+             for st in sets]
     timers = {k: EventTimer(torch) for k in outs}
     # one plain 512 MiB device copy (untimed): under rocprofv3 --pmc its
     # FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes
@@ -126,16 +129,43 @@ def run_config2(torch, _abi, synthetic, steps, warmup):
             _abi.log_softmax(outs["log_softmax"], s["logits"], -1)
             _abi.mean(outs["mean"], s["m"], [0])
 
+    def dispatch_step(i):
+        # the PrivateUse1 path: torch ops on gcu tensors, through the
+        # generated wrappers into the same kernels
+        s = gsets[i % 2]
+        torch.sum(s["logits"], -1)
+        torch.amax(s["logits"], -1)
+        torch.log_softmax(s["logits"], -1)
+        torch.mean(s["m"], 0)
+
     for i in range(warmup):
         step(i, False)
+        dispatch_step(i)
     torch.cuda.synchronize()
+    torch.gcu.synchronize()
     log(f"bench: warmup done ({warmup} steps), timing {steps} steps")
-    # whole-job wall time of exactly `steps` steps
+    # whole-job wall time of exactly `steps` steps, through the dispatcher
+    t0 = time.perf_counter()
+    for i in range(steps):
+        dispatch_step(i)
+    torch.gcu.synchronize()
+    wall = time.perf_counter() - t0
+    # the same steps called through the C ABI directly
     t0 = time.perf_counter()
     for i in range(steps):
         step(i, False)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    wall_abi = time.perf_counter() - t0
+    # host cost of one dispatched op: the enqueue loop timed while a spin
+    # kernel holds the device (gcu's default stream is the null stream the
+    # spin runs on), so the host never waits on it
+    hold_device(torch)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        dispatch_step(i)
+    host_us = (time.perf_counter() - t0) / (4 * steps) * 1e6
+    torch.gcu.synchronize()
+    torch.cuda.synchronize()
     # per-kernel device time: the same steps again with HIP events around each
     # launch, queued behind a spin kernel so no host launch gap is counted
     hold_device(torch)
@@ -143,7 +173,7 @@ def run_config2(torch, _abi, synthetic, steps, warmup):
         step(i, True)
     torch.cuda.synchronize()
     per_op_ms = {k: t.total_ms() / steps for k, t in timers.items()}
-    return wall, per_op_ms
+    return wall, wall_abi, host_us, per_op_ms
 
 
 TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "log_softmax_config2_traffic.md")
@@ -160,6 +190,99 @@ def committed_traffic():
         return None
     m = re.search(r"traffic_bytes_per_launch = (\d+)", text)
     return int(m.group(1)) if m else None
+
+
+def cpu_model():
+    """The host CPU's model name (the first `model name` of /proc/cpuinfo,
+    what lscpu prints)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_time(fn, min_s=0.6, max_n=50):
+    """Mean wall time of fn on the host after one warm-up call."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= min_s or n >= max_n:
+            return el / n
+
+
+def cpu_config_ops(torch, synthetic):
+    """CPU ATen (the reference's fallback path) on every config op of the
+    bench, on bounded samples of the same workloads: {op name: record}.
+    Fused ops without a reference op (RMSNorm, RoPE, SiLU-mul, int8 linear)
+    run as their fp32 closed forms (oracle.aten)."""
+    from oracle import aten
+    from torch_gcu.utils import decoder_layer as dl
+
+    log("bench: CPU ATen per config")
+    thr = torch.get_num_threads()
+    out = {}
+
+    def rec(name, sec, sample, alg=None, flops=None, tokens=None):
+        r = {"ms": round(sec * 1e3, 3), "threads": thr, "sample": sample}
+        if alg is not None:
+            r["GB/s"] = round(alg / sec / 1e9, 2)
+        if flops is not None:
+            r["TFLOP/s"] = round(flops / sec / 1e12, 4)
+        if tokens is not None:
+            r["tok/s"] = round(tokens / sec, 1)
+        out[name] = r
+
+    c1 = synthetic.config1()
+    rec("c1.mul [4096,4096]x[4096] f32", cpu_time(lambda: aten.mul(c1["a"], c1["b"])),
+        "full size", alg=4096 * 4096 * 8 + 4096 * 4)
+    rec("c1.add [4096,4096]+0.5 f32", cpu_time(lambda: aten.add(c1["a"], 0.5)), "full size",
+        alg=4096 * 4096 * 8)
+    rec("c1.index_select int64 [1048576,8] x 262144",
+        cpu_time(lambda: aten.index_select(c1["table"], 0, c1["idx"])), "full size", alg=35651584)
+    del c1
+    T = 2048  # 1/8 of config 3's 16384 tokens
+    c3 = synthetic.config3(tokens=T)
+    rec("c3.rms_norm bf16 [16384,4096]", cpu_time(lambda: aten.rms_norm(c3["x"], c3["w"], 1e-6)),
+        f"{T} of 16384 rows", alg=T * 4096 * 4 + 8192)
+    rec("c3.rope q,k bf16 [16384,32,128]",
+        cpu_time(lambda: (aten.rope(c3["q"], c3["pos"], 1e4), aten.rope(c3["k"], c3["pos"], 1e4))),
+        f"{T} of 16384 tokens", alg=4 * T * 32 * 128 * 2)
+    rec("c3.silu_mul bf16 [16384,11008]", cpu_time(lambda: aten.silu_mul(c3["gate"], c3["up"])),
+        f"{T} of 16384 rows", alg=3 * T * 11008 * 2)
+    del c3
+    gen = torch.Generator().manual_seed(20261204)
+    M = 1024  # 1/8 of config 4's 8192 rows
+    A = (torch.randn(M, 4096, generator=gen) * 0.02).bfloat16()
+    B = (torch.randn(4096, 4096, generator=gen) * 0.02).bfloat16()
+    bias = (torch.randn(4096, generator=gen) * 0.02).bfloat16()
+    sec = cpu_time(lambda: torch.addmm(bias, A, B))
+    for lay in ("B row-major [K,N]", "B = W^T, K-contiguous"):
+        rec(f"c4.addmm bf16 M8192 N4096 K4096 ({lay})", sec, f"CPU ATen bf16 addmm, M={M} rows",
+            flops=2 * M * 4096 * 4096)
+    W = torch.randint(-127, 128, (11008, 4096), generator=gen, dtype=torch.int8)
+    sc = torch.rand(11008, generator=gen) * 0.009 + 0.001
+    for Mi in (16, 256, 4096):
+        m = min(Mi, 512)
+        x = torch.randn(m, 4096, generator=gen).bfloat16()
+        rec(f"c4.int8_linear M={Mi} W int8 [11008,4096]",
+            cpu_time(lambda: aten.int8_linear(x, W, sc)),
+            f"fp32 closed form, M={m} rows" + ("" if m == Mi else f" of {Mi}"),
+            flops=2 * m * 11008 * 4096)
+    del A, B, W
+    cfg = dl.LayerConfig()
+    w = dl.init_weights(cfg)
+    ids = torch.randint(0, cfg.vocab, (1, 2048), generator=gen)
+    sec = cpu_time(lambda: dl.forward(w, ids, cfg), min_s=1.0, max_n=3)
+    for name in ("eager", "gcugraph replay"):
+        rec(f"c5.decoder_layer fwd B8xS2048 ({name})", sec,
+            "CPU ATen bf16 layer on 1 of the 8 sequences (2048 tokens)", tokens=2048)
+    return out
 
 
 def cpu_baseline(torch, synthetic, seconds):
@@ -190,6 +313,8 @@ def cpu_baseline(torch, synthetic, seconds):
         "value": round(total * n / el / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
+        "cpu_count": os.cpu_count(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"CPU ATen (the reference's CPU fallback path, via oracle.aten) running "
                    f"sum/amax/log_softmax on bf16 [{rows},32000] and mean(0) on fp32 "
@@ -550,7 +675,10 @@ def main():
     props = torch.cuda.get_device_properties(0)
     log(f"bench: device {props.name}, {props.multi_processor_count} CUs")
 
-    wall, per_op_ms = run_config2(torch, _abi, synthetic, args.steps, args.warmup)
+    import torch_gcu  # noqa: F401  (the gcu device for the dispatcher path)
+
+    wall, wall_abi, host_us, per_op_ms = run_config2(torch, _abi, synthetic, args.steps,
+                                                     args.warmup)
     ab = config2_alg_bytes()
     total_bytes = sum(ab.values())
     ms_per_step = wall * 1e3 / args.steps
@@ -575,7 +703,11 @@ def main():
         "data": "synthetic (seeded CPU generators of BASELINE config 2, copied to HBM)",
         "config": {"workload": "config2: sum/amax/log_softmax over bf16 [8192,32000] + "
                                "mean(0) over fp32 [16384,4096]",
-                   "alg_bytes_per_step": total_bytes, "per_op": per_op},
+                   "path": "torch.sum/amax/log_softmax/mean on gcu tensors (PrivateUse1 "
+                           "dispatcher -> generated wrappers -> C ABI -> gfx950 kernels)",
+                   "alg_bytes_per_step": total_bytes, "per_op": per_op,
+                   "c_abi_ms_per_step": round(wall_abi * 1e3 / args.steps, 4),
+                   "host_us_per_dispatched_op": round(host_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": committed_traffic(),
@@ -590,6 +722,11 @@ def main():
     if not args.no_cpu:
         log("bench: CPU baseline")
         line["cpu_baseline"] = cpu_baseline(torch, synthetic, args.cpu_seconds)
+        if not args.no_ops:
+            cpu_ops = cpu_config_ops(torch, synthetic)
+            for r in line["ops"]:
+                if r["op"] in cpu_ops:
+                    r["cpu_aten"] = cpu_ops[r["op"]]
     print(json.dumps(line), flush=True)
     return 0
 
