@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ops", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--section", choices=sorted(SECTIONS),
+                    help="time one group of op lines only (one JSON line per op, no headline "
+                         "step): the command a counter profile of those kernels runs")
     return ap.parse_args()
 
 
@@ -656,8 +659,36 @@ def decoder_ops(torch, steps=5):
     return out
 
 
+SECTIONS = {
+    "gemm": lambda torch, _abi: gemm_ops(torch, _abi),
+    "attention": lambda torch, _abi: attention_ops(torch, _abi),
+    "transfer": lambda torch, _abi: transfer_ops(torch, _abi),
+    "backward": lambda torch, _abi: backward_ops(torch, _abi),
+    "decoder": lambda torch, _abi: decoder_ops(torch),
+}
+
+
+def run_section(name):
+    import torch
+
+    from torch_gcu import _abi
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.cuda.init()
+    _abi.install_workspace()
+    import torch_gcu  # noqa: F401
+
+    for r in SECTIONS[name](torch, _abi):
+        print(json.dumps(r), flush=True)
+    return 0
+
+
 def main():
     args = parse()
+    if args.section:
+        return run_section(args.section)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every GPU box "
               "in this setup has one MI355X.  Run with --gpus 1.", file=sys.stderr)

@@ -384,17 +384,26 @@ __device__ __forceinline__ int dl_swz64(int r, int c) { return c ^ (((r >> 1) & 
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-// 8 int8 (two words) -> 8 x bf16 / f16, exact
+// 8 int8 (two words) -> 8 x bf16 / f16, exact. One sign-extending byte
+// convert per value (v_cvt_f32_i32 with a byte select), then two values per
+// word: the upper halves of the two floats for bf16 (exact, an int8 has at
+// most 8 significant bits), a round-toward-zero pack for f16 (exact too).
+// 12 VALU per 8 values; a (__bf16) cast of the float costs twice that.
 template <typename T>
 __device__ __forceinline__ typename MfmaOp<T>::vec widen8(u32x2_t w) {
-  typename MfmaOp<T>::vec v;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 r;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float f = (float)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
-    if constexpr (std::is_same<T, BF16>::value) v[e] = (__bf16)f;
-    else v[e] = (_Float16)f;
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t d = w[p >> 1];
+    const float lo = (float)(int)(int8_t)(d >> (16 * (p & 1)));
+    const float hi = (float)(int)(int8_t)(d >> (16 * (p & 1) + 8));
+    if constexpr (std::is_same<T, BF16>::value)
+      r[p] = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+    else
+      r[p] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
   }
-  return v;
+  return __builtin_bit_cast(typename MfmaOp<T>::vec, r);
 }
 
 template <typename T, bool HAS_BIAS, bool B_INT8>
@@ -810,13 +819,17 @@ mi_status_t launch_skinny(const GemmArgs& q, hipStream_t s) {
 // contiguous runs; a wave load spread over 16 rows, as the MFMA operand
 // layout would ask for, streams at about two thirds of the rate), into a
 // ring of two slabs; the slab's x fragments are loaded into registers right
-// after it.  Wave w multiplies k-steps 4w .. 4w + 3 (32 k each) of every
-// slab: 8-byte fragment reads from LDS (row pitch 1056 B, so the 16 rows of
-// a read land on different banks), widened to bf16 (exact), into
-// v_mfma_f32_16x16x32 with x as the 16-row operand.  The 8 waves' partial
-// tiles are added in a fixed order through LDS; the epilogue applies the
-// per-column scale and bias and rounds once.
-constexpr int kStRows = 32, kStSlab = 1024, kStPitch = kStSlab + 32, kStWaves = 8;
+// after it.  Wave w multiplies bytes 128w .. 128w + 127 of every slab row:
+// lane (r, g) reads 16 bytes of row r at 64 kp + 16 g (kp = 0, 1), which
+// feed two v_mfma_f32_16x16x32 (8 bytes each, widened to bf16 exactly) with
+// x as the 16-row operand, x's fragments taken at the same k.  The row pitch
+// is 1040 B = 260 dwords, 4 mod 64 banks: the 16 lanes of one 16-byte read
+// pass (one g, rows 0..15) cover the 64 banks once, so reads are
+// conflict-free.  The 8 waves' partial tiles are added in a fixed order
+// through LDS; the epilogue applies the per-column scale and bias and rounds
+// once.
+constexpr int kStRows = 32, kStSlab = 1024, kStPitch = kStSlab + 16, kStWaves = 8;
+static_assert((kStPitch / 4) % 64 == 4, "slab pitch must be 4 dwords mod 64 banks");
 constexpr int kStLds = 2 * kStRows * kStPitch;
 
 template <typename T, int MT, bool HAS_BIAS>
@@ -834,11 +847,11 @@ __global__ __launch_bounds__(64 * kStWaves, MT <= 2 ? 4 : 2) void int8_stream_ke
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     wsrc[i] = (const int8_t*)p.b + min<int64_t>(n0 + 4 * wave + i, p.N - 1) * p.ldb + lane * 16;
-  // x fragment of k-step ks of slab s: row 16 mt + r, k = 1024 s + 32 (4 wave + ks) + 8 g
+  // x fragment j = 2 kp + h of slab s: row 16 mt + r, k = 1024 s + 128 wave + 64 kp + 16 g + 8 h
   const uint16_t* xrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
-    xrow[mt] = p.a + min<int64_t>(16 * mt + r, p.M - 1) * p.lda + 128 * wave + 8 * g;
+    xrow[mt] = p.a + min<int64_t>(16 * mt + r, p.M - 1) * p.lda + 128 * wave + 16 * g;
   auto issue = [&](int buf, int s) __attribute__((always_inline)) {
     char* dst = st_lds + buf * (kStRows * kStPitch) + 4 * wave * kStPitch;
 #pragma unroll
@@ -850,8 +863,8 @@ __global__ __launch_bounds__(64 * kStWaves, MT <= 2 ? 4 : 2) void int8_stream_ke
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        xf[mt][ks] = *(const vec*)(xrow[mt] + (int64_t)s * kStSlab + 32 * ks);
+      for (int j = 0; j < 4; ++j)
+        xf[mt][j] = *(const vec*)(xrow[mt] + (int64_t)s * kStSlab + 64 * (j >> 1) + 8 * (j & 1));
   };
   f32x4_t acc[MT][2];
 #pragma unroll
@@ -859,14 +872,18 @@ __global__ __launch_bounds__(64 * kStWaves, MT <= 2 ? 4 : 2) void int8_stream_ke
 #pragma unroll
     for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4_t{};
   auto compute = [&](int buf, const vec (&xf)[MT][4]) __attribute__((always_inline)) {
-    const char* wb = st_lds + buf * (kStRows * kStPitch) + r * kStPitch + 128 * wave + 8 * g;
+    const char* wb = st_lds + buf * (kStRows * kStPitch) + r * kStPitch + 128 * wave + 16 * g;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int kp = 0; kp < 2; ++kp)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const vec wk = widen8<T>(*(const u32x2_t*)(wb + t * 16 * kStPitch + 32 * ks));
+        const u32x4_t w16 = *(const u32x4_t*)(wb + t * 16 * kStPitch + 64 * kp);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][t] = Mfma16<T>::mma(xf[mt][ks], wk, acc[mt][t]);
+        for (int h = 0; h < 2; ++h) {
+          const vec wk = widen8<T>(u32x2_t{w16[2 * h], w16[2 * h + 1]});
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt][t] = Mfma16<T>::mma(xf[mt][2 * kp + h], wk, acc[mt][t]);
+        }
       }
   };
   // slab s lives in LDS buffer s % 2 and x registers xa (s even) / xb (s odd);
