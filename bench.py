@@ -413,6 +413,18 @@ def gemm_ops(torch, _abi):
 
 
 def other_ops(torch, _abi, synthetic):
+    res = config1_ops(torch, _abi, synthetic)
+    res.extend(config3_ops(torch, _abi, synthetic))
+    res.extend(gemm_ops(torch, _abi))
+    res.extend(transfer_ops(torch, _abi))
+    res.extend(attention_ops(torch, _abi))
+    res.extend(decoder_ops(torch))
+    return res
+
+
+def config1_ops(torch, _abi, synthetic):
+    """Config 1: f32 broadcast mul and scalar add [4096, 4096], int64
+    index_select of 262144 rows from a [1048576, 8] table."""
     res = []
     log("bench: config 1 ops")
     c1 = synthetic.config1()
@@ -429,6 +441,13 @@ def other_ops(torch, _abi, synthetic):
     res.append(bench_op(torch, "c1.index_select int64 [1048576,8] x 262144", tsets,
                         lambda s: _abi.index_select(s["o"], s["t"], 0, idx), 35651584))
     del tsets, table
+    return res
+
+
+def config3_ops(torch, _abi, synthetic):
+    """Config 3: RMSNorm, RoPE on q and k, SiLU-mul at the Llama-7B token
+    shapes."""
+    res = []
     log("bench: config 3 ops")
     c3 = synthetic.config3()
     x, w = c3["x"].cuda(), c3["w"].cuda()
@@ -448,10 +467,6 @@ def other_ops(torch, _abi, synthetic):
     res.append(bench_op(torch, "c3.silu_mul bf16 [16384,11008]", gs,
                         lambda s: _abi.silu_mul(s["o"], s["g"], s["u"]), 1082130432))
     del gs, gt, up, c3
-    res.extend(gemm_ops(torch, _abi))
-    res.extend(transfer_ops(torch, _abi))
-    res.extend(attention_ops(torch, _abi))
-    res.extend(decoder_ops(torch))
     return res
 
 
@@ -660,12 +675,20 @@ def decoder_ops(torch, steps=5):
 
 
 SECTIONS = {
+    "config1": lambda torch, _abi: config1_ops(torch, _abi, _synthetic()),
+    "config3": lambda torch, _abi: config3_ops(torch, _abi, _synthetic()),
     "gemm": lambda torch, _abi: gemm_ops(torch, _abi),
     "attention": lambda torch, _abi: attention_ops(torch, _abi),
     "transfer": lambda torch, _abi: transfer_ops(torch, _abi),
     "backward": lambda torch, _abi: backward_ops(torch, _abi),
     "decoder": lambda torch, _abi: decoder_ops(torch),
 }
+
+
+def _synthetic():
+    from torch_gcu.utils import synthetic
+
+    return synthetic
 
 
 def run_section(name):

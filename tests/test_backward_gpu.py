@@ -204,6 +204,30 @@ def test_layer_norm_backward_masks_and_no_rows():
     assert float(got[1].abs().sum()) == 0.0 and float(got[2].abs().sum()) == 0.0
 
 
+@pytest.mark.parametrize("rows", [64, 61])
+def test_layer_norm_backward_16bit_statistics(rows):
+    """mean / rstd in the input's 16-bit dtype (what a bf16 forward on gcu
+    stores), through the fused kernel, with a last block of fewer rows than
+    a step when rows is odd; CPU ATen given the same statistics (its bf16
+    forward stores them in bf16 too)."""
+    n = 1024
+    x = rn((rows, n), torch.bfloat16, 34, 2.0) + 0.5
+    w, b = rn((n,), torch.bfloat16, 35), rn((n,), torch.bfloat16, 36)
+    _, mean, rstd = aten.layer_norm_forward(x, [n], w, b, 1e-5)
+    mean, rstd = mean.bfloat16(), rstd.bfloat16()
+    dy = rn((rows, n), torch.bfloat16, 37)
+    want = aten.layer_norm_backward(dy, x, [n], mean, rstd, w, b, [True, False, False])
+    got = torch.ops.aten.native_layer_norm_backward(dy.to("gcu"), x.to("gcu"), [n], mean.to("gcu"),
+                                                    rstd.to("gcu"), w.to("gcu"), b.to("gcu"),
+                                                    [True, True, True])
+    assert_close(got[0].cpu(), want[0], "bf16", f"dx, bf16 statistics, {rows} rows")
+    _, rdw, rdb = npr.layer_norm_backward64(dy.float().numpy(), x.float().numpy(),
+                                            mean.double().numpy(), rstd.double().numpy(),
+                                            w.float().numpy())
+    assert_close(got[1].cpu(), torch.from_numpy(rdw).bfloat16(), "bf16", "dgamma, bf16 statistics")
+    assert_close(got[2].cpu(), torch.from_numpy(rdb).bfloat16(), "bf16", "dbeta, bf16 statistics")
+
+
 # ---- autograd end to end ---------------------------------------------------------------------
 
 def test_autograd_layer_norm_silu_log_softmax_on_gcu():

@@ -59,20 +59,23 @@ __global__ __launch_bounds__(256) void rms_norm_wave_kernel(
   if (row >= rows) return;
   const V* px = (const V*)(x + row * x_row_stride);
   const int64_t nv = H / VEC;
+  // every load of the row is issued before the first sum (a sum inside the
+  // guarded load loop makes each load wait for the one before it)
   V v[VPL];
-  float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int64_t i = lane + (int64_t)k * 64;
-    if (i < nv) {
-      v[k] = ld_stream(px + i);
+    if (i < nv) v[k] = ld_stream(px + i);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k)
+    if (lane + (int64_t)k * 64 < nv)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float f = FT<Tag>::load(v[k].s[e]);
         ss += f * f;
       }
-    }
-  }
   ss = wave_sum(ss);
   const float r = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
   V* po = (V*)(out + row * out_row_stride);
