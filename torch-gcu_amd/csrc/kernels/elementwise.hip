@@ -65,58 +65,73 @@ struct Arg2D {
   int mode;
 };
 
-// out[R, C] = op(a, b) with each input in one of the Mode layouts.
-template <typename Tag, int OP>
+// out[R, C] = op(a, b) with each input in one of the Mode layouts.  MA / MB
+// fix the layouts at compile time for the common pairs (a full operand with
+// a full, row, column or scalar one); -1 reads them from the arguments.  With
+// fixed layouts every load is unconditional (a vector past the end re-reads
+// the last one and is not stored), so the compiler waits once for all of a
+// lane's loads; a load under a branch is waited alone.
+template <typename Tag, int OP, int MA, int MB>
 __global__ __launch_bounds__(kBlock) void binary_2d_kernel(
     typename TypeOf<Tag>::storage* __restrict__ out, Arg2D<Tag> a, Arg2D<Tag> b,
     typename TypeOf<Tag>::acc alpha, int64_t rows, int64_t cols) {
   typedef typename TypeOf<Tag>::storage St;
   typedef typename TypeOf<Tag>::acc Acc;
   constexpr int VEC = 16 / sizeof(St);
+  constexpr bool FIXED = MA >= 0 && MB >= 0;
   union V {
     uint4 u;
     St s[VEC];
   };
+  const int am = MA >= 0 ? MA : a.mode, bm = MB >= 0 ? MB : b.mode;
   const int64_t vcols = cols / VEC;
   const int64_t nvec = rows * vcols;
   const int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x;
 
   Acc sa = a.imm, sb = b.imm;
-  if (a.mode == M_SCALAR && a.p) sa = TypeOf<Tag>::load(a.p[0]);
-  if (b.mode == M_SCALAR && b.p) sb = TypeOf<Tag>::load(b.p[0]);
+  if (am == M_SCALAR && a.p) sa = TypeOf<Tag>::load(a.p[0]);
+  if (bm == M_SCALAR && b.p) sb = TypeOf<Tag>::load(b.p[0]);
 
   V va[kUnroll], vb[kUnroll];
   int64_t rowv[kUnroll], colv[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t v = base + (int64_t)u * kBlock;
-    if (v < nvec) {
+    const int64_t v0 = base + (int64_t)u * kBlock;
+    if (FIXED || v0 < nvec) {
+      const int64_t v = FIXED && v0 >= nvec ? nvec - 1 : v0;
       int64_t r = 0, c = v;
-      if (rows > 1) {
+      if (rows > 1 && (am == M_ROW || bm == M_ROW || am == M_COL || bm == M_COL)) {
         r = v / vcols;
         c = v - r * vcols;
       }
       rowv[u] = r;
       colv[u] = c;
       // full operands are streamed (read once); a broadcast row stays cached
-      if (a.mode == M_FULL) va[u].u = ld_stream((const uint4*)a.p + v);
-      else if (a.mode == M_ROW) va[u].u = ((const uint4*)a.p)[c];
-      if (b.mode == M_FULL) vb[u].u = ld_stream((const uint4*)b.p + v);
-      else if (b.mode == M_ROW) vb[u].u = ((const uint4*)b.p)[c];
+      if (am == M_FULL) va[u].u = ld_stream((const uint4*)a.p + v);
+      else if (am == M_ROW) va[u].u = ((const uint4*)a.p)[c];
+      if (bm == M_FULL) vb[u].u = ld_stream((const uint4*)b.p + v);
+      else if (bm == M_ROW) vb[u].u = ((const uint4*)b.p)[c];
+    }
+  }
+  Acc cav[kUnroll], cbv[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    cav[u] = sa;
+    cbv[u] = sb;
+    if (FIXED || base + (int64_t)u * kBlock < nvec) {
+      if (am == M_COL) cav[u] = TypeOf<Tag>::load(a.p[rowv[u]]);
+      if (bm == M_COL) cbv[u] = TypeOf<Tag>::load(b.p[rowv[u]]);
     }
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t v = base + (int64_t)u * kBlock;
     if (v < nvec) {
-      Acc ca = sa, cb = sb;
-      if (a.mode == M_COL) ca = TypeOf<Tag>::load(a.p[rowv[u]]);
-      if (b.mode == M_COL) cb = TypeOf<Tag>::load(b.p[rowv[u]]);
       V o;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        const Acc x = (a.mode == M_FULL || a.mode == M_ROW) ? TypeOf<Tag>::load(va[u].s[e]) : ca;
-        const Acc y = (b.mode == M_FULL || b.mode == M_ROW) ? TypeOf<Tag>::load(vb[u].s[e]) : cb;
+        const Acc x = (am == M_FULL || am == M_ROW) ? TypeOf<Tag>::load(va[u].s[e]) : cav[u];
+        const Acc y = (bm == M_FULL || bm == M_ROW) ? TypeOf<Tag>::load(vb[u].s[e]) : cbv[u];
         o.s[e] = TypeOf<Tag>::store(apply<OP, Acc>(x, y, alpha));
       }
       st_stream((uint4*)out + v, o.u);
@@ -430,10 +445,26 @@ mi_status_t launch_2d(const Iter& it, int ia, int ib, const BinArgs& ba, hipStre
     alpha = (Acc)al;
   }
   const int64_t nvec = rows * (cols / VEC);
+  if (nvec == 0) return MI_OK;
   const unsigned grid = ceil_div_u(nvec, (int64_t)kBlock * kUnroll);
-  hipLaunchKernelGGL((binary_2d_kernel<Tag, OP>), dim3(grid < 1 ? 1 : grid), dim3(kBlock), 0,
-                     stream, (St*)it.data[0], a, b, alpha, rows, cols);
-  return check_launch("binary_2d");
+  St* o = (St*)it.data[0];
+  auto go = [&](auto ma, auto mb) -> mi_status_t {
+    hipLaunchKernelGGL((binary_2d_kernel<Tag, OP, decltype(ma)::value, decltype(mb)::value>),
+                       dim3(grid), dim3(kBlock), 0, stream, o, a, b, alpha, rows, cols);
+    return check_launch("binary_2d");
+  };
+  typedef std::integral_constant<int, M_FULL> Full;
+  typedef std::integral_constant<int, M_ROW> Row;
+  typedef std::integral_constant<int, M_COL> Col;
+  typedef std::integral_constant<int, M_SCALAR> Sc;
+  typedef std::integral_constant<int, -1> Any;
+  if (a.mode == M_FULL && b.mode == M_FULL) return go(Full(), Full());
+  if (a.mode == M_FULL && b.mode == M_ROW) return go(Full(), Row());
+  if (a.mode == M_FULL && b.mode == M_COL) return go(Full(), Col());
+  if (a.mode == M_FULL && b.mode == M_SCALAR) return go(Full(), Sc());
+  if (a.mode == M_ROW && b.mode == M_FULL) return go(Row(), Full());
+  if (a.mode == M_SCALAR && b.mode == M_FULL) return go(Sc(), Full());
+  return go(Any(), Any());
 }
 
 template <typename Tag>

@@ -51,16 +51,19 @@ __global__ __launch_bounds__(64 * kGemvRows) void gemv_rows_kernel(GemvArgs a) {
   const V* pv1 = (const V*)p1;
   const V* xv = (const V*)x;
   for (int64_t v0 = lane; v0 < nv; v0 += 64 * U) {
+    // unconditional loads (a piece past the row end re-reads the last one and
+    // is not used): under a per-piece branch each load was waited alone
     V m0[U], m1[U], w[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t v = v0 + (int64_t)u * 64;
-      if (v < nv) {
-        m0[u] = ld_stream(pv0 + v);
-        m1[u] = ld_stream(pv1 + v);
-        w[u] = xv[v];
-      }
+      const int64_t v = v0 + (int64_t)u * 64 < nv ? v0 + (int64_t)u * 64 : nv - 1;
+      m0[u] = ld_stream(pv0 + v);
+      m1[u] = ld_stream(pv1 + v);
+      w[u] = xv[v];
     }
+    // keep the scheduler from pulling the multiplies between the loads (each
+    // use of a just-issued load costs a wait for all loads before it)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (v0 + (int64_t)u * 64 < nv) {

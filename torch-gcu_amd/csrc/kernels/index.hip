@@ -34,11 +34,16 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
   const int64_t total = outer * n_idx * words_per_row;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   const bool small = total < 0x7fffffffLL;
-  int64_t tt[kGatherU], row[kGatherU], w[kGatherU], o[kGatherU], s[kGatherU];
+  // Every load is unconditional: a word past the end decodes word total - 1
+  // (not stored), and an out-of-range index reads row 0 (stored as zeros),
+  // so the compiler's waits cover all kGatherU index loads at once and then
+  // all row loads at once (with the loads under a branch each waited alone).
+  int64_t tt[kGatherU], w[kGatherU], o[kGatherU], s[kGatherU];
 #pragma unroll
   for (int u = 0; u < kGatherU; ++u) {
-    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x + u * stride;
-    tt[u] = t;
+    const int64_t t0 = (int64_t)blockIdx.x * kBlock + threadIdx.x + u * stride;
+    tt[u] = t0;
+    const int64_t t = t0 < total ? t0 : total - 1;
     int64_t rr, ww, i;
     if (log2_wpr >= 0) {
       rr = t >> log2_wpr;
@@ -58,26 +63,24 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
       o[u] = rr / n_idx;
       i = rr - o[u] * n_idx;
     }
-    row[u] = i;
     w[u] = ww;
-    s[u] = t < total ? read_index(idx, i, istride) : 0;
+    s[u] = read_index(idx, i, istride);
   }
   W v[kGatherU];
+  bool ok[kGatherU];
 #pragma unroll
   for (int u = 0; u < kGatherU; ++u) {
-    if (tt[u] < total && s[u] >= 0 && s[u] < src_rows)
-      v[u] = self[(o[u] * src_rows + s[u]) * words_per_row + w[u]];
-    else
-      v[u] = W{};
+    ok[u] = s[u] >= 0 && s[u] < src_rows;
+    v[u] = self[(o[u] * src_rows + (ok[u] ? s[u] : 0)) * words_per_row + w[u]];
   }
 #pragma unroll
   for (int u = 0; u < kGatherU; ++u) {
     if (tt[u] < total) {
-      if constexpr (sizeof(W) == 16) st_stream(out + tt[u], v[u]);
-      else out[tt[u]] = v[u];
+      const W r = ok[u] ? v[u] : W{};
+      if constexpr (sizeof(W) == 16) st_stream(out + tt[u], r);
+      else out[tt[u]] = r;
     }
   }
-  (void)row;
 }
 
 // General layout: iterate over out elements; coordinates decoded per element.
@@ -126,6 +129,10 @@ mi_status_t launch_rows(const mi_tensor_t* out, const mi_tensor_t* self, const I
                         int64_t istride, int64_t outer, int64_t n_idx, int64_t src_rows,
                         int64_t row_bytes, hipStream_t stream) {
   const uintptr_t align = (uintptr_t)out->data | (uintptr_t)self->data;
+  if (outer * n_idx * row_bytes == 0) return MI_OK;
+  // no source rows: every index is out of range, and the kernel's loads of
+  // row 0 would have nothing to read
+  if (src_rows == 0) return mi_fill(out, mi_scalar_t{0.0, 0, MI_F32, 1}, (mi_stream_t)stream);
   auto go = [&](auto word) -> mi_status_t {
     typedef decltype(word) W;
     const int64_t wpr = row_bytes / (int64_t)sizeof(W);
