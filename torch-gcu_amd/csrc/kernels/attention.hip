@@ -6,10 +6,11 @@
 // (key j is visible to query i when j <= i), as torch's is_causal.
 //
 // A 256-lane block owns 128 query rows (32 per wave) of one (b, h) and walks
-// the keys in tiles of 64, with two LDS stages so the global loads of tile
-// i+1 overlap the MFMAs of tile i (one barrier per tile):
-//   1. K rows go to LDS as [key][d]; V rows as [d][key], transposed on the
-//      way in four keys at a time (one 8-byte LDS store per 4 keys x 1 d);
+// the keys in tiles of 64, with two LDS stages so the copies of tile i+1
+// overlap the MFMAs of tile i (one barrier per tile):
+//   1. K and V rows go to LDS as [key][d] by global_load_lds (no registers,
+//      no LDS stores), each row's 16-byte chunks XOR-swizzled by key so the
+//      fragment reads below are free of bank conflicts;
 //   2. each wave computes the transposed scores S^T = K Q^T (32 keys x its 32
 //      queries per MFMA tile, v_mfma_f32_32x32x16): Q stays in registers as
 //      the B operand for the whole block, so lane l owns query l % 32 and
@@ -22,8 +23,10 @@
 //      FMA per score);
 //   4. P, rounded to the input type, is already laid out as the B operand of
 //      O^T += V^T P^T (keys are fed to the MFMA's k dimension in a permuted
-//      order that matches the S^T accumulator layout, and V^T is read in the
-//      same order), so P never goes through LDS.
+//      order that matches the S^T accumulator layout), so P never goes
+//      through LDS; the V^T operand comes from V [key][d] by
+//      ds_read_b64_tr_b16, which hands each lane one d for 4 consecutive
+//      keys.
 // Key tiles above a wave's causal diagonal are skipped.  Blocks are ordered
 // head-major with the longest query tiles first, and renumbered so each of
 // the 8 XCDs (which receive workgroups round robin) walks a contiguous run of
@@ -85,23 +88,29 @@ constexpr int QT = 128;  // query rows per block
 constexpr int KT = 64;   // keys per tile
 constexpr int NT = 256;
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// LDS stage: K tile [KT keys][D] then V tile [KT keys][D], rows unpadded,
+// both filled by global_load_lds (each lane's 16-byte chunk goes to LDS at
+// lane * 16 of a 1 KiB wave copy, so the chunk order inside a row is chosen
+// by which global chunk a lane fetches).  Chunk c of key row r sits at
+// position c ^ swz(r):
+//   K (read as 16-byte MFMA fragments, 16 rows per pass): swz_k spreads one
+//     chunk of 16 consecutive rows over all 64 banks;
+//   V (read by ds_read_b64_tr_b16, a pass covering 4 consecutive rows x 4
+//     chunks): swz_v puts those 16 chunks on distinct banks.
 template <int D>
 struct FlashCfg {
-  static constexpr int KP = D + 8;                // K pitch ([key][d]), 16 B pad
-  static constexpr int VP = KT + 4;               // V^T pitch ([d][key]), 8 B pad
-  static constexpr int KS = KT * KP;              // elements of one K stage
-  static constexpr int STAGE = KS + D * VP;       // K + V^T
-  static constexpr int KCH = KT * D / 8 / NT;     // 16-byte K chunks per lane
-  static constexpr int VGR = (KT / 4) * (D / 8);  // (4 keys x 8 d) V groups
-  static size_t lds() { return (size_t)2 * STAGE * sizeof(uint16_t); }
+  static constexpr int CPR = D / 8;     // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;  // rows per 1 KiB wave copy
+  static constexpr int NINS = KT / RPI; // wave copies per K (or V) tile
+  static constexpr int TILE = KT * D;   // elements of one K (or V) tile
+  static constexpr int STAGE = 2 * TILE;
+  static __device__ __forceinline__ int swz_k(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+  static __device__ __forceinline__ int swz_v(int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+  static_assert(NINS % 4 == 0, "four waves share a tile's copies");
 };
-
-__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
-  return (a & 0xffffu) | (b << 16);
-}
-__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
-  return (a >> 16) | (b & 0xffff0000u);
-}
 
 template <typename T, int D>
 __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
@@ -109,7 +118,12 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   typedef FlashCfg<D> C;
   constexpr int DF = D / 16;  // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;  // 32-row d tiles of O^T
-  extern __shared__ __align__(16) uint16_t smem[];
+  // two stages as separate arrays: with the loop unrolled by two, each
+  // half-iteration reads one and copies into the other, so the compiler can
+  // tell the next tile's copies from this tile's fragment reads (through one
+  // array it made every transposed read wait for the copies in flight)
+  __shared__ __align__(16) uint16_t stage0[C::STAGE];
+  __shared__ __align__(16) uint16_t stage1[C::STAGE];
 
   // block -> (b, h, query tile); head-major, longest query tile first
   int bid = (int)blockIdx.x;
@@ -136,54 +150,46 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
     for (int t = 0; t < DF; ++t) qf[t] = *(const vec*)(Q + r * p.q_ss + 16 * t + 8 * half);
   }
 
-  // ---- K / V staging: global -> registers -> LDS ----
+  // ---- K / V: global -> LDS by wave copies (no registers, no ds_write) ----
   // Per-lane element offsets are 32-bit (the host checked Sk * stride fits);
-  // a tile adds kv0 * stride, and only the last tile clamps its rows.
-  u32x4 kr[C::KCH];
-  u32x4 vr0, vr1, vr2, vr3;
-  const bool v_lane = C::VGR >= NT || (int)threadIdx.x < C::VGR;
-  const int vkg = threadIdx.x & 15, vdc = (threadIdx.x >> 4) * 8;
+  // keys past the end of the last tile re-read the last key (masked later).
   const int k_ss = (int)p.k_ss, v_ss = (int)p.v_ss, Sk = (int)p.Sk;
-  auto load_kv = [&](int kv0) __attribute__((always_inline)) {
-    const bool full = kv0 + KT <= Sk;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  auto issue_kv = [&](int kv0, uint16_t* ks) __attribute__((always_inline)) {
+    uint16_t* vs = ks + C::TILE;
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int c = threadIdx.x + i * NT;
-      const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
-      const int gk = full ? kv0 + key : min(kv0 + key, Sk - 1);
-      kr[i] = *(const u32x4*)(K + gk * k_ss + dc);
-    }
-    if (v_lane) {
-      const int g0 = kv0 + 4 * vkg;
-      const int r0 = full ? g0 : min(g0, Sk - 1), r1 = full ? g0 + 1 : min(g0 + 1, Sk - 1);
-      const int r2 = full ? g0 + 2 : min(g0 + 2, Sk - 1), r3 = full ? g0 + 3 : min(g0 + 3, Sk - 1);
-      vr0 = *(const u32x4*)(V + r0 * v_ss + vdc);
-      vr1 = *(const u32x4*)(V + r1 * v_ss + vdc);
-      vr2 = *(const u32x4*)(V + r2 * v_ss + vdc);
-      vr3 = *(const u32x4*)(V + r3 * v_ss + vdc);
+    for (int i = 0; i < C::NINS / 4; ++i) {
+      const int q = wv * (C::NINS / 4) + i;
+      const int key = q * C::RPI + lane / C::CPR, cp = lane % C::CPR;
+      const int gk = min(kv0 + key, Sk - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(K + gk * k_ss + 8 * (cp ^ C::swz_k(key))),
+                                       (lds_void_t*)(ks + q * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(V + gk * v_ss + 8 * (cp ^ C::swz_v(key))),
+                                       (lds_void_t*)(vs + q * 512), 16, 0, 0);
     }
   };
-  auto store_kv = [&](int stage) __attribute__((always_inline)) {
-    uint16_t* ks = smem + stage * C::STAGE;
-    uint16_t* vt = ks + C::KS;
+  // K fragment k-step t of sub-tile st: key 32 st + col, chunk 2 t + half
+  // (swz_k(32 + col) == swz_k(col))
+  int koff[DF];
+  {
+    const int sk = C::swz_k(col);
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int c = threadIdx.x + i * NT;
-      const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
-      *(u32x4*)(ks + key * C::KP + dc) = kr[i];
-    }
-    if (v_lane) {
+    for (int t = 0; t < DF; ++t) koff[t] = col * D + 8 * ((2 * t + half) ^ sk);
+  }
+  // V^T fragment (k-step t, d tile dt) by two transposed reads: in each 16-lane
+  // group G, lane j names row key 16 t + 4 (G / 2) + j / 4 (then + 8), columns
+  // d0 = 32 dt + 16 (G % 2) + 4 (j % 4) .. + 3, and receives d = 32 dt +
+  // 16 (G % 2) + j for 4 consecutive keys: the A operand of O^T += V^T P^T
+  // for keys 16 t + 4 half + 0..3 and 16 t + 8 + 4 half + 0..3
+  int voff[DT];
+  {
+    const int G = lane >> 4, j = lane & 15;
+    const int key = 4 * (G >> 1) + (j >> 2);  // plus 16 t
+    const int sv = C::swz_v(key) >> 2;        // swz_v(key + 16 t) == swz_v(key)
+    const int low = 2 * (G & 1) + ((j & 3) >> 1), within = 4 * (j & 1);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int j = e >> 1;
-        const uint32_t a0 = vr0[j], a1 = vr1[j], a2 = vr2[j], a3 = vr3[j];
-        u32x2 w;
-        w[0] = (e & 1) ? hi_pair(a0, a1) : lo_pair(a0, a1);
-        w[1] = (e & 1) ? hi_pair(a2, a3) : lo_pair(a2, a3);
-        *(u32x2*)(vt + (vdc + e) * C::VP + 4 * vkg) = w;
-      }
-    }
-  };
+    for (int dt = 0; dt < DT; ++dt) voff[dt] = key * D + 8 * (4 * (dt ^ sv) + low) + within;
+  }
 
   f32x16 o[DT];
 #pragma unroll
@@ -193,34 +199,31 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   const int kv_end = (int)(p.causal ? min(p.Sk, q0 + QT) : p.Sk);
   const int n_tiles = (kv_end + KT - 1) / KT;
   const int wq = (int)wq0, qr = (int)qrow;
-  load_kv(0);
-  store_kv(0);
+  issue_kv(0, stage0);
   // the Q fragments and the first tile have landed: inside the loop the only
-  // outstanding global loads are the next tile's K / V
+  // outstanding global loads are the next tile's K / V copies
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int it = 0; it < n_tiles; ++it) {
+  auto tile = [&](int it, const uint16_t* ks, uint16_t* next) __attribute__((always_inline)) {
     const int kv0 = it * KT;
     const bool more = it + 1 < n_tiles;
-    if (more) load_kv(kv0 + KT);
+    if (more) issue_kv(kv0 + KT, next);
     __builtin_amdgcn_sched_barrier(0);
-    const uint16_t* ks = smem + (it & 1) * C::STAGE;
-    const uint16_t* vt = ks + C::KS;
+    const uint16_t* vs = ks + C::TILE;
     if (!p.causal || kv0 <= wq + 31) {
       // ---- S^T = K Q^T: two 32-key tiles x this wave's 32 queries, the two
       // accumulator chains interleaved ----
       f32x16 s[2] = {f32x16{}, f32x16{}};
-      const uint16_t* kb0 = ks + col * C::KP + 8 * half;
-      const uint16_t* kb1 = kb0 + 32 * C::KP;
+      const uint16_t* kb1 = ks + 32 * D;
       // K fragments double-buffered one k-step ahead of their MFMAs
       vec kf[2][2];
-      kf[0][0] = *(const vec*)kb0;
-      kf[0][1] = *(const vec*)kb1;
+      kf[0][0] = *(const vec*)(ks + koff[0]);
+      kf[0][1] = *(const vec*)(kb1 + koff[0]);
 #pragma unroll
       for (int t = 0; t < DF; ++t) {
         if (t + 1 < DF) {
-          kf[(t + 1) & 1][0] = *(const vec*)(kb0 + 16 * (t + 1));
-          kf[(t + 1) & 1][1] = *(const vec*)(kb1 + 16 * (t + 1));
+          kf[(t + 1) & 1][0] = *(const vec*)(ks + koff[t + 1]);
+          kf[(t + 1) & 1][1] = *(const vec*)(kb1 + koff[t + 1]);
         }
         __builtin_amdgcn_sched_barrier(0);
         s[0] = AttnOp<T>::mma(kf[t & 1][0], qf[t], s[0]);
@@ -294,10 +297,12 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
       auto read_v = [&](int t, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
-          const uint16_t* vb = vt + (d * 32 + col) * C::VP + 16 * t + 4 * half;
-          const u32x2 a0 = *(const u32x2*)vb, a1 = *(const u32x2*)(vb + 8);
-          const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
-          vf[buf][d] = __builtin_bit_cast(vec, a);
+          typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+          const uint16_t* vb = vs + 16 * t * D + voff[d];
+          const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)vb);
+          const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 8 * D));
+          const s16x4 lo = a0, hi = a1;
+          vf[buf][d] = __builtin_bit_cast(vec, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
       };
       read_v(0, 0);
@@ -310,8 +315,14 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (more) store_kv((it + 1) & 1);
+    // this wave's copies of the next tile have landed; the barrier publishes
+    // every wave's and retires this tile's stage for the copy after next
+    if (more) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  };
+  for (int it = 0; it < n_tiles; it += 2) {
+    tile(it, stage0, stage1);
+    if (it + 1 < n_tiles) tile(it + 1, stage1, stage0);
   }
 
   // ---- normalise and store: accumulator r of d tile dt is
@@ -341,14 +352,7 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
 
 template <typename T, int D>
 mi_status_t launch_flash(const AttnArgs& a, hipStream_t s) {
-  static bool attr = [] {
-    (void)hipFuncSetAttribute((const void*)flash_fwd_kernel<T, D>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)FlashCfg<D>::lds());
-    return true;
-  }();
-  (void)attr;
-  hipLaunchKernelGGL((flash_fwd_kernel<T, D>), dim3((unsigned)a.n_blocks), dim3(NT),
-                     FlashCfg<D>::lds(), s, a);
+  hipLaunchKernelGGL((flash_fwd_kernel<T, D>), dim3((unsigned)a.n_blocks), dim3(NT), 0, s, a);
   return check_launch("flash_attention_fwd");
 }
 
