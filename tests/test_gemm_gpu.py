@@ -244,6 +244,44 @@ def test_int8_linear_large_tile_path(dtype, bias):
     assert_close(out, aten.int8_linear(x, w, scales, b), "bf16", f"int8 large tile {dtype} {bias}")
 
 
+@pytest.mark.parametrize("M,N,K,dtype,bias", [
+    (256, 1000, 1024, torch.bfloat16, None),     # 2 x rows, ragged last W panel
+    (200, 777, 64, torch.bfloat16, "bf16"),      # one K step, ragged x tile, odd N
+    (512, 4104, 512, torch.float16, "f32"),      # 4 x tiles, fp32 bias
+    (65, 96, 128, torch.bfloat16, "row"),        # smallest M of the path, [M, N] bias
+])
+def test_int8_linear_mid_path(M, N, K, dtype, bias):
+    """64 < M <= 512: 128-row x tiles against W panels sized so the blocks
+    about fill the CUs (config 4's M = 256 runs here)."""
+    x, w, scales = int8_inputs(M, N=N, K=K, seed=100 + M)
+    x = x.to(dtype)
+    b = None
+    if bias == "bf16":
+        b = torch.randn(N, generator=g(101)).to(torch.bfloat16)
+    elif bias == "f32":
+        b = torch.randn(N, generator=g(102))
+    elif bias == "row":
+        b = torch.randn(M, N, generator=g(103)).to(dtype)
+    out = torch.empty(M, N, dtype=dtype, device="cuda")
+    _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda(), None if b is None else b.cuda())
+    assert_close(out, aten.int8_linear(x, w, scales, b), "bf16", f"int8 mid {M},{N},{K} {dtype} {bias}")
+
+
+@pytest.mark.parametrize("dtype,bias", [(torch.float16, "f32"), (torch.float16, None),
+                                        (torch.bfloat16, "f32")])
+def test_int8_linear_register_staged_path(dtype, bias):
+    """M > 512 with fewer 256 x 256 tiles than CUs: 128 x 64 tiles whose int8
+    W rows are widened to the type of x on the way into LDS (an f16 x used to
+    get bf16 bit patterns there)."""
+    M, N, K = 1024, 4104, 512
+    x, w, scales = int8_inputs(M, N=N, K=K, seed=110)
+    x = x.to(dtype)
+    b = torch.randn(N, generator=g(111)) if bias == "f32" else None
+    out = torch.empty(M, N, dtype=dtype, device="cuda")
+    _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda(), None if b is None else b.cuda())
+    assert_close(out, aten.int8_linear(x, w, scales, b), "bf16", f"int8 staged {dtype} {bias}")
+
+
 # ---- addmv (GEMV) and the linear / matmul override ---------------------------------
 
 def _kind(dtype):

@@ -90,6 +90,31 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* 
   *tn = in_group / gsize;
 }
 
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// 8 int8 (two words) -> 8 x bf16 / f16, exact. One sign-extending byte
+// convert per value (v_cvt_f32_i32 with a byte select), then two values per
+// word: the upper halves of the two floats for bf16 (exact, an int8 has at
+// most 8 significant bits), a round-toward-zero pack for f16 (exact too).
+// 12 VALU per 8 values; a (__bf16) cast of the float costs twice that.
+template <typename T>
+__device__ __forceinline__ typename MfmaOp<T>::vec widen8(u32x2_t w) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t d = w[p >> 1];
+    const float lo = (float)(int)(int8_t)(d >> (16 * (p & 1)));
+    const float hi = (float)(int)(int8_t)(d >> (16 * (p & 1) + 8));
+    if constexpr (std::is_same<T, BF16>::value)
+      r[p] = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+    else
+      r[p] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+  }
+  return __builtin_bit_cast(typename MfmaOp<T>::vec, r);
+}
+
+
 // Per-lane loader of a ROWS x 64 tile of a K-contiguous 16-bit matrix: V
 // 16-byte vectors per lane, 8 lanes per 128-byte row segment; vector i of a
 // lane covers tile row row0 + i * (NT / 8).  Rows past the end of the matrix
@@ -142,8 +167,8 @@ struct Tile16 {
 };
 
 // int8 rows: ROWS x 64 bytes = ROWS*4 vectors of 16 values per tile, widened
-// to bf16 when written to LDS (same clamping and tail rules).
-template <int ROWS, int NT>
+// to T (bf16 or f16, exact) when written to LDS (same clamping and tail rules).
+template <typename T, int ROWS, int NT>
 struct Tile8 {
   static constexpr int V = ROWS * 4 / NT;
   static constexpr int RS = NT / 4;
@@ -189,14 +214,9 @@ struct Tile8 {
         int8_t b[16];
       } in;
       in.u = r[i];
-      union {
-        uint4 u[2];
-        uint16_t h[16];
-      } out;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) out.h[e] = (uint16_t)(__float_as_uint((float)in.b[e]) >> 16);
-      *(uint4*)(d + i * RS * PITCH) = out.u[0];
-      *(uint4*)(d + i * RS * PITCH + 8) = out.u[1];
+      typedef typename MfmaOp<T>::vec vec;
+      *(vec*)(d + i * RS * PITCH) = widen8<T>(u32x2_t{in.u.x, in.u.y});
+      *(vec*)(d + i * RS * PITCH + 8) = widen8<T>(u32x2_t{in.u.z, in.u.w});
     }
   }
 };
@@ -228,7 +248,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_mfma_kernel(GemmArgs p) 
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
 
   Tile16<BM, NT> ta;
-  typename std::conditional<B_INT8, Tile8<BN, NT>, Tile16<BN, NT>>::type tb;
+  typename std::conditional<B_INT8, Tile8<T, BN, NT>, Tile16<BN, NT>>::type tb;
   ta.init(p.a + batch * p.sa, p.lda, p.M, m0);
   if constexpr (B_INT8)
     tb.init((const int8_t*)p.b + batch * p.sb, p.ldb, p.N, n0);
@@ -377,34 +397,24 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// waits until at most `later` steps' loads (LPW per step) are outstanding
+template <int MAXL, int LPW>
+__device__ __forceinline__ void wait_later(int later) {
+  if constexpr (MAXL > 0) {
+    if (later >= MAXL) {
+      wait_vmcnt<MAXL * LPW>();
+      return;
+    }
+    wait_later<MAXL - 1, LPW>(later);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
 __device__ __forceinline__ int dl_swz(int r, int c) { return c ^ ((r & 7) ^ ((r >> 3) & 1)); }
 // 64-byte rows: chunk c of row r at c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1), conflict-free for
 // 16-byte reads of 16 consecutive rows under 32- or 64-bank LDS
 __device__ __forceinline__ int dl_swz64(int r, int c) { return c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1)); }
-
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-
-// 8 int8 (two words) -> 8 x bf16 / f16, exact. One sign-extending byte
-// convert per value (v_cvt_f32_i32 with a byte select), then two values per
-// word: the upper halves of the two floats for bf16 (exact, an int8 has at
-// most 8 significant bits), a round-toward-zero pack for f16 (exact too).
-// 12 VALU per 8 values; a (__bf16) cast of the float costs twice that.
-template <typename T>
-__device__ __forceinline__ typename MfmaOp<T>::vec widen8(u32x2_t w) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const uint32_t d = w[p >> 1];
-    const float lo = (float)(int)(int8_t)(d >> (16 * (p & 1)));
-    const float hi = (float)(int)(int8_t)(d >> (16 * (p & 1) + 8));
-    if constexpr (std::is_same<T, BF16>::value)
-      r[p] = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-    else
-      r[p] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-  }
-  return __builtin_bit_cast(typename MfmaOp<T>::vec, r);
-}
 
 template <typename T, bool HAS_BIAS, bool B_INT8>
 __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
@@ -639,6 +649,253 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
       }
     }
   }
+}
+
+// ---- int8 weight-only linear, mid-size M (64 < M <= 512): 128 x R tiles -------------
+//
+// Config 4's M = 256 against W [11008, 4096] has 2 x 11008 / 256 = 86 W rows
+// per CU: 128 x 256 tiles give 86 blocks, 128 x 64 tiles 344 (1.34 waves).
+// Here a 256-lane block owns 128 rows of x (32 per wave) and R W rows, R a
+// multiple of 8 up to 96 chosen so that the blocks about fill the CUs (R = 88
+// for config 4: 252 blocks).  K steps of 64 flow through four LDS stages
+// filled by global_load_lds (three steps in flight while one is multiplied:
+// one block per CU has no other block to cover the latency): x rows as bf16
+// (128-byte rows, chunk swizzle dl_swz), W rows as int8 (64-byte rows,
+// dl_swz64), which waves 0..2 widen, 32 rows each, into one of two bf16
+// copies (dl_swz) once their own copies of the next step have landed.
+// (Measured on config 4's M = 256: 49 us, against 54-56 us for the 128 x 64
+// register-staged tiles; two stages 53 us; widening spread over all four
+// waves, or two steps ahead through a third copy with five stages, 53-58 us.
+// The kernel stays far from its 11.7 us MFMA time: per K step its four waves
+// stall on the barrier, the widening and the fragment reads in turn.)
+// Each wave multiplies its 32 x rows with three 32-row W fragments
+// (v_mfma_f32_32x32x16, W as the A operand, so a lane owns one output row and
+// runs of 4 columns); the epilogue applies alpha, the per-column scale and
+// the bias, rounds once and stores through LDS.
+// cache policy operand of global_load_lds on gfx950: non-temporal (NT = bit 1)
+constexpr int kCpolNT = 2;
+
+namespace mid {
+constexpr int BM = 128, BNF = 96, KB = 64, NT = 256, NW = 4;
+constexpr int STAGES = 4;                     // copies in flight: steps kt + 1 .. kt + 3
+constexpr int COPIES = 2;                     // bf16 W copies (steps kt, kt + 1)
+constexpr int FN = BNF / 32;                  // W fragments per wave
+constexpr int TA = BM * KB;                   // x tile, 16-bit elements
+constexpr int TB8 = BNF * KB / 2;             // int8 W tile, in 16-bit units
+constexpr int TB = BNF * KB;                  // bf16 copy of the W tile
+constexpr int STAGE = TA + TB8;               // the part global_load_lds fills
+constexpr int NQA = BM * KB * 2 / 1024 / NW;  // x copies per wave (4)
+constexpr int NQB = 2;                        // W copies per wave 0..2 (16 rows each)
+constexpr int KS = KB / 16;
+constexpr int EP = BNF + 8;                   // epilogue row pitch
+constexpr size_t LDS = ((size_t)STAGES * STAGE + (size_t)COPIES * TB) * 2;
+static_assert(LDS >= (size_t)NW * 32 * EP * 2, "epilogue staging fits");
+static_assert(LDS <= 160 * 1024, "one block's LDS");
+}  // namespace mid
+
+template <typename T, bool HAS_BIAS>
+__global__ __launch_bounds__(mid::NT, 1) void int8_mid_kernel(GemmArgs p, int R) {
+  using namespace mid;
+  typedef typename MfmaOp<T>::vec vec;
+  extern __shared__ __align__(16) uint16_t smem[];
+  // XCD-aware order (round-robin dispatch over 8 XCDs): consecutive logical
+  // blocks, the m tiles of one W panel first, run on one XCD and share the
+  // panel through its L2
+  int id = blockIdx.x;
+  {
+    const int total = p.tiles_m * p.tiles_n;
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+  }
+  const int tm = id % p.tiles_m, tn = id / p.tiles_m;
+  const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
+  const int m0 = tm * BM, n0 = tn * R;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool w_rows = wave < BNF / 32;  // waves copying and widening W rows
+  const char* Bbase = (const char*)p.b;
+
+  // per-lane byte offsets (the host checked they fit 32 bits); rows past the
+  // matrix are clamped to its last row and only feed outputs never stored
+  uint32_t ao[NQA], bo[NQB];
+#pragma unroll
+  for (int q = 0; q < NQA; ++q) {
+    const int row = (wave * NQA + q) * 8 + lane / 8;
+    ao[q] = (uint32_t)(((int64_t)min(m0 + row, M - 1) * p.lda + dl_swz(row, lane % 8) * 8) * 2);
+  }
+#pragma unroll
+  for (int q = 0; q < NQB; ++q) {
+    const int row = (wave * NQB + q) * 16 + lane / 4;
+    bo[q] = (uint32_t)((int64_t)min(n0 + row, N - 1) * p.ldb + dl_swz64(row, lane % 4) * 16);
+  }
+  auto issue = [&](int st, int k0) __attribute__((always_inline)) {
+    uint16_t* as = smem + st * STAGE;
+    uint16_t* bs = as + TA;
+    const char* Ab = (const char*)(p.a + k0);
+    const char* Bb = Bbase + k0;
+#pragma unroll
+    for (int q = 0; q < NQA; ++q)
+      __builtin_amdgcn_global_load_lds((const void*)(Ab + ao[q]),
+                                       (lds_void_t*)(as + (wave * NQA + q) * 512), 16, 0, 0);
+    if (w_rows) {
+      // W is streamed once (non-temporal: it should not push x out of L2)
+#pragma unroll
+      for (int q = 0; q < NQB; ++q)
+        __builtin_amdgcn_global_load_lds((const void*)(Bb + bo[q]),
+                                         (lds_void_t*)(bs + (wave * NQB + q) * 512), 16, 0, kCpolNT);
+    }
+  };
+  // wave w < 3 copied W rows 32 w .. 32 w + 31 of every stage itself and
+  // widens exactly those rows into a bf16 copy; lane: row 32 w + l / 2, k half l % 2
+  auto convert = [&](int st, int cb) __attribute__((always_inline)) {
+    if (w_rows) {
+      const char* b8 = (const char*)(smem + st * STAGE + TA);
+      uint16_t* bb = smem + STAGES * STAGE + cb * TB;
+      const int r = wave * 32 + (lane >> 1), h = lane & 1;
+      const u32x4_t c0 = *(const u32x4_t*)(b8 + r * 64 + dl_swz64(r, 2 * h) * 16);
+      const u32x4_t c1 = *(const u32x4_t*)(b8 + r * 64 + dl_swz64(r, 2 * h + 1) * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4_t& c = j < 2 ? c0 : c1;
+        const u32x2_t w = {c[2 * (j & 1)], c[2 * (j & 1) + 1]};
+        *(vec*)(bb + r * KB + dl_swz(r, 4 * h + j) * 8) = widen8<T>(w);
+      }
+    }
+  };
+  // fragment read offsets: lane supplies row l % 32, k chunk 2 s + l / 32
+  int roff[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) roff[s] = (lane & 31) * KB + dl_swz(lane & 31, 2 * s + (lane >> 5)) * 8;
+
+  f32x16 acc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) acc[j] = f32x16{};
+  vec af[2], bfr[2][FN];
+  auto read_frags = [&](int st, int cb, int s, int buf) __attribute__((always_inline)) {
+    af[buf] = *(const vec*)(smem + st * STAGE + wave * 32 * KB + roff[s]);
+    const uint16_t* bs = smem + STAGES * STAGE + cb * TB + roff[s];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * 32 * KB);
+  };
+  auto mfmas = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[j] = MfmaOp<T>::mma(bfr[buf][j], af[buf], acc[j]);
+  };
+  const int KT = K / KB;
+  // this wave's copies of a step: the wait until step kt + 1 has landed
+  // while `later` newer steps stay in flight
+  auto wait_step = [&](int later) __attribute__((always_inline)) {
+    if (w_rows) wait_later<STAGES - 1, NQA + NQB>(later);
+    else wait_later<STAGES - 1, NQA>(later);
+  };
+  // One K step kt: x from stage kt % STAGES, W from bf16 copy kt % 2.  At
+  // its last K substep step kt + 1 is waited for (steps kt + 2 .. kt +
+  // STAGES - 1 stay in flight), widened, published by the barrier (which
+  // also retires stage kt % STAGES, refilled with step kt + STAGES) and its
+  // first fragments read.
+  auto step = [&](int kt) __attribute__((always_inline)) {
+    const int st = kt % STAGES, cb = kt & 1;
+    const int st1 = (kt + 1) % STAGES, cb1 = cb ^ 1;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int buf = s & 1;
+      if (s + 1 < KS) {
+        read_frags(st, cb, s + 1, buf ^ 1);
+        mfmas(buf);
+        // MFMA, two fragment reads, then MFMA and one read each
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int k = 1; k < FN; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      } else {
+        if (kt + 1 < KT) {
+          wait_step(min(STAGES - 2, KT - 2 - kt));
+          convert(st1, cb1);
+          __syncthreads();
+          if (kt + STAGES < KT) issue(st, (kt + STAGES) * KB);
+          read_frags(st1, cb1, 0, buf ^ 1);
+        }
+        mfmas(buf);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+    if (s < KT) issue(s, s * KB);
+  // step 0 has landed once only steps 1 .. STAGES - 1 (those that exist) are in flight
+  wait_step(min(STAGES, KT) - 1);
+  convert(0, 0);
+  __syncthreads();
+  read_frags(0, 0, 0, 0);
+  for (int kt = 0; kt < KT; ++kt) step(kt);
+
+  // epilogue: out = alpha * scale[n] * acc + beta * bias, one rounding,
+  // staged per wave as [32 x rows][96 W rows] and stored in 16-byte pieces
+  __syncthreads();
+  uint16_t* es = smem + wave * 32 * EP;
+  const float alpha = p.alpha, beta = p.beta;
+  const bool bias_f32 = p.bias_dtype == MI_F32;
+  const int ml = lane & 31;
+  const int64_t m = m0 + wave * 32 + ml;
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
+      u16x4_t v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t n = min<int64_t>(n0 + nl + e, p.N - 1);
+        float x = alpha * acc[j][4 * g + e] * p.scale[n];
+        if (HAS_BIAS) {
+          const int64_t bo_ = min<int64_t>(m, p.M - 1) * p.bias_sm + n * p.bias_sn;
+          x += beta * (bias_f32 ? ((const float*)p.bias)[bo_]
+                                : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo_]));
+        }
+        v[e] = MfmaOp<T>::store(x);
+      }
+      *(u16x4_t*)(es + ml * EP + nl) = v;
+    }
+  // the block's columns: n0 .. n0 + R - 1 (fewer in the last tile)
+  const int ncols = min(R, N - n0);
+  const bool vec_ok = (p.ldc % 8) == 0 && (((uintptr_t)p.c) & 15) == 0 && (n0 % 8) == 0;
+  for (int idx = lane; idx < 32 * (BNF / 8); idx += 64) {
+    const int r = idx / (BNF / 8), c = (idx % (BNF / 8)) * 8;
+    const int64_t mr = m0 + wave * 32 + r;
+    if (mr >= p.M || c >= ncols) continue;
+    const uint4 v = *(const uint4*)(es + r * EP + c);
+    uint16_t* dst = p.c + mr * p.ldc + n0 + c;
+    if (vec_ok && c + 8 <= ncols) {
+      *(uint4*)dst = v;
+    } else {
+      const uint16_t* pv = (const uint16_t*)&v;
+      for (int e = 0; e < 8 && c + e < ncols; ++e) dst[e] = pv[e];
+    }
+  }
+}
+
+template <typename T, bool HB>
+mi_status_t launch_mid(const GemmArgs& q0, hipStream_t s, const char* what) {
+  static bool attr = [] {
+    (void)hipFuncSetAttribute((const void*)int8_mid_kernel<T, HB>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)mid::LDS);
+    return true;
+  }();
+  (void)attr;
+  GemmArgs q = q0;
+  q.tiles_m = (int)((q.M + mid::BM - 1) / mid::BM);
+  // W rows per block: a multiple of 8 up to 96, so that the blocks about fill the CUs
+  const int64_t want_n = std::max<int64_t>(1, cu_count() / q.tiles_m);
+  int64_t R = (q.N + want_n - 1) / want_n;
+  R = std::min<int64_t>(mid::BNF, std::max<int64_t>(32, (R + 7) / 8 * 8));
+  q.tiles_n = (int)((q.N + R - 1) / R);
+  hipLaunchKernelGGL((int8_mid_kernel<T, HB>), dim3((unsigned)(q.tiles_m * q.tiles_n)),
+                     dim3(mid::NT), mid::LDS, s, q, (int)R);
+  return check_launch(what);
 }
 
 // ---- int8 weight-only linear for few rows (M <= 64): HBM-bound on W -------------------
@@ -1156,6 +1413,9 @@ mi_status_t launch_dl(const GemmArgs& q0, int64_t batch, hipStream_t s, const ch
 template <typename T, bool I8, bool HB>
 mi_status_t launch_mfma(const GemmArgs& q, int64_t batch, hipStream_t s, const char* what) {
   const int64_t cus = cu_count();
+  // int8 W and 64 < M <= 512 (config 4's M = 256): tiles sized to the CUs
+  if (I8 && batch == 1 && q.M > 64 && q.M <= 4 * mid::BM && dl_eligible(q, true))
+    return launch_mid<T, HB>(q, s, what);
   const int64_t big = ((q.M + 255) / 256) * ((q.N + 255) / 256) * batch;
   if (big >= cus && dl_eligible(q, I8)) return launch_dl<T, HB, I8>(q, batch, s, what);
   if (big >= cus) return Cfg<T, 256, 256, 2, 4, I8, HB>::launch(q, batch, s, what);
