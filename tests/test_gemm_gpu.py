@@ -201,8 +201,10 @@ def test_row_major_b_transpose_path():
                                    (48, 1000, 2048), (2, 33, 3072), (64, 96, 5120)])
 @pytest.mark.parametrize("bias", [None, "bf16", "f32"])
 def test_int8_linear_skinny(M, N, K, bias):
-    """M <= 64: K % 1024 == 0 takes the LDS-staged weight stream (32 W rows
-    per block in 1 KiB slabs, an odd slab count included, ragged N), other
+    """M <= 64: K % 1024 == 0 takes the LDS-staged weight stream (N / CUs W
+    rows per block, at least 16 and at most 48, in 1 KiB slabs that each
+    wave streams through its own ring: slab counts of 1, 2, 3 and 5 against
+    the three-slot ring, ragged N, blocks with a single row), other
     K % 128 == 0 the register weight stream (K split over eight waves);
     partial tiles are added in a fixed order.  K = 192 exercises the general
     kernel's int8 path."""

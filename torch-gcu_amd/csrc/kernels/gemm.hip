@@ -1070,150 +1070,174 @@ mi_status_t launch_skinny(const GemmArgs& q, hipStream_t s) {
 // ---- int8 weight-only linear for few rows, weight staged through LDS ------------------
 //
 // The contraction of int8_skinny_kernel for K % 1024 == 0 and 16-byte aligned
-// W rows.  A 512-lane block owns 32 W rows and walks K in 1 KiB slabs.  A
-// slab (32 rows x 1 KiB) is copied by global_load_lds_dwordx4 straight into
-// LDS, each wave load one contiguous 1 KiB row segment (HBM sees long
-// contiguous runs; a wave load spread over 16 rows, as the MFMA operand
-// layout would ask for, streams at about two thirds of the rate), into a
-// ring of two slabs; the slab's x fragments are loaded into registers right
-// after it.  Wave w multiplies bytes 128w .. 128w + 127 of every slab row:
-// lane (r, g) reads 16 bytes of row r at 64 kp + 16 g (kp = 0, 1), which
+// W rows.  A 512-lane block owns R consecutive W rows, R = N / CUs rounded up
+// (43 for N = 11008 on 256 CUs) and at most 48, so every CU streams the same
+// share of W once (with 32-row blocks, 344 blocks on 256 CUs left 88 CUs
+// streaming twice the bytes of the others).  K is walked in 1 KiB slabs of
+// 48 rows (three 16-row MFMA tiles; rows past R re-read the block's last
+// row, an L2 hit, and feed columns that are never stored), and wave w owns
+// bytes 128 w .. 128 w + 127 of every slab row: it copies them into its own
+// LDS ring by global_load_lds_dwordx4 (one copy = 8 rows x 128 bytes, whole
+// cache lines) together with the matching x fragments into registers, and
+// multiplies them, so the waves never wait for each other until the final
+// combine.  The ring holds three slabs (two slabs of lead on the one being
+// multiplied; a wave refills a slot as soon as it has multiplied it).  Lane
+// (r, g) reads 16 bytes of row 16 t + r at 64 kp + 16 g (kp = 0, 1), which
 // feed two v_mfma_f32_16x16x32 (8 bytes each, widened to bf16 exactly) with
-// x as the 16-row operand, x's fragments taken at the same k.  The row pitch
-// is 1040 B = 260 dwords, 4 mod 64 banks: the 16 lanes of one 16-byte read
-// pass (one g, rows 0..15) cover the 64 banks once, so reads are
-// conflict-free.  The 8 waves' partial tiles are added in a fixed order
-// through LDS; the epilogue applies the per-column scale and bias and rounds
-// once.
-constexpr int kStRows = 32, kStSlab = 1024, kStPitch = kStSlab + 16, kStWaves = 8;
-static_assert((kStPitch / 4) % 64 == 4, "slab pitch must be 4 dwords mod 64 banks");
-constexpr int kStLds = 2 * kStRows * kStPitch;
+// x as the 16-row operand, x's fragments taken at the same k.  Rows are 128
+// bytes in LDS, chunk c of row r stored at c ^ ((r >> 1) & 7) (the copying
+// lane fetches the matching global chunk), so the 16 rows of a read pass hit
+// 16 distinct 16-byte bank groups.  The 8 waves' partial tiles are added in
+// a fixed order through LDS; the epilogue applies the per-column scale and
+// bias and rounds once.
+constexpr int kStTiles = 3, kStRows = 16 * kStTiles, kStSlab = 1024, kStWaves = 8;
+constexpr int kStPart = kStSlab / kStWaves;    // bytes of a slab row per wave (128)
+constexpr int kStCopies = kStRows * kStPart / 1024;  // wave copies per slab (6)
+constexpr int kStRing = 3;
+constexpr int kStWaveLds = kStRing * kStRows * kStPart;  // one wave's ring
+constexpr int kStLds = kStWaves * kStWaveLds;
+static_assert(kStLds <= 160 * 1024, "slab rings fit the LDS");
+static_assert(kStLds >= kStWaves * kStTiles * 16 * 17 * 4, "combine staging fits");
 
-template <typename T, int MT, bool HAS_BIAS>
-__global__ __launch_bounds__(64 * kStWaves, MT <= 2 ? 4 : 2) void int8_stream_kernel(GemmArgs p) {
+template <typename T, int MT, int RING, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * kStWaves, 1) void int8_stream_kernel(GemmArgs p, int R) {
   typedef typename Mfma16<T>::vec vec;
   extern __shared__ __align__(16) char st_lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * kStRows;
+  const int64_t n0 = (int64_t)blockIdx.x * R;
+  const int nrows = (int)min<int64_t>(R, p.N - n0);
   const int S = (int)(p.K / kStSlab);
-  // the wave copies rows 4 wave .. 4 wave + 3 of every slab (rows past N are
-  // clamped to the last row and only feed columns never stored)
-  const int8_t* wsrc[4];
+  char* ring = st_lds + wave * kStWaveLds;
+  // copy q moves slab rows 8 q .. 8 q + 7: lane l fetches row 8 q + l / 8, the
+  // global chunk that lands at chunk l % 8 of the swizzled row (source rows
+  // past the block's nrows re-read its last row)
+  const int8_t* wsrc[kStCopies];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    wsrc[i] = (const int8_t*)p.b + min<int64_t>(n0 + 4 * wave + i, p.N - 1) * p.ldb + lane * 16;
+  for (int q = 0; q < kStCopies; ++q) {
+    const int row = 8 * q + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    wsrc[q] = (const int8_t*)p.b + (n0 + min(row, nrows - 1)) * p.ldb + kStPart * wave + 16 * c;
+  }
   // x fragment j = 2 kp + h of slab s: row 16 mt + r, k = 1024 s + 128 wave + 64 kp + 16 g + 8 h
   const uint16_t* xrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
-    xrow[mt] = p.a + min<int64_t>(16 * mt + r, p.M - 1) * p.lda + 128 * wave + 16 * g;
-  auto issue = [&](int buf, int s) __attribute__((always_inline)) {
-    char* dst = st_lds + buf * (kStRows * kStPitch) + 4 * wave * kStPitch;
+    xrow[mt] = p.a + min<int64_t>(16 * mt + r, p.M - 1) * p.lda + kStPart * wave + 16 * g;
+  // slab s: this wave's W copies into ring slot s % RING, then its x fragments
+  vec xf[RING][MT][4];
+  auto issue = [&](auto B, int s) __attribute__((always_inline)) {
+    constexpr int buf = decltype(B)::value;
+    char* dst = ring + buf * (kStRows * kStPart);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(wsrc[i] + (int64_t)s * kStSlab),
-                                       (lds_void_t*)(dst + i * kStPitch), 16, 0, 0);
-  };
-  auto loadx = [&](vec (&xf)[MT][4], int s) __attribute__((always_inline)) {
+    for (int q = 0; q < kStCopies; ++q)
+      __builtin_amdgcn_global_load_lds((const void*)(wsrc[q] + (int64_t)s * kStSlab),
+                                       (lds_void_t*)(dst + q * 1024), 16, 0, kCpolNT);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        xf[mt][j] = *(const vec*)(xrow[mt] + (int64_t)s * kStSlab + 64 * (j >> 1) + 8 * (j & 1));
+        xf[buf][mt][j] = *(const vec*)(xrow[mt] + (int64_t)s * kStSlab + 64 * (j >> 1) + 8 * (j & 1));
   };
-  f32x4_t acc[MT][2];
+  f32x4_t acc[MT][kStTiles];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4_t{};
-  auto compute = [&](int buf, const vec (&xf)[MT][4]) __attribute__((always_inline)) {
-    const char* wb = st_lds + buf * (kStRows * kStPitch) + r * kStPitch + 128 * wave + 16 * g;
+    for (int t = 0; t < kStTiles; ++t) acc[mt][t] = f32x4_t{};
+  // lane (r, g) reads chunk 4 kp + g of row 16 t + r: swizzled by (r >> 1) & 7
+  const int rsw = (r >> 1) & 7;
+  auto compute = [&](auto B) __attribute__((always_inline)) {
+    constexpr int buf = decltype(B)::value;
+    const char* wb = ring + buf * (kStRows * kStPart) + r * kStPart;
 #pragma unroll
     for (int kp = 0; kp < 2; ++kp)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const u32x4_t w16 = *(const u32x4_t*)(wb + t * 16 * kStPitch + 64 * kp);
+      for (int t = 0; t < kStTiles; ++t) {
+        const u32x4_t w16 = *(const u32x4_t*)(wb + t * 16 * kStPart + 16 * ((4 * kp + g) ^ rsw));
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const vec wk = widen8<T>(u32x2_t{w16[2 * h], w16[2 * h + 1]});
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[mt][t] = Mfma16<T>::mma(xf[mt][2 * kp + h], wk, acc[mt][t]);
+          for (int mt = 0; mt < MT; ++mt)
+            acc[mt][t] = Mfma16<T>::mma(xf[buf][mt][2 * kp + h], wk, acc[mt][t]);
         }
       }
   };
-  // slab s lives in LDS buffer s % 2 and x registers xa (s even) / xb (s odd);
-  // a slab is complete once at most the next slab's loads (4 W + 4 MT x) are
-  // outstanding, and the barrier makes every wave's copy visible
-  constexpr int NEXT = 4 + 4 * MT;
-  vec xa[MT][4], xb[MT][4];
-  issue(0, 0);
-  loadx(xa, 0);
-  if (S > 1) {
-    issue(1, 1);
-    loadx(xb, 1);
+  // slab s has landed once at most the later slabs' loads (each kStCopies W
+  // copies and 4 MT x loads, issued together and in slab order) are
+  // outstanding; the copies are this wave's own, so no barrier is needed
+  constexpr int PER = kStCopies + 4 * MT;
+  auto wait_slab = [&](int later) __attribute__((always_inline)) {
+    if (RING > 2 && later >= 2) wait_vmcnt<2 * PER>();
+    else if (later >= 1) wait_vmcnt<PER>();
+    else wait_vmcnt<0>();
+  };
+  // one slab step: U = s % RING picks the slot (the loop is unrolled by RING)
+  auto step = [&](auto U, int s) __attribute__((always_inline)) {
+    wait_slab(min(RING - 1, S - 1 - s));
+    compute(U);
+    if (s + RING < S) issue(U, s + RING);
+  };
+  static_assert(RING == 2 || RING == 3, "two or three slabs in flight");
+  issue(std::integral_constant<int, 0>{}, 0);
+  if (S > 1) issue(std::integral_constant<int, 1>{}, 1);
+  if constexpr (RING == 3) {
+    if (S > 2) issue(std::integral_constant<int, 2>{}, 2);
   }
-  for (int s = 0; s < S; s += 2) {
-    if (s + 1 < S) wait_vmcnt<NEXT>();
-    else wait_vmcnt<0>();
-    __syncthreads();
-    compute(0, xa);
-    __syncthreads();
-    if (s + 2 < S) {
-      issue(0, s + 2);
-      loadx(xa, s + 2);
-    }
-    if (s + 1 >= S) break;
-    if (s + 2 < S) wait_vmcnt<NEXT>();
-    else wait_vmcnt<0>();
-    __syncthreads();
-    compute(1, xb);
-    __syncthreads();
-    if (s + 3 < S) {
-      issue(1, s + 3);
-      loadx(xb, s + 3);
+  for (int s = 0; s < S; s += RING) {
+    step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < S) step(std::integral_constant<int, 1>{}, s + 1);
+    if constexpr (RING == 3) {
+      if (s + 2 < S) step(std::integral_constant<int, 2>{}, s + 2);
     }
   }
-  // fixed-order combine of the 8 waves' partial tiles (the slab ring is free)
-  float(*red)[2][16][17] = (float(*)[2][16][17])st_lds;
-  const int tn = threadIdx.x & 15, tm = (threadIdx.x >> 4) & 15, tt = threadIdx.x >> 8;
+  // fixed-order combine of the 8 waves' partial tiles (the rings are free
+  // once every wave is done)
+  __syncthreads();
+  float(*red)[kStTiles][16][17] = (float(*)[kStTiles][16][17])st_lds;
   const bool bias_f32 = p.bias_dtype == MI_F32;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     if (mt > 0) __syncthreads();
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < kStTiles; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) red[wave][t][4 * g + i][r] = acc[mt][t][i];
     __syncthreads();
-    const int64_t m = mt * 16 + tm;
-    if (m >= p.M) continue;
-    const int64_t n = n0 + 16 * tt + tn;
-    if (n >= p.N) continue;
-    float sum = red[0][tt][tm][tn];
+    for (int idx = threadIdx.x; idx < kStTiles * 256; idx += 64 * kStWaves) {
+      const int tt = idx >> 8, tm = (idx >> 4) & 15, tn = idx & 15;
+      const int64_t m = mt * 16 + tm;
+      if (m >= p.M || 16 * tt + tn >= nrows) continue;
+      const int64_t n = n0 + 16 * tt + tn;
+      float sum = red[0][tt][tm][tn];
 #pragma unroll
-    for (int w = 1; w < kStWaves; ++w) sum += red[w][tt][tm][tn];
-    float v = p.alpha * p.scale[n] * sum;
-    if (HAS_BIAS) {
-      const int64_t bo = m * p.bias_sm + n * p.bias_sn;
-      v += p.beta * (bias_f32 ? ((const float*)p.bias)[bo]
-                              : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo]));
+      for (int w = 1; w < kStWaves; ++w) sum += red[w][tt][tm][tn];
+      float v = p.alpha * p.scale[n] * sum;
+      if (HAS_BIAS) {
+        const int64_t bo = m * p.bias_sm + n * p.bias_sn;
+        v += p.beta * (bias_f32 ? ((const float*)p.bias)[bo]
+                                : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo]));
+      }
+      p.c[m * p.ldc + n] = MfmaOp<T>::store(v);
     }
-    p.c[m * p.ldc + n] = MfmaOp<T>::store(v);
   }
 }
 
 template <typename T, int MT, bool HB>
 mi_status_t launch_stream_mt(const GemmArgs& q, hipStream_t s) {
+  constexpr int RING = MT <= 2 ? 3 : 2;
   static bool attr = [] {
-    (void)hipFuncSetAttribute((const void*)int8_stream_kernel<T, MT, HB>,
+    (void)hipFuncSetAttribute((const void*)int8_stream_kernel<T, MT, RING, HB>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, kStLds);
     return true;
   }();
   (void)attr;
-  hipLaunchKernelGGL((int8_stream_kernel<T, MT, HB>), dim3(ceil_div_u(q.N, kStRows)),
-                     dim3(64 * kStWaves), kStLds, s, q);
+  // rows per block: N / CUs rounded up, at least one tile and at most a slab
+  const int64_t cus = std::max(1, cu_count());
+  const int R = (int)std::min<int64_t>(kStRows, std::max<int64_t>(16, (q.N + cus - 1) / cus));
+  hipLaunchKernelGGL((int8_stream_kernel<T, MT, RING, HB>), dim3((unsigned)ceil_div_u(q.N, R)),
+                     dim3(64 * kStWaves), kStLds, s, q, R);
   return check_launch("int8_linear stream");
 }
 
