@@ -1099,7 +1099,11 @@ constexpr int kStLds = kStWaves * kStWaveLds;
 static_assert(kStLds <= 160 * 1024, "slab rings fit the LDS");
 static_assert(kStLds >= kStWaves * kStTiles * 16 * 17 * 4, "combine staging fits");
 
-template <typename T, int MT, int RING, bool HAS_BIAS>
+// SFIX > 0 fixes the slab count at compile time (K = 1024 SFIX): the loop is
+// then fully unrolled and the compiler can count the loads in flight at
+// every step (through the loop's back edge it waits for all of them before
+// a step's first MFMA).
+template <typename T, int MT, int RING, bool HAS_BIAS, int SFIX>
 __global__ __launch_bounds__(64 * kStWaves, 1) void int8_stream_kernel(GemmArgs p, int R) {
   typedef typename Mfma16<T>::vec vec;
   extern __shared__ __align__(16) char st_lds[];
@@ -1108,7 +1112,7 @@ __global__ __launch_bounds__(64 * kStWaves, 1) void int8_stream_kernel(GemmArgs 
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * R;
   const int nrows = (int)min<int64_t>(R, p.N - n0);
-  const int S = (int)(p.K / kStSlab);
+  const int S = SFIX > 0 ? SFIX : (int)(p.K / kStSlab);
   char* ring = st_lds + wave * kStWaveLds;
   // copy q moves slab rows 8 q .. 8 q + 7: lane l fetches row 8 q + l / 8, the
   // global chunk that lands at chunk l % 8 of the swizzled row (source rows
@@ -1185,6 +1189,7 @@ __global__ __launch_bounds__(64 * kStWaves, 1) void int8_stream_kernel(GemmArgs 
   if constexpr (RING == 3) {
     if (S > 2) issue(std::integral_constant<int, 2>{}, 2);
   }
+#pragma unroll
   for (int s = 0; s < S; s += RING) {
     step(std::integral_constant<int, 0>{}, s);
     if (s + 1 < S) step(std::integral_constant<int, 1>{}, s + 1);
@@ -1224,21 +1229,28 @@ __global__ __launch_bounds__(64 * kStWaves, 1) void int8_stream_kernel(GemmArgs 
   }
 }
 
-template <typename T, int MT, bool HB>
-mi_status_t launch_stream_mt(const GemmArgs& q, hipStream_t s) {
+template <typename T, int MT, bool HB, int SFIX>
+mi_status_t launch_stream_k(const GemmArgs& q, hipStream_t s, int R) {
   constexpr int RING = MT <= 2 ? 3 : 2;
   static bool attr = [] {
-    (void)hipFuncSetAttribute((const void*)int8_stream_kernel<T, MT, RING, HB>,
+    (void)hipFuncSetAttribute((const void*)int8_stream_kernel<T, MT, RING, HB, SFIX>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, kStLds);
     return true;
   }();
   (void)attr;
+  hipLaunchKernelGGL((int8_stream_kernel<T, MT, RING, HB, SFIX>), dim3((unsigned)ceil_div_u(q.N, R)),
+                     dim3(64 * kStWaves), kStLds, s, q, R);
+  return check_launch("int8_linear stream");
+}
+
+template <typename T, int MT, bool HB>
+mi_status_t launch_stream_mt(const GemmArgs& q, hipStream_t s) {
   // rows per block: N / CUs rounded up, at least one tile and at most a slab
   const int64_t cus = std::max(1, cu_count());
   const int R = (int)std::min<int64_t>(kStRows, std::max<int64_t>(16, (q.N + cus - 1) / cus));
-  hipLaunchKernelGGL((int8_stream_kernel<T, MT, RING, HB>), dim3((unsigned)ceil_div_u(q.N, R)),
-                     dim3(64 * kStWaves), kStLds, s, q, R);
-  return check_launch("int8_linear stream");
+  // K = 4096 (a 4096-wide hidden layer) with the slab count fixed
+  if (q.K == 4 * kStSlab) return launch_stream_k<T, MT, HB, 4>(q, s, R);
+  return launch_stream_k<T, MT, HB, 0>(q, s, R);
 }
 
 template <typename T, bool HB>
