@@ -115,6 +115,41 @@ __device__ __forceinline__ typename MfmaOp<T>::vec widen8(u32x2_t w) {
 }
 
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
+
+// Four consecutive per-column values n .. n + 3 of a row vector (the int8
+// scale, or a bias broadcast over rows) as floats: element k at
+// base + off + k * stride, fp32 or of the output's 16-bit type T.  One
+// vector load when all four columns exist, the stride is 1 and the address
+// is aligned; else four loads with the column clamped to N - 1 (clamped
+// columns only feed outputs that are never stored).
+template <typename T>
+__device__ __forceinline__ f32x4_t load_col4_t(const void* base, int dtype, int64_t n, int64_t stride,
+                                               int64_t N, int64_t off) {
+  f32x4_t r;
+  if (dtype == MI_F32) {
+    const float* b = (const float*)base + off;
+    if (stride == 1 && n + 3 < N && (((uintptr_t)(b + n)) & 15) == 0) {
+      r = *(const f32x4_t*)(b + n);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = b[min<int64_t>(n + e, N - 1) * stride];
+    }
+  } else {
+    const uint16_t* b = (const uint16_t*)base + off;
+    if (stride == 1 && n + 3 < N && (((uintptr_t)(b + n)) & 7) == 0) {
+      const u16x4_t v = *(const u16x4_t*)(b + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = MfmaOp<T>::load(v[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = MfmaOp<T>::load(b[min<int64_t>(n + e, N - 1) * stride]);
+    }
+  }
+  return r;
+}
+
 // Per-lane loader of a ROWS x 64 tile of a K-contiguous 16-bit matrix: V
 // 16-byte vectors per lane, 8 lanes per 128-byte row segment; vector i of a
 // lane covers tile row row0 + i * (NT / 8).  Rows past the end of the matrix
@@ -331,6 +366,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_mfma_kernel(GemmArgs p) 
     if (n >= p.N) continue;
     const int64_t bcol = batch * p.bias_sb + n * p.bias_sn;
     const float colscale = B_INT8 ? p.alpha * p.scale[n] : p.alpha;
+    // a bias broadcast over rows: one load per column
+    const bool row_bias = HAS_BIAS && p.bias_sm == 0;
+    float bcolv = 0.f;
+    if (row_bias)
+      bcolv = bias_f32 ? ((const float*)p.bias)[bcol] : MfmaOp<T>::load(((const uint16_t*)p.bias)[bcol]);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -339,9 +379,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_mfma_kernel(GemmArgs p) 
         if (m < p.M) {
           float v = colscale * acc[i][j][r];
           if (HAS_BIAS) {
-            const int64_t bo = bcol + m * p.bias_sm;
-            const float bv = bias_f32 ? ((const float*)p.bias)[bo]
-                                      : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo]);
+            float bv = bcolv;
+            if (!row_bias) {
+              const int64_t bo = bcol + m * p.bias_sm;
+              bv = bias_f32 ? ((const float*)p.bias)[bo] : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo]);
+            }
             v += p.beta * bv;
           }
           C[m * p.ldc + n] = MfmaOp<T>::store(v);
@@ -600,36 +642,51 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
     st = st + 1 == STAGES ? 0 : st + 1;
   }
 
-  // epilogue: out = alpha * acc + beta * bias, one rounding, staged per wave
+  // epilogue: out = alpha * acc + beta * bias, one rounding, staged per wave.
+  // A lane's outputs come in runs of 4 columns; the per-column factors (the
+  // int8 scale, a bias broadcast over rows) are loaded once per run, four
+  // at a time, and used for both row fragments (one scalar load per output
+  // made the bias epilogue cost 13 % of config 4's addmm)
   __syncthreads();
   uint16_t* es = smem + wave * TM * EP;
   const float alpha = p.alpha, beta = p.beta;
-  const bool bias_f32 = p.bias_dtype == MI_F32;
+  const bool row_bias = HAS_BIAS && p.bias_sm == 0;
+  auto load_col4 = [&](const void* base, int dtype, int64_t n, int64_t stride, int64_t N,
+                       int64_t off = 0) __attribute__((always_inline)) {
+    return load_col4_t<T>(base, dtype, n, stride, N, off);
+  };
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int ml = i * 32 + (lane & 31);
-    const int64_t m = m0 + wm * TM + ml;
+  for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+    for (int g = 0; g < 4; ++g) {
+      const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
+      const int64_t n = n0 + wn * TN + nl;
+      f32x4_t sc4 = {1.f, 1.f, 1.f, 1.f}, bb4 = {};
+      if constexpr (B_INT8) sc4 = load_col4(p.scale, MI_F32, n, 1, p.N);
+      if (row_bias) bb4 = load_col4(p.bias, p.bias_dtype, n, p.bias_sn, p.N, batch * p.bias_sb);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
+      for (int i = 0; i < FM; ++i) {
+        const int ml = i * 32 + (lane & 31);
+        const int64_t m = m0 + wm * TM + ml;
         u16x4_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float x = alpha * acc[j][i][4 * g + e];
-          if (B_INT8) x *= p.scale[min<int64_t>(n0 + wn * TN + nl + e, p.N - 1)];
+          float x = alpha * acc[j][i][4 * g + e] * sc4[e];
           if (HAS_BIAS) {
-            const int64_t n = min<int64_t>(n0 + wn * TN + nl + e, p.N - 1);
-            const int64_t bo_ = batch * p.bias_sb + min<int64_t>(m, p.M - 1) * p.bias_sm + n * p.bias_sn;
-            x += beta * (bias_f32 ? ((const float*)p.bias)[bo_]
-                                  : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo_]));
+            float bv = bb4[e];
+            if (!row_bias) {
+              const int64_t bo_ = batch * p.bias_sb + min<int64_t>(m, p.M - 1) * p.bias_sm +
+                                  min<int64_t>(n + e, p.N - 1) * p.bias_sn;
+              bv = p.bias_dtype == MI_F32 ? ((const float*)p.bias)[bo_]
+                                          : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo_]);
+            }
+            x += beta * bv;
           }
           v[e] = MfmaOp<T>::store(x);
         }
         *(u16x4_t*)(es + ml * EP + nl) = v;
       }
-  }
+    }
   uint16_t* Cb = p.c + batch * p.sc;
   const int64_t rbase = m0 + wm * TM, cbase = n0 + wn * TN;
   constexpr int LPR = TN / 8, RPI = 64 / LPR;  // lanes per row, rows per pass
@@ -841,20 +898,29 @@ __global__ __launch_bounds__(mid::NT, 1) void int8_mid_kernel(GemmArgs p, int R)
   const bool bias_f32 = p.bias_dtype == MI_F32;
   const int ml = lane & 31;
   const int64_t m = m0 + wave * 32 + ml;
+  // the per-column scale (and a bias broadcast over rows) four columns per load
+  const bool row_bias = HAS_BIAS && p.bias_sm == 0;
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
+      const f32x4_t sc4 = load_col4_t<T>(p.scale, MI_F32, n0 + nl, 1, p.N, 0);
+      f32x4_t bb4 = {};
+      if (row_bias) bb4 = load_col4_t<T>(p.bias, p.bias_dtype, n0 + nl, p.bias_sn, p.N, 0);
       u16x4_t v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t n = min<int64_t>(n0 + nl + e, p.N - 1);
-        float x = alpha * acc[j][4 * g + e] * p.scale[n];
+        float x = alpha * acc[j][4 * g + e] * sc4[e];
         if (HAS_BIAS) {
-          const int64_t bo_ = min<int64_t>(m, p.M - 1) * p.bias_sm + n * p.bias_sn;
-          x += beta * (bias_f32 ? ((const float*)p.bias)[bo_]
-                                : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo_]));
+          float bv = bb4[e];
+          if (!row_bias) {
+            const int64_t n = min<int64_t>(n0 + nl + e, p.N - 1);
+            const int64_t bo_ = min<int64_t>(m, p.M - 1) * p.bias_sm + n * p.bias_sn;
+            bv = bias_f32 ? ((const float*)p.bias)[bo_]
+                          : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo_]);
+          }
+          x += beta * bv;
         }
         v[e] = MfmaOp<T>::store(x);
       }
@@ -1189,13 +1255,18 @@ __global__ __launch_bounds__(64 * kStWaves, 1) void int8_stream_kernel(GemmArgs 
   if constexpr (RING == 3) {
     if (S > 2) issue(std::integral_constant<int, 2>{}, 2);
   }
-#pragma unroll
-  for (int s = 0; s < S; s += RING) {
+  auto round = [&](int s) __attribute__((always_inline)) {
     step(std::integral_constant<int, 0>{}, s);
     if (s + 1 < S) step(std::integral_constant<int, 1>{}, s + 1);
     if constexpr (RING == 3) {
       if (s + 2 < S) step(std::integral_constant<int, 2>{}, s + 2);
     }
+  };
+  if constexpr (SFIX > 0) {
+#pragma unroll
+    for (int s = 0; s < SFIX; s += RING) round(s);
+  } else {
+    for (int s = 0; s < S; s += RING) round(s);
   }
   // fixed-order combine of the 8 waves' partial tiles (the rings are free
   // once every wave is done)
