@@ -167,6 +167,34 @@ def test_dl_kernel_bias_alpha_beta(bias_shape):
         assert_close(out, ref, "bf16", f"dl addmm {bias_shape} a={alpha} b={beta}")
 
 
+@pytest.mark.parametrize("kind", ["strided", "misaligned", "ragged_n", "f32_misaligned"])
+def test_dl_kernel_row_bias_layouts(kind):
+    """Row-broadcast bias through the epilogue's four-column loads: a strided
+    view (stride 2: per-element loads), an offset view (not 8-byte aligned:
+    per-element loads), an N that is not a multiple of 4 (the last run of a
+    tile clamps its columns) and an fp32 bias one element into its buffer."""
+    M, N, K = 4160, 4096, 128
+    if kind == "ragged_n":
+        N = 4098
+    a, w = rn((M, K), 62, std=1.0), rn((N, K), 63, std=1.0)
+    if kind == "strided":
+        base = rn((2 * N,), 64, std=1.0)
+        bias_cpu, bias_dev = base[::2], base.cuda()[::2]
+    elif kind == "misaligned":
+        base = rn((N + 1,), 64, std=1.0)
+        bias_cpu, bias_dev = base[1:], base.cuda()[1:]
+    elif kind == "f32_misaligned":
+        base = torch.randn(N + 1, generator=g(64))
+        bias_cpu, bias_dev = base[1:], base.cuda()[1:]
+    else:
+        bias_cpu = rn((N,), 64, std=1.0)
+        bias_dev = bias_cpu.cuda()
+    ref = aten.addmm(bias_cpu, a, w.t(), beta=0.75, alpha=1.25)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _abi.addmm(out, bias_dev, a.cuda(), w.cuda().t(), beta=0.75, alpha=1.25)
+    assert_close(out, ref, "bf16", f"dl addmm row bias {kind}")
+
+
 def test_dl_kernel_batched_strided_and_odd_ldc():
     # bmm with enough batches to select the large-tile kernel
     B, M, N, K = 64, 512, 512, 128
