@@ -275,14 +275,17 @@ def test_int8_linear_large_tile_path(dtype, bias):
 
 
 @pytest.mark.parametrize("M,N,K,dtype,bias", [
-    (256, 1000, 1024, torch.bfloat16, None),     # 2 x rows, ragged last W panel
-    (200, 777, 64, torch.bfloat16, "bf16"),      # one K step, ragged x tile, odd N
-    (512, 4104, 512, torch.float16, "f32"),      # 4 x tiles, fp32 bias
-    (65, 96, 128, torch.bfloat16, "row"),        # smallest M of the path, [M, N] bias
+    (256, 1000, 1024, torch.bfloat16, None),     # split-K: 4 tiles x 16 slices of one K step
+    (256, 1001, 512, torch.bfloat16, "f32"),     # split-K, N not a multiple of 4, fp32 bias
+    (512, 4104, 512, torch.float16, "f32"),      # split-K: 2 x 17 tiles x 7 uneven slices
+    (65, 96, 128, torch.bfloat16, "row"),        # split-K, smallest M of the path, [M, N] bias
+    (200, 777, 64, torch.bfloat16, "bf16"),      # one K step: 128-row tiles, odd N
+    (130, 65536, 128, torch.bfloat16, "bf16"),   # 256 tiles fill the CUs: 128-row tiles
 ])
 def test_int8_linear_mid_path(M, N, K, dtype, bias):
-    """64 < M <= 512: 128-row x tiles against W panels sized so the blocks
-    about fill the CUs (config 4's M = 256 runs here)."""
+    """64 < M <= 512: split-K over 256 x 256 tiles with an fp32 combine when
+    the tiles are too few to fill the CUs (config 4's M = 256: 43 tiles x 5
+    slices), else 128-row x tiles against W panels sized to the CUs."""
     x, w, scales = int8_inputs(M, N=N, K=K, seed=100 + M)
     x = x.to(dtype)
     b = None

@@ -458,8 +458,12 @@ __device__ __forceinline__ int dl_swz(int r, int c) { return c ^ ((r & 7) ^ ((r 
 // 16-byte reads of 16 consecutive rows under 32- or 64-bank LDS
 __device__ __forceinline__ int dl_swz64(int r, int c) { return c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1)); }
 
-template <typename T, bool HAS_BIAS, bool B_INT8>
-__global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
+// SPLIT: blockIdx.y is a K slice instead of a batch; the block multiplies
+// its slice's whole 64-wide steps (slice s of S gets KT / S steps, one more
+// for s < KT % S) and stores the raw fp32 sums to part[s][M][ldp] for
+// splitk_combine_kernel (no scale, bias or rounding here).
+template <typename T, bool HAS_BIAS, bool B_INT8, bool SPLIT = false>
+__global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* part, int64_t ldp) {
   constexpr int BK = dl::BK, STAGES = dl::STAGES, WN = dl::WN, FM = dl::FM, FN = dl::FN;
   constexpr int BM = dl::BM, BN = dl::BN, CH = dl::CH, RPK = dl::RPK, NQA = dl::NQA,
                 TA = dl::TA, KS = dl::KS, TM = dl::TM, TN = dl::TN, EP = dl::EP,
@@ -487,14 +491,21 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
     tm = first_m + in_group % gsize;
     tn = in_group / gsize;
   }
-  const int64_t batch = blockIdx.y;
+  const int64_t batch = SPLIT ? 0 : blockIdx.y;
   const int M = (int)p.M, N = (int)p.N, K = (int)p.K;
   const int m0 = tm * BM, n0 = tn * BN;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  const uint16_t* A = p.a + batch * p.sa;
-  const char* Bbase = (const char*)p.b + batch * p.sb * (B_INT8 ? 1 : 2);
+  int KT = K / BK, k_first = 0;
+  if constexpr (SPLIT) {
+    const int S = gridDim.y, sl = blockIdx.y, base = KT / S, rem = KT % S;
+    k_first = sl * base + min(sl, rem);
+    KT = base + (sl < rem ? 1 : 0);
+  }
+  const uint16_t* A = p.a + batch * p.sa + (int64_t)k_first * BK;
+  const char* Bbase =
+      (const char*)p.b + (batch * p.sb + (int64_t)k_first * BK) * (B_INT8 ? 1 : 2);
 
   // per-lane byte offsets (the host checked they fit 32 bits); rows past the
   // matrix are clamped to its last row and only feed outputs never stored
@@ -623,7 +634,6 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
     }
   };
 
-  const int KT = K / BK;
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < KT) issue(s, s * BK);
@@ -642,6 +652,27 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
     st = st + 1 == STAGES ? 0 : st + 1;
   }
 
+  if constexpr (SPLIT) {
+    // raw sums of this K slice: a lane's runs of 4 columns as 16-byte stores
+    // (ldp is a multiple of 4, so a run that starts inside the row fits)
+    float* P = part + (int64_t)blockIdx.y * p.M * ldp;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t n = n0 + wn * TN + j * 32 + 8 * g + 4 * (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int64_t m = m0 + wm * TM + i * 32 + (lane & 31);
+          if (m < p.M && n < p.N) {
+            const f32x4_t v = {acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2],
+                               acc[j][i][4 * g + 3]};
+            *(f32x4_t*)(P + m * ldp + n) = v;
+          }
+        }
+      }
+    return;
+  }
   // epilogue: out = alpha * acc + beta * bias, one rounding, staged per wave.
   // A lane's outputs come in runs of 4 columns; the per-column factors (the
   // int8 scale, a bias broadcast over rows) are loaded once per run, four
@@ -710,6 +741,9 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p) {
 
 // ---- int8 weight-only linear, mid-size M (64 < M <= 512): 128 x R tiles -------------
 //
+// (Runs where split-K over 256 x 256 tiles does not apply: a single K step,
+// or enough tiles to fill the CUs; the sizes below are config 4's, which
+// split-K now runs faster.)
 // Config 4's M = 256 against W [11008, 4096] has 2 x 11008 / 256 = 86 W rows
 // per CU: 128 x 256 tiles give 86 blocks, 128 x 64 tiles 344 (1.34 waves).
 // Here a 256-lane block owns 128 rows of x (32 per wave) and R W rows, R a
@@ -1513,16 +1547,108 @@ mi_status_t launch_dl(const GemmArgs& q0, int64_t batch, hipStream_t s, const ch
   q.tiles_m = (int)((q.M + dl::BM - 1) / dl::BM);
   q.tiles_n = (int)((q.N + dl::BN - 1) / dl::BN);
   dim3 grid((unsigned)(q.tiles_m * q.tiles_n), (unsigned)batch);
-  hipLaunchKernelGGL((gemm_dl_kernel<T, HB, I8>), grid, dim3(dl::NT), lds, s, q);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, HB, I8>), grid, dim3(dl::NT), lds, s, q, nullptr,
+                     (int64_t)0);
+  return check_launch(what);
+}
+
+// ---- split-K over 256 x 256 tiles, for too few tiles to fill the CUs ----------------
+//
+// The int8 linear at M = 256 has 43 tiles of 256 x 256 for 256 CUs.  With S
+// K slices per tile (one block per CU, S = 5 there) each block keeps the
+// large tile's low LDS traffic per MFMA, which 128-row tiles over the whole
+// K cannot (every CU would copy all of x into LDS); the price is the fp32
+// partial sums, written once and read once by the combine (M = 256: 34.5 us
+// for the slices, 10.5 us for the combine of 56 MB).
+//
+// out = alpha * scale[n] * sum_s part[s] + beta * bias, the slices added in
+// order s = 0 .. S - 1 (deterministic) and rounded once.  One lane per run
+// of 4 columns of a row.
+template <typename T, bool HAS_BIAS>
+__global__ __launch_bounds__(256) void splitk_combine_kernel(GemmArgs p, const float* part, int S,
+                                                             int64_t ldp) {
+  const int64_t runs = ldp / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t m = idx / runs, n = (idx - m * runs) * 4;
+  if (m >= p.M || n >= p.N) return;
+  const float* src = part + m * ldp + n;
+  const int64_t slice = p.M * ldp;
+  f32x4_t acc = *(const f32x4_t*)src;
+#pragma unroll 4
+  for (int s = 1; s < S; ++s) acc += *(const f32x4_t*)(src + s * slice);
+  f32x4_t sc4 = {1.f, 1.f, 1.f, 1.f}, bb4 = {};
+  if (p.scale != nullptr) sc4 = load_col4_t<T>(p.scale, MI_F32, n, 1, p.N, 0);
+  const bool row_bias = HAS_BIAS && p.bias_sm == 0;
+  if (row_bias) bb4 = load_col4_t<T>(p.bias, p.bias_dtype, n, p.bias_sn, p.N, 0);
+  u16x4_t v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float x = p.alpha * acc[e] * sc4[e];
+    if (HAS_BIAS) {
+      float bv = bb4[e];
+      if (!row_bias) {
+        const int64_t bo = m * p.bias_sm + min<int64_t>(n + e, p.N - 1) * p.bias_sn;
+        bv = p.bias_dtype == MI_F32 ? ((const float*)p.bias)[bo]
+                                    : MfmaOp<T>::load(((const uint16_t*)p.bias)[bo]);
+      }
+      x += p.beta * bv;
+    }
+    v[e] = MfmaOp<T>::store(x);
+  }
+  uint16_t* dst = p.c + m * p.ldc + n;
+  if (n + 3 < p.N && (p.ldc % 4) == 0 && (((uintptr_t)p.c) & 7) == 0) {
+    *(u16x4_t*)dst = v;
+  } else {
+    for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = v[e];
+  }
+}
+
+// Slices for split-K over 256 x 256 tiles: as many as fill the CUs with one
+// block each (at least 2, at most one 64-wide K step per slice); 1 = no split.
+int splitk_slices(const GemmArgs& q) {
+  const int64_t tiles = ((q.M + dl::BM - 1) / dl::BM) * ((q.N + dl::BN - 1) / dl::BN);
+  const int64_t s = std::min<int64_t>(cu_count() / std::max<int64_t>(tiles, 1), q.K / dl::BK);
+  return s >= 2 ? (int)std::min<int64_t>(s, 16) : 1;
+}
+
+template <typename T, bool HB, bool I8>
+mi_status_t launch_splitk(const GemmArgs& q0, int S, hipStream_t s, const char* what) {
+  constexpr size_t lds = I8 ? dl::LDS_BYTES8 : dl::LDS_BYTES;
+  static bool attr = [] {
+    (void)hipFuncSetAttribute((const void*)gemm_dl_kernel<T, false, I8, true>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    return true;
+  }();
+  (void)attr;
+  GemmArgs q = q0;
+  q.tiles_m = (int)((q.M + dl::BM - 1) / dl::BM);
+  q.tiles_n = (int)((q.N + dl::BN - 1) / dl::BN);
+  const int64_t ldp = (q.N + 3) / 4 * 4;
+  Workspace wp;
+  MI_RETURN_IF(wp.alloc((size_t)S * (size_t)q.M * (size_t)ldp * sizeof(float), s));
+  float* part = (float*)wp.get();
+  hipLaunchKernelGGL((gemm_dl_kernel<T, false, I8, true>),
+                     dim3((unsigned)(q.tiles_m * q.tiles_n), (unsigned)S), dim3(dl::NT), lds, s, q,
+                     part, ldp);
+  MI_RETURN_IF(check_launch(what));
+  const int64_t lanes = q.M * (ldp / 4);
+  hipLaunchKernelGGL((splitk_combine_kernel<T, HB>), dim3((unsigned)((lanes + 255) / 256)),
+                     dim3(256), 0, s, q, (const float*)part, S, ldp);
   return check_launch(what);
 }
 
 template <typename T, bool I8, bool HB>
 mi_status_t launch_mfma(const GemmArgs& q, int64_t batch, hipStream_t s, const char* what) {
   const int64_t cus = cu_count();
-  // int8 W and 64 < M <= 512 (config 4's M = 256): tiles sized to the CUs
-  if (I8 && batch == 1 && q.M > 64 && q.M <= 4 * mid::BM && dl_eligible(q, true))
+  // int8 W and 64 < M <= 512 (config 4's M = 256): split-K over 256 x 256
+  // tiles when they are too few to fill the CUs (M = 256: 43 tiles x 5 K
+  // slices, 43.6 us against 49.9 us for 128-row tiles over the whole K; M =
+  // 96 .. 512 all faster), else 128-row tiles sized to the CUs
+  if (I8 && batch == 1 && q.M > 64 && q.M <= 4 * mid::BM && dl_eligible(q, true)) {
+    const int S = splitk_slices(q);
+    if (S > 1) return launch_splitk<T, HB, true>(q, S, s, what);
     return launch_mid<T, HB>(q, s, what);
+  }
   const int64_t big = ((q.M + 255) / 256) * ((q.N + 255) / 256) * batch;
   if (big >= cus && dl_eligible(q, I8)) return launch_dl<T, HB, I8>(q, batch, s, what);
   if (big >= cus) return Cfg<T, 256, 256, 2, 4, I8, HB>::launch(q, batch, s, what);
