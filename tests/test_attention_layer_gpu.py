@@ -41,6 +41,8 @@ def ref_attention(q, k, v, causal, scale=None):
     (2, 2, 2, 96, 300, 128, False),
     (1, 1, 1, 1, 77, 128, False),
     (1, 2, 2, 129, 129, 64, True),
+    (1, 2, 2, 40, 33, 128, False),   # fewer keys than one tile: only the clamped copy form
+    (1, 2, 2, 17, 17, 64, True),
 ])
 def test_flash_attention_parity(B, H, Hk, Sq, Sk, D, causal):
     q, k, v = rn((B, H, Sq, D), 1), rn((B, Hk, Sk, D), 2), rn((B, Hk, Sk, D), 3)

@@ -157,17 +157,48 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   // keys past the end of the last tile re-read the last key (masked later).
   const int k_ss = (int)p.k_ss, v_ss = (int)p.v_ss, Sk = (int)p.Sk;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
+  // A full tile's copies are a tile base (scalar) plus these per-lane byte
+  // offsets of key row `key` of the tile, fixed for the whole loop: no
+  // per-tile address arithmetic on the VALU, which the softmax saturates
+  // (the clamped form cost 33 VALU per tile, 8 of them quarter-rate
+  // multiplies).  Only a last tile that runs past Sk clamps per lane.
+  uint32_t kob[C::NINS / 4], vob[C::NINS / 4];
+#pragma unroll
+  for (int i = 0; i < C::NINS / 4; ++i) {
+    const int q = wv * (C::NINS / 4) + i;
+    const int key = q * C::RPI + lane / C::CPR, cp = lane % C::CPR;
+    kob[i] = (uint32_t)(((int64_t)key * k_ss + 8 * (cp ^ C::swz_k(key))) * 2);
+    vob[i] = (uint32_t)(((int64_t)key * v_ss + 8 * (cp ^ C::swz_v(key))) * 2);
+  }
   auto issue_kv = [&](int kv0, uint16_t* ks) __attribute__((always_inline)) {
     uint16_t* vs = ks + C::TILE;
+    if (kv0 + KT <= Sk) {
+      const char* kb = (const char*)(K + (int64_t)kv0 * k_ss);
+      const char* vb = (const char*)(V + (int64_t)kv0 * v_ss);
 #pragma unroll
-    for (int i = 0; i < C::NINS / 4; ++i) {
-      const int q = wv * (C::NINS / 4) + i;
-      const int key = q * C::RPI + lane / C::CPR, cp = lane % C::CPR;
-      const int gk = min(kv0 + key, Sk - 1);
-      __builtin_amdgcn_global_load_lds((const void*)(K + gk * k_ss + 8 * (cp ^ C::swz_k(key))),
-                                       (lds_void_t*)(ks + q * 512), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(V + gk * v_ss + 8 * (cp ^ C::swz_v(key))),
-                                       (lds_void_t*)(vs + q * 512), 16, 0, 0);
+      for (int i = 0; i < C::NINS / 4; ++i) {
+        const int q = wv * (C::NINS / 4) + i;
+        // the offsets enter each copy as 32-bit registers (hoisted out of the
+        // loop as 64-bit values they cost a 64-bit add per copy); the copy
+        // then takes the scalar base + 32-bit offset form
+        uint32_t ko = kob[i], vo = vob[i];
+        asm volatile("" : "+v"(ko), "+v"(vo));
+        __builtin_amdgcn_global_load_lds((const void*)(kb + ko), (lds_void_t*)(ks + q * 512), 16, 0,
+                                         0);
+        __builtin_amdgcn_global_load_lds((const void*)(vb + vo), (lds_void_t*)(vs + q * 512), 16, 0,
+                                         0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::NINS / 4; ++i) {
+        const int q = wv * (C::NINS / 4) + i;
+        const int key = q * C::RPI + lane / C::CPR, cp = lane % C::CPR;
+        const int gk = min(kv0 + key, Sk - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(K + gk * k_ss + 8 * (cp ^ C::swz_k(key))),
+                                         (lds_void_t*)(ks + q * 512), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(V + gk * v_ss + 8 * (cp ^ C::swz_v(key))),
+                                         (lds_void_t*)(vs + q * 512), 16, 0, 0);
+      }
     }
   };
   // K fragment k-step t of sub-tile st: key 32 st + col, chunk 2 t + half
