@@ -1,21 +1,24 @@
 // Matrix-vector product: out = beta * self + alpha * (mat @ vec), mat [M, K],
 // vec [K], out [M] (addmv; mv is addmv with beta = 0).
 //
-// HBM-bound on mat (read once).  One wave owns two rows of mat: its 64 lanes
-// read them in 16-byte non-temporal pieces, four per row in flight per lane,
-// multiply by the matching pieces of vec (read through the cache once for
-// both rows), accumulate in fp32, add the lanes in a fixed shuffle tree and
-// round once.  mat is used as [M, K] with
-// K contiguous; another layout (a transposed view, a leading dim that breaks
-// 16-byte alignment) is first copied densely into workspace, and so is a
-// strided vec.
+// HBM-bound on mat (read once).  One wave owns one row of mat: its 64 lanes
+// read it in 16-byte non-temporal pieces, eight in flight per lane (a whole
+// 8 KiB row of K = 4096 bf16 in one round), multiply by the matching pieces
+// of vec (read through the cache), accumulate in fp32, add the lanes in a
+// fixed shuffle tree and round once.  (On addmv [11008, 4096] one row per
+// wave and eight pieces a lane took 14.6 us against 16.7 us for two rows per
+// wave with four pieces each: twice the waves in flight, each with its loads
+// in one round; 16 pieces a lane, or 8 or 16 waves per block, were slower.)
+// mat is used as [M, K] with K contiguous; another layout (a transposed
+// view, a leading dim that breaks 16-byte alignment) is first copied densely
+// into workspace, and so is a strided vec.
 #include "iter.h"
 
 namespace mi {
 namespace {
 
-constexpr int kGemvRows = 4;  // waves per 256-lane block (two rows each)
-constexpr int kGemvUnroll = 8;
+constexpr int kGemvRows = 4;    // waves per 256-lane block (one row each)
+constexpr int kGemvUnroll = 8;  // 16-byte pieces in flight per lane
 
 struct GemvArgs {
   const void* mat;
@@ -32,33 +35,29 @@ template <typename Tag>
 __global__ __launch_bounds__(64 * kGemvRows) void gemv_rows_kernel(GemvArgs a) {
   typedef typename Num<Tag>::storage St;
   constexpr int VEC = 16 / sizeof(St);
-  constexpr int U = kGemvUnroll / 2;  // per row: two rows share each vec piece
+  constexpr int U = kGemvUnroll;
   union V {
     uint4 u;
     St s[VEC];
   };
   const int lane = threadIdx.x & 63;
-  const int64_t row0 = ((int64_t)blockIdx.x * kGemvRows + (threadIdx.x >> 6)) * 2;
-  if (row0 >= a.M) return;  // a whole wave
-  const bool two = row0 + 1 < a.M;
-  const St* p0 = (const St*)a.mat + row0 * a.lda;
-  const St* p1 = two ? p0 + a.lda : p0;
+  const int64_t row = (int64_t)blockIdx.x * kGemvRows + (threadIdx.x >> 6);
+  if (row >= a.M) return;  // a whole wave
+  const St* p = (const St*)a.mat + row * a.lda;
   const St* x = (const St*)a.vec;
-  float acc0 = 0.f, acc1 = 0.f;
+  float acc = 0.f;
   // the host checked: mat rows and vec 16-byte aligned
   const int64_t nv = a.K / VEC;
-  const V* pv0 = (const V*)p0;
-  const V* pv1 = (const V*)p1;
+  const V* pv = (const V*)p;
   const V* xv = (const V*)x;
   for (int64_t v0 = lane; v0 < nv; v0 += 64 * U) {
     // unconditional loads (a piece past the row end re-reads the last one and
     // is not used): under a per-piece branch each load was waited alone
-    V m0[U], m1[U], w[U];
+    V m[U], w[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t v = v0 + (int64_t)u * 64 < nv ? v0 + (int64_t)u * 64 : nv - 1;
-      m0[u] = ld_stream(pv0 + v);
-      m1[u] = ld_stream(pv1 + v);
+      m[u] = ld_stream(pv + v);
       w[u] = xv[v];
     }
     // keep the scheduler from pulling the multiplies between the loads (each
@@ -68,25 +67,17 @@ __global__ __launch_bounds__(64 * kGemvRows) void gemv_rows_kernel(GemvArgs a) {
     for (int u = 0; u < U; ++u) {
       if (v0 + (int64_t)u * 64 < nv) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float xe = Num<Tag>::load(w[u].s[e]);
-          acc0 = __builtin_fmaf(Num<Tag>::load(m0[u].s[e]), xe, acc0);
-          acc1 = __builtin_fmaf(Num<Tag>::load(m1[u].s[e]), xe, acc1);
-        }
+        for (int e = 0; e < VEC; ++e)
+          acc = __builtin_fmaf(Num<Tag>::load(m[u].s[e]), Num<Tag>::load(w[u].s[e]), acc);
       }
     }
   }
-  for (int64_t k = nv * VEC + lane; k < a.K; k += 64) {
-    const float xe = Num<Tag>::load(x[k]);
-    acc0 = __builtin_fmaf(Num<Tag>::load(p0[k]), xe, acc0);
-    acc1 = __builtin_fmaf(Num<Tag>::load(p1[k]), xe, acc1);
-  }
-  acc0 = wave_sum(acc0);
-  acc1 = wave_sum(acc1);
-  if (lane < 2 && (lane == 0 || two)) {
-    const int64_t row = row0 + lane;
+  for (int64_t k = nv * VEC + lane; k < a.K; k += 64)
+    acc = __builtin_fmaf(Num<Tag>::load(p[k]), Num<Tag>::load(x[k]), acc);
+  acc = wave_sum(acc);
+  if (lane == 0) {
     // alpha == 0 leaves mat and vec out, as BLAS gemv (and CPU ATen) do
-    float r = a.alpha != 0.f ? a.alpha * (lane == 0 ? acc0 : acc1) : 0.f;
+    float r = a.alpha != 0.f ? a.alpha * acc : 0.f;
     if (a.beta != 0.f) r += a.beta * load_as<float>(a.bias, row * a.bias_s, a.bias_dtype);
     ((St*)a.out)[row * a.out_s] = Num<Tag>::store(r);
   }
@@ -94,7 +85,7 @@ __global__ __launch_bounds__(64 * kGemvRows) void gemv_rows_kernel(GemvArgs a) {
 
 template <typename Tag>
 mi_status_t launch_gemv(const GemvArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_rows_kernel<Tag>), dim3(ceil_div_u(a.M, 2 * kGemvRows)),
+  hipLaunchKernelGGL((gemv_rows_kernel<Tag>), dim3(ceil_div_u(a.M, kGemvRows)),
                      dim3(64 * kGemvRows), 0, s, a);
   return check_launch("addmv");
 }
