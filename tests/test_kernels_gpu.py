@@ -93,6 +93,41 @@ def test_binary_parity(dtype, layout, op):
     assert_exact(out, ref, f"{op} {dtype} {layout}")
 
 
+# The typed 2-D path (dense rows of whole 16-byte vectors): a lane finds the
+# row and column of its vectors by one division and then steps when a row
+# holds at least 256 vectors, else divides each; ragged last blocks.
+@pytest.mark.parametrize("shape,dtype", [
+    ((33, 2048), torch.float32),    # 512 vectors a row: stepped
+    ((1031, 2048), torch.float32),  # stepped, last block ragged
+    ((7, 8192), torch.bfloat16),    # 1024 vectors a row, fewer vectors than one block
+    ((5, 1000), torch.float32),     # 250 vectors a row: divided
+    ((300, 1024), torch.bfloat16),  # 128 vectors a row: divided
+    ((1, 4096), torch.float32),     # one row
+])
+@pytest.mark.parametrize("layout", ["row", "col", "full", "scalar"])
+@pytest.mark.parametrize("op", ["add", "mul"])
+def test_binary_2d_path_parity(shape, dtype, layout, op):
+    a = rand(shape, dtype, 11)
+    if layout == "row":
+        b = rand(shape[-1:], dtype, 12)
+    elif layout == "col":
+        b = rand((shape[0], 1), dtype, 12)
+    elif layout == "full":
+        b = rand(shape, dtype, 12)
+    else:
+        b = 0.5
+    ref = getattr(aten, op)(a, b)
+    out = empty_like_ref(ref)
+    getattr(_abi, op)(out, dev(a), b if layout == "scalar" else dev(b))
+    assert_exact(out, ref, f"{op} {shape} {dtype} {layout}")
+    # the operand order swapped: the broadcast one first
+    if layout in ("row", "col"):
+        ref2 = getattr(aten, op)(b, a)
+        out2 = empty_like_ref(ref2)
+        getattr(_abi, op)(out2, dev(b), dev(a))
+        assert_exact(out2, ref2, f"{op} {shape} {dtype} {layout} swapped")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.int64,
                                    torch.int32, torch.uint8])
 @pytest.mark.parametrize("value", [0.5, 0.1, 3, -2])

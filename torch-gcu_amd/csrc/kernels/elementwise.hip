@@ -385,10 +385,14 @@ int mode_2d(const Iter& it, int o, int64_t rows, int64_t cols) {
   const int64_t s0 = it.ndim == 2 ? it.strides[o][0] : 0;
   const int64_t s1 = it.ndim == 2 ? it.strides[o][1] : it.strides[o][0];
   if (s0 == cols && s1 == 1) return M_FULL;
+  // one row (a coalesced 1-D iterator): a dense operand is the whole tensor,
+  // streamed as a full one (as a broadcast row it took the kernel with
+  // run-time layouts and cached loads: config 1's x + 0.5 ran 7 % slower
+  // than x * row)
+  if (rows == 1 && s1 == 1) return M_FULL;
   if (s0 == 0 && s1 == 1) return M_ROW;
   if (s0 == 1 && s1 == 0) return M_COL;
   if (s0 == 0 && s1 == 0) return M_SCALAR;
-  (void)rows;
   return -1;
 }
 
