@@ -363,8 +363,11 @@ mi_status_t mi_baddbmm(const mi_tensor_t* out, const mi_tensor_t* self,
  * (+ bias[n]); x and out bf16 or fp16 [M, K] / [M, N], w int8 [N, K], scales
  * fp32 [N], bias (optional, NULL data for none) broadcast to [M, N].  The
  * weight is widened to bf16/fp16 exactly on its way into LDS and multiplied
- * on MFMA with fp32 accumulation.  New efficient op: no TopsAten
- * counterpart. */
+ * on MFMA with fp32 accumulation.  For 64 < M <= 512 with too few 256 x 256
+ * tiles to fill the CUs, K is split and the fp32 partial sums (S x M x N
+ * floats, S = CUs / tiles, at most 16) come from the workspace allocator;
+ * they are added in a fixed slice order, so results do not depend on
+ * scheduling.  New efficient op: no TopsAten counterpart. */
 mi_status_t mi_int8_linear(const mi_tensor_t* out, const mi_tensor_t* x,
                            const mi_tensor_t* weight, const mi_tensor_t* scales,
                            const mi_tensor_t* bias, mi_stream_t stream);
