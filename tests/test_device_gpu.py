@@ -202,6 +202,37 @@ def test_graph_replay_matches_eager():
     graph.reset()
 
 
+def test_graph_replay_int8_linear_split_k():
+    """The int8 linear at M = 256 runs split-K: its fp32 partials come from
+    the workspace allocator inside the capture (the graph's pool).  Every
+    replay, with eager work on the same weights between replays, equals the
+    eager result bit-exactly."""
+    M, N, K = 256, 11008, 4096
+    x = (torch.randn(M, K, generator=g(40)) * 0.5).to(torch.bfloat16).to("gcu")
+    w = torch.randint(-127, 128, (N, K), generator=g(41), dtype=torch.int8).to("gcu")
+    sc = (torch.rand(N, generator=g(42)) * 0.01 + 0.001).to("gcu")
+    bias = torch.randn(N, generator=g(43)).to(torch.bfloat16).to("gcu")
+    lin = torch.gcu.efficient.int8_linear
+    eager = lin(x, w, sc, bias)
+    torch.gcu.synchronize()
+    graph = torch.gcu.GCUGraph()
+    with torch.gcu.graph(graph):
+        out = lin(x, w, sc, bias)
+    for k in range(3):
+        graph.replay()
+        torch.gcu.synchronize()
+        assert_exact(out.cpu(), eager.cpu(), f"int8 split-K replay {k}")
+        # eager work between replays: the same op outside the graph's pool
+        other = lin(x * 2, w, sc, None)
+        torch.gcu.synchronize()
+        del other
+    x.copy_((torch.randn(M, K, generator=g(44)) * 0.5).to(torch.bfloat16).to("gcu"))
+    graph.replay()
+    torch.gcu.synchronize()
+    assert_exact(out.cpu(), lin(x, w, sc, bias).cpu(), "int8 split-K replay with new input")
+    graph.reset()
+
+
 def test_graph_capture_rejects_default_stream_and_cpu_fallback():
     gr = torch.gcu.GCUGraph()
     with pytest.raises(RuntimeError, match="non-default stream"):
