@@ -65,6 +65,19 @@ def assert_close(actual: torch.Tensor, expected: torch.Tensor, kind: str, what: 
             f"first at {bad}: got {ad[i].item()} expected {ed[i].item()}")
 
 
+def bar_ratio(actual: torch.Tensor, expected: torch.Tensor, kind: str) -> float:
+    """max over finite elements of |d| / (rtol*|ref| + atol) under the bar
+    `kind`: assert_close passes exactly when this is <= 1 (and the non-finite
+    elements agree), so it shows the margin a passing result has."""
+    a, e = actual.cpu().double(), expected.cpu().double()
+    rtol, atol = bar(e, kind)
+    fin = torch.isfinite(e) & torch.isfinite(a)
+    if not bool(fin.any()):
+        return 0.0
+    r = (a - e).abs()[fin] / (rtol * e.abs()[fin] + atol).clamp_min(1e-300)
+    return float(r.max())
+
+
 def max_rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     a, e = actual.cpu().double(), expected.cpu().double()
     return float(((a - e).abs() / e.abs().clamp_min(1e-30)).max())

@@ -14,7 +14,7 @@ import torch.nn.functional as F
 import torch_gcu  # noqa: F401
 from oracle import aten
 from oracle import numpy_ref as npr
-from oracle.tolerance import assert_close, assert_composed_close, assert_exact
+from oracle.tolerance import assert_close, assert_composed_close, assert_exact, bar_ratio
 from torch_gcu import _abi
 from torch_gcu.utils import decoder_layer as dl
 
@@ -82,6 +82,45 @@ def test_flash_attention_scale_and_rescale(scale, ramp, causal):
     assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2 * max(1.0, ref_lse.abs().max().item())
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_attention_long_ramp_forces_late_rescales(causal):
+    """1024 keys (16 tiles) whose scale ramps from 0.2 to 8 along the
+    sequence: after the first 8 tiles (exact running max) the row max keeps
+    growing by more than 8 log2 units, so the late rescale branch runs, and
+    rows between two rescales carry p up to 2^8 into the P V product."""
+    B, H, S, D = 1, 2, 1024, 128
+    q, k, v = rn((B, H, S, D), 41), rn((B, H, S, D), 42), rn((B, H, S, D), 43)
+    k = (k.float() * torch.linspace(0.2, 8.0, S)[None, None, :, None]).to(torch.bfloat16)
+    # the late branch is reached: some row's scaled max grows by > 8 log2
+    # units after key 512 (checked on the fp32 scores of the first head)
+    s = (q[0, 0].float() @ k[0, 0].float().t()) * (D ** -0.5) * 1.4426950408889634
+    if causal:
+        s = s.masked_fill(torch.ones(S, S).triu(1).bool(), float("-inf"))
+    growth = s[:, 512:].amax(1) - s[:, :512].amax(1)
+    assert (growth > 8.0).any(), growth.max()
+    ref, ref_lse = ref_attention(q, k, v, causal)
+    out = torch.empty(B, H, S, D, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(B, H, S, dtype=torch.float32, device="cuda")
+    _abi.flash_attention_fwd(out, lse, q.cuda(), k.cuda(), v.cuda(), causal)
+    r = bar_ratio(out, ref, "bf16")
+    print(f"long ramp causal={causal}: max |error| / bar = {r:.3f}", flush=True)
+    assert_close(out, ref, "bf16", f"long ramp causal={causal}")
+    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2 * max(1.0, ref_lse.abs().max().item())
+
+
+def test_flash_attention_long_non_causal_keys():
+    """[1, 2, 128 x 2048, 128] non-causal: 32 key tiles, 24 of them past
+    the exact-max tiles."""
+    q, k, v = rn((1, 2, 128, 128), 44), rn((1, 2, 2048, 128), 45), rn((1, 2, 2048, 128), 46)
+    ref, ref_lse = ref_attention(q, k, v, False)
+    out = torch.empty(1, 2, 128, 128, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(1, 2, 128, dtype=torch.float32, device="cuda")
+    _abi.flash_attention_fwd(out, lse, q.cuda(), k.cuda(), v.cuda(), False)
+    print(f"long non-causal: max |error| / bar = {bar_ratio(out, ref, 'bf16'):.3f}", flush=True)
+    assert_close(out, ref, "bf16", "long non-causal")
+    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-2 * max(1.0, ref_lse.abs().max().item())
+
+
 def test_config5_attention_shape_head_sample():
     """[8, 32, 2048, 128] causal: all heads computed, 3 heads checked."""
     B, H, S, D = 8, 32, 2048, 128
@@ -91,6 +130,8 @@ def test_config5_attention_shape_head_sample():
     o = out.cpu()
     for b, h in [(0, 0), (3, 17), (7, 31)]:
         ref, _ = ref_attention(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], True)
+        r = bar_ratio(o[b:b + 1, h:h + 1], ref, "bf16")
+        print(f"config-5 head {b},{h}: max |error| / bar = {r:.3f}", flush=True)
         assert_close(o[b:b + 1, h:h + 1], ref, "bf16", f"head {b},{h}")
 
 
@@ -181,6 +222,54 @@ def test_config5_layer_full_shape_matches_cpu_per_sequence(c5_layer, b):
     assert out[rows].shape == ref.shape
     assert torch.isfinite(out[rows].float()).all()
     assert_composed_close(out[rows], ref, truth, f"config-5 layer, sequence {b}")
+
+
+def test_config5_layer_full_shape_under_op_check(c5_layer):
+    """The full B8 x S2048 layer with op_check on every native op: each call
+    runs on gcu, then on CPU ATen over host copies of its arguments, and the
+    outputs are compared at the bf16 op bar (rtol 1e-2; atol 1e-3, which the
+    test requires to be at most 1e-2 x the rms of every output compared
+    inexactly, so it is no looser than the bar's absolute floor; the
+    embedding gather and the adds must match bit for bit).  Op-check statistics
+    show what was compared: the projections at their three shapes (mm),
+    the embedding (index_select) and the residual adds.  The host copies
+    themselves (_copy_from) and the fused and attention ops have no CPU ATen
+    kernel under the same schema and are not op-checked (as in the
+    reference's YAML); their parity is tested above and in the kernel
+    tests.  The layer output under op_check equals the eager output bit
+    for bit (op_check returns the gcu result)."""
+    _, _, ids, wg, out = c5_layer
+    idg = ids.to("gcu")
+    C = torch_gcu._C
+    C._set_op_debug_config("op_check=all_ops op_check_tol_bf16=1e-2,1e-3 "
+                           "op_check_tol_fp32=1e-5,1e-5 op_statistics=true")
+    C._clear_op_check_statistics()
+    C._clear_op_statistics()
+    try:
+        got = dl.forward(wg, idg, C5).cpu()
+        checks = C._op_check_statistics()
+        info = C._get_op_statistics_info()
+    finally:
+        C._set_op_debug_config("")
+    for op, e in sorted(checks.items()):
+        print(f"op_check {op}: compared {e['compared']} failed {e['failed']} "
+              f"max |d|/tol {e['max_ratio']:.3f} min rms(ref) {e['min_ref_rms']:.4g}", flush=True)
+    assert checks["mm"]["compared"] == 7, checks
+    assert checks["index_select"]["compared"] == 1, checks
+    assert checks["add_Tensor"]["compared"] == 2, checks
+    for op, e in checks.items():
+        assert e["failed"] == 0 and e["max_ratio"] <= 1.0, (op, e)
+        if e["max_ratio"] > 0 and e["min_ref_rms"] >= 0:
+            assert 1e-3 <= 1e-2 * e["min_ref_rms"], (op, e)
+    # the gather and the residual adds (fp32 sum, one rounding) are bit-exact
+    assert checks["index_select"]["max_ratio"] == 0.0, checks
+    assert checks["add_Tensor"]["max_ratio"] == 0.0, checks
+    mm_lines = [ln for ln in info.splitlines() if "x (self=Tensor" in ln and "mat2=" in ln]
+    shapes = {(ln.split("shape")[1].split("]")[0], ln.split("mat2=Tensor(shape")[1].split("]")[0])
+              for ln in mm_lines}
+    assert shapes == {("[16384, 4096", "[4096, 4096"), ("[16384, 4096", "[4096, 11008"),
+                      ("[16384, 11008", "[11008, 4096")}, mm_lines
+    assert_exact(got, out, "layer under op_check equals eager")
 
 
 def test_config5_layer_full_shape_graph_replay_equals_eager(c5_layer):

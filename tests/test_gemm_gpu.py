@@ -59,18 +59,18 @@ def test_addmm_bias_alpha_beta(bias_shape):
     assert_close(out, ref, "bf16", "addmm fp32 bias")
 
 
-def test_config4_addmm_full_size_row_sample():
-    """M8192 N4096 K4096: every output checked on 64 sampled rows (exact
-    subset of the closed form) plus a column checksum."""
+def test_config4_addmm_full_size():
+    """M8192 N4096 K4096 with a row bias: the whole output against the fp32
+    closed form (275 GFLOP of CPU work, about a second on the box's cores),
+    plus a column checksum that is independent of the oracle's product."""
     M, N, K = 8192, 4096, 4096
     a, b, bias = rn((M, K), 7), rn((K, N), 8), rn((N,), 9)
     out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
     _abi.addmm(out, bias.cuda(), a.cuda(), b.cuda())
-    rows = torch.randperm(M, generator=g(10))[:64]
-    ref = aten.addmm(bias, a[rows], b)
-    assert_close(out.cpu()[rows], ref, "bf16", "addmm sampled rows")
+    got = out.cpu()
+    assert_close(got, aten.addmm(bias, a, b), "bf16", "addmm config 4, every output")
     # checksum: sum over rows of C equals (sum of A rows) @ B + M * bias
-    colsum = out.float().sum(0).cpu()
+    colsum = got.float().sum(0)
     want = (a.float().sum(0) @ b.float()) + M * bias.float()
     rel = ((colsum - want).norm() / want.norm()).item()
     assert rel < 2e-2, rel
@@ -124,12 +124,13 @@ def test_config4_int8_linear(M):
     assert_close(out, aten.int8_linear(x, w, scales), "bf16", f"int8 linear M={M}")
 
 
-def test_config4_int8_linear_m4096_row_sample():
+def test_config4_int8_linear_m4096_full():
+    """M=4096: the whole [4096, 11008] output against the fp32 closed form
+    (369 GFLOP of CPU work)."""
     x, w, scales = int8_inputs(4096)
     out = torch.empty(4096, w.shape[0], dtype=torch.bfloat16, device="cuda")
     _abi.int8_linear(out, x.cuda(), w.cuda(), scales.cuda())
-    rows = torch.randperm(4096, generator=g(30))[:48]
-    assert_close(out.cpu()[rows], aten.int8_linear(x[rows], w, scales), "bf16", "int8 M=4096 rows")
+    assert_close(out, aten.int8_linear(x, w, scales), "bf16", "int8 M=4096, every output")
 
 
 def test_int8_linear_edges_and_bias():

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import aten, numpy_ref as npr
-from oracle.tolerance import assert_close, assert_exact
+from oracle.tolerance import assert_close, assert_exact, bar, bar_ratio
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
@@ -574,3 +574,24 @@ def test_widened_fallback_vs_float64_closed_forms(low):
     assert bool(((got.double() - ref.double()).abs() <= ulp).all())
     # a planted mistake: forgetting to round the result back leaves float32
     assert torch.special.erfcx(x.float()).dtype != low
+
+
+def test_bar_ratio_agrees_with_assert_close():
+    """bar_ratio <= 1 exactly when assert_close passes: an error of k times
+    the bar at one element gives ratio k (hand-computed bar: rtol 1e-2 and
+    atol 1e-2 * rms of the reference)."""
+    e = torch.tensor([3.0, -4.0, 0.0, 0.5], dtype=torch.float64)
+    rms = math.sqrt((9 + 16 + 0 + 0.25) / 4)
+    assert bar(e, "bf16") == (1e-2, pytest.approx(1e-2 * rms))
+    for k in (0.5, 0.99, 1.01, 3.0):
+        a = e.clone()
+        a[2] = k * 1e-2 * rms  # error at the zero element is k times the floor
+        assert bar_ratio(a, e, "bf16") == pytest.approx(k)
+        if k <= 1:
+            assert_close(a, e, "bf16")
+        else:
+            with pytest.raises(AssertionError):
+                assert_close(a, e, "bf16")
+    a = e.clone()
+    a[1] = -4.0 * (1 + 2 * 1e-2) - 1e-2 * rms  # past rtol|ref| + atol by 4e-2
+    assert bar_ratio(a, e, "bf16") == pytest.approx((8e-2 + 1e-2 * rms) / (4e-2 + 1e-2 * rms))

@@ -140,3 +140,47 @@ def test_noalloc_mean_refuses_more_than_its_scratch():
     ref = torch.empty(4096, device="cuda")
     _abi.mean(ref, x, [0])
     assert_close(ref, aten.mean(x.cpu(), 0), "fp32", "mi_mean transposed")
+
+
+def _noalloc_on_current_gcu_stream(out, x, dims, keepdim=False):
+    arr, n = _abi._dims(dims)
+    st = _abi.lib().mi_mean_noalloc(_abi.desc(out), _abi.desc(x), arr, n, int(keepdim),
+                                    torch.gcu.current_stream().gcu_stream)
+    _abi.check("mi_mean_noalloc", st)
+
+
+def test_noalloc_mean_captured_in_a_gcu_graph_replays_equal_eager():
+    """A GCUGraph capture of mi_mean_noalloc on the capture side stream, on
+    config 2's mean over dim 0 (which takes 4 MiB of the scratch): the
+    scratch's address is fixed in the graph, so every replay must equal the
+    eager mean bit for bit although eager no-alloc calls on other inputs
+    overwrite the scratch between replays; no workspace request is made
+    during the capture or the replays."""
+    _abi.install_workspace()
+    x = rn((16384, 4096), 7).to("gcu")
+    small = rn((3000, 1000), 8).to("gcu")
+    eager = torch.mean(x, 0)  # mi_mean through the gcu dispatcher
+    eager_small = torch.mean(small, 0)
+    out = torch.full((4096,), float("nan"), device="gcu")
+    small_out = torch.empty(1000, device="gcu")
+    graph = torch.gcu.GCUGraph()
+    torch.gcu.synchronize()
+    with CountingWorkspace() as ws:
+        with torch.gcu.graph(graph):
+            _noalloc_on_current_gcu_stream(out, x, [0])
+        for k in range(3):
+            graph.replay()
+            torch.gcu.synchronize()
+            assert_exact(out.cpu(), eager.cpu(), f"no-alloc mean replay {k}")
+            # eager work between replays that rewrites the scratch
+            _noalloc_on_current_gcu_stream(small_out, small, [0])
+            torch.gcu.synchronize()
+            assert_exact(small_out.cpu(), eager_small.cpu(), f"eager no-alloc {k}")
+            out.fill_(float("nan"))
+        assert ws.allocs == 0, f"{ws.allocs} workspace requests"
+    x.copy_(rn((16384, 4096), 9).to("gcu"))
+    graph.replay()
+    torch.gcu.synchronize()
+    assert_exact(out.cpu(), torch.mean(x, 0).cpu(), "no-alloc mean replay with new input")
+    assert_close(out, aten.mean(rn((16384, 4096), 9), 0), "fp32", "replay vs CPU ATen")
+    graph.reset()

@@ -273,6 +273,19 @@ PYBIND11_MODULE(_C, m) {
     for (const auto& kv : op_statistics()) d[py::str(kv.first)] = py::make_tuple(kv.second.first, kv.second.second);
     return d;
   });
+  m.def("_op_check_statistics", []() {
+    py::dict d;
+    for (const auto& kv : op_check_statistics()) {
+      py::dict e;
+      e["compared"] = kv.second.compared;
+      e["failed"] = kv.second.failed;
+      e["max_ratio"] = kv.second.max_ratio;
+      e["min_ref_rms"] = kv.second.min_ref_rms;
+      d[py::str(kv.first)] = e;
+    }
+    return d;
+  });
+  m.def("_clear_op_check_statistics", &clear_op_check_statistics);
   m.def("_clear_op_statistics", &clear_op_statistics);
   m.def("_clear_statistics", &clear_op_statistics);
   m.def("_get_op_statistics_info", &op_statistics_info);

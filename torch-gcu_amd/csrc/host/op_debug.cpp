@@ -8,6 +8,7 @@
 #include <unistd.h>
 
 #include <chrono>
+#include <cmath>
 #include <cstdlib>
 #include <ctime>
 #include <filesystem>
@@ -635,8 +636,25 @@ at::ScalarType lower_float(at::ScalarType a, at::ScalarType b) {
   return rank(a) <= rank(b) ? a : b;
 }
 
+std::mutex g_check_mu;
+std::map<std::string, OpCheckStat> g_check_stats;
+
+void record_check(const std::string& op, bool ok, double ratio, double ref_rms) {
+  std::lock_guard<std::mutex> g(g_check_mu);
+  OpCheckStat& e = g_check_stats[op];
+  ++e.compared;
+  if (!ok) ++e.failed;
+  if (ratio > e.max_ratio) e.max_ratio = ratio;
+  if (ref_rms >= 0.0 && (e.min_ref_rms < 0.0 || ref_rms < e.min_ref_rms)) e.min_ref_rms = ref_rms;
+}
+
+// *ratio: max |a - b| / (atol + rtol |b|) over elements both finite (float
+// outputs), 0 or +inf for exact comparisons; *ref_rms: rms of b's finite
+// elements for float outputs, -1 otherwise.
 bool close_enough(const at::Tensor& dev, const at::Tensor& cpu, const OpDebugConfig& c,
-                  std::string* why) {
+                  std::string* why, double* ratio, double* ref_rms) {
+  *ratio = 0.0;
+  *ref_rms = -1.0;
   at::Tensor a = dev.detach().cpu();
   at::Tensor b = cpu.detach();
   if (a.sizes() != b.sizes()) {
@@ -653,6 +671,7 @@ bool close_enough(const at::Tensor& dev, const at::Tensor& cpu, const OpDebugCon
   bool equal_nan = true;
   if (!a.is_floating_point() && !a.is_complex()) {
     ok = a.eq(b);
+    if (!ok.all().item<bool>()) *ratio = INFINITY;
   } else {
     if (dt == at::kHalf) {
       rtol = c.rtol_fp16;
@@ -665,6 +684,15 @@ bool close_enough(const at::Tensor& dev, const at::Tensor& cpu, const OpDebugCon
     }
     ok = at::isclose(a.to(a.is_complex() ? a.scalar_type() : at::kDouble),
                      b.to(a.is_complex() ? a.scalar_type() : at::kDouble), rtol, atol, equal_nan);
+    if (!a.is_complex() && a.numel() > 0) {
+      const at::Tensor ad = a.to(at::kDouble), bd = b.to(at::kDouble);
+      const at::Tensor fin = at::isfinite(ad).logical_and(at::isfinite(bd));
+      if (fin.any().item<bool>()) {
+        const at::Tensor af = ad.masked_select(fin), bf = bd.masked_select(fin);
+        *ratio = ((af - bf).abs() / (bf.abs() * rtol + atol).clamp_min(1e-300)).max().item<double>();
+        *ref_rms = bf.pow(2).mean().sqrt().item<double>();
+      }
+    }
   }
   if (ok.all().item<bool>()) return true;
   // the first mismatching elements, as the reference lists them
@@ -745,12 +773,14 @@ void op_check_boxed(const c10::OperatorHandle& op, torch::jit::Stack* stack,
     if (!dev_out[i].defined() && !cpu_out[i].defined()) continue;
     std::string why;
     bool ok;
+    double ratio = INFINITY, ref_rms = -1.0;
     if (!dev_out[i].defined() || !cpu_out[i].defined()) {
       ok = false;
       why = "one of the gcu and cpu outputs is undefined";
     } else {
-      ok = close_enough(dev_out[i], cpu_out[i], cfg, &why);
+      ok = close_enough(dev_out[i], cpu_out[i], cfg, &why, &ratio, &ref_rms);
     }
+    record_check(cpp_name, ok, ratio, ref_rms);
     if (ok) continue;
     const int64_t err = g_check_err_idx.fetch_add(1);
     std::ostringstream os;
@@ -771,6 +801,16 @@ void op_check_boxed(const c10::OperatorHandle& op, torch::jit::Stack* stack,
     }
     break;
   }
+}
+
+std::map<std::string, OpCheckStat> op_check_statistics() {
+  std::lock_guard<std::mutex> g(g_check_mu);
+  return g_check_stats;
+}
+
+void clear_op_check_statistics() {
+  std::lock_guard<std::mutex> g(g_check_mu);
+  g_check_stats.clear();
 }
 
 // ---- fallback policy -----------------------------------------------------------------

@@ -99,6 +99,19 @@ void clear_op_statistics();
 std::string op_statistics_info();
 std::string dump_op_statistics_json();
 
+// op_check results per op (the reference logs "<op> acc check pass" for each
+// compared call, gcu_op_check.cpp:180-196): outputs compared, outputs outside
+// the tolerance, the largest |gcu - cpu| / (atol + rtol |cpu|) seen (0 for an
+// exact comparison that passed) and the smallest root-mean-square of a CPU
+// float output (so a caller can relate a fixed atol to the outputs' scale).
+struct OpCheckStat {
+  int64_t compared = 0, failed = 0;
+  double max_ratio = 0.0;
+  double min_ref_rms = -1.0;  // -1: no float output compared
+};
+std::map<std::string, OpCheckStat> op_check_statistics();
+void clear_op_check_statistics();
+
 // Saves the tensor and non-tensor arguments of a call under
 // <dir>/<prefix>_args<i>.pt / .txt (tensors loadable with torch.load).
 void dump_ivalues(const std::string& dir, const std::string& prefix,
