@@ -200,3 +200,223 @@ def test_pinned_host_allocator_bookkeeping():
     assert st["num_host_free"] == st["num_host_alloc"], st
     print("ok")
     """)
+
+
+# ---- history, snapshots, checkpoints and the rest of the allocator interface ----
+
+def test_base_allocation_and_cache_info():
+    """getBaseAllocation of a block split from a segment is the segment's
+    start and size (gcu_caching_allocator.cpp:861-880); cacheInfo reports the
+    largest free cached block (:936-950)."""
+    run("""
+    a = C._allocator_alloc(0, 3 * MiB, S1)      # 20 MiB segment, split
+    b = C._allocator_alloc(0, 5 * MiB, S1)      # the next piece of it
+    assert b == a + 3 * MiB
+    assert C._get_base_allocation(b) == (a, 20 * MiB)
+    assert C._get_base_allocation(a) == (a, 20 * MiB)
+    try:
+        C._get_base_allocation(a + 512)
+        raise SystemExit("an interior pointer was accepted")
+    except RuntimeError:
+        pass
+    # free cached: the 12 MiB tail of the segment; a start of 0 is replaced
+    # by the device's free memory, so ask from a start of 1 byte
+    assert C._cache_info_from(0, 1) == 12 * MiB
+    C._allocator_free(a)                         # 3 MiB free, not merged (b is live)
+    assert C._cache_info_from(0, 1) == 12 * MiB
+    C._allocator_free(b)                         # all merged: one 20 MiB free block
+    assert C._cache_info_from(0, 1) == 20 * MiB
+    assert C._cache_info(0) >= 20 * MiB          # starts from the fake device's free bytes
+    """)
+
+
+def test_check_pool_live_allocations():
+    """checkPoolLiveAllocations (:547-566) on a graph pool: true exactly when
+    the expected set equals the pool's allocated blocks."""
+    run("""
+    pool = C._allocator_new_pool()
+    C._allocator_begin_pool(0, pool[0], pool[1], S2)
+    x = C._allocator_alloc(0, 4096, S2)
+    y = C._allocator_alloc(0, 2 * MiB, S2)
+    C._allocator_end_pool(0, pool[0], pool[1])
+    z = C._allocator_alloc(0, 4096, S1)          # default pool, never counted
+    assert C._check_pool_live_allocations(0, pool, {x, y})
+    assert not C._check_pool_live_allocations(0, pool, {x})         # y is live too
+    assert not C._check_pool_live_allocations(0, pool, {x, y, z})   # z is not in the pool
+    C._allocator_free(x)
+    assert C._check_pool_live_allocations(0, pool, {y})
+    assert not C._check_pool_live_allocations(0, pool, {x, y})
+    try:
+        C._check_pool_live_allocations(0, (9, 9), set())
+        raise SystemExit("an unknown pool was accepted")
+    except RuntimeError:
+        pass
+    """)
+
+
+def test_checkpoint_restore_reproduces_pool_layout_and_stats():
+    """getCheckpointState / setCheckpointPoolState (:1007-1222): after the
+    checkpoint the pool's blocks change (frees, new allocations, a new
+    split); restoring frees what the pool holds now and re-creates the
+    checkpointed blocks at the same addresses, with the same allocated set
+    and the same statistics."""
+    run("""
+    pool = C._allocator_new_pool()
+    C._allocator_begin_pool(0, pool[0], pool[1], S2)
+    a = C._allocator_alloc(0, 1000, S2)
+    b = C._allocator_alloc(0, 3000, S2)
+    c = C._allocator_alloc(0, 5000, S2)
+    big = C._allocator_alloc(0, 12 * MiB, S2)
+    C._allocator_free(b)                      # a hole between a and c
+    ck = C._get_checkpoint_state(0, pool)
+    layout = [list(seg) for seg in ck.segments]
+    assert ck.pool_id == tuple(pool) and len(layout) == 2, layout
+    def pool_layout():
+        return [[(bl["address"], bl["size"], bl["state"] == "active_allocated")
+                 for bl in s["blocks"]] for s in sorted(C._memory_snapshot(), key=lambda s: s["address"])
+                if tuple(s["segment_pool_id"]) == tuple(pool)]
+    assert pool_layout() == [[tuple(b) for b in seg] for seg in layout]
+    keys = ["allocated_bytes.all.current", "allocation.all.current", "active_bytes.all.current",
+            "inactive_split.all.current", "inactive_split_bytes.all.current",
+            "reserved_bytes.all.current", "segment.all.current"]
+    before = {k: st()[k] for k in keys}
+    # change the pool: free a and big, allocate new blocks with other sizes
+    C._allocator_free(a); C._allocator_free(big)
+    d = C._allocator_alloc(0, 7000, S2)
+    e = C._allocator_alloc(0, 2 * MiB + 512, S2)
+    assert pool_layout() != [[tuple(b) for b in seg] for seg in layout]
+    try:
+        C._set_checkpoint_pool_state(0, ck)   # storage form: d and e would go stale unnamed
+        raise SystemExit("the restore did not ask for the stale storages")
+    except RuntimeError as err:
+        assert "stale" in str(err)
+    assert pool_layout() != [[tuple(b) for b in seg] for seg in layout]   # nothing changed
+    freed, allocd = C._set_checkpoint_pool_state_raw(0, ck)
+    assert sorted(freed) == sorted([c, d, e]), (freed, [c, d, e])
+    assert sorted(allocd) == sorted([a, c, big])
+    assert pool_layout() == [[tuple(b) for b in seg] for seg in layout]
+    assert {k: st()[k] for k in keys} == before
+    # the restored blocks are ordinary live allocations again
+    assert C._check_pool_live_allocations(0, pool, {a, c, big})
+    C._allocator_end_pool(0, pool[0], pool[1])
+    for p in (a, c, big):
+        C._allocator_free(p)
+    assert st()["allocated_bytes.all.current"] == 0
+    """)
+
+
+def test_memory_history_records_events_with_stacks():
+    """_record_memory_history (:531-546, memory.py:635-690): alloc,
+    free_requested, free_completed, segment_alloc, segment_free and snapshot
+    events with their addresses and sizes, Python frames of the calls, a
+    ring of max_entries, and nothing after recording stops."""
+    run('''
+    import torch_gcu.gcu.memory as M
+    def make_block():
+        return C._allocator_alloc(0, 3 * MiB, S1)
+    M._record_memory_history("all", context="all", stacks="python")
+    assert C._is_history_enabled()
+    a = make_block()
+    C._allocator_free(a)
+    C._empty_cache()
+    snap = M._snapshot()
+    tr = snap["device_traces"][0]
+    acts = [e["action"] for e in tr]
+    assert acts == ["segment_alloc", "alloc", "free_requested", "free_completed",
+                    "segment_free", "snapshot"], acts
+    seg_alloc, alloc = tr[0], tr[1]
+    assert alloc["addr"] == a and alloc["size"] == 3 * MiB and alloc["stream"] == S1
+    assert seg_alloc["addr"] == a and seg_alloc["size"] == 20 * MiB
+    assert tr[4]["addr"] == a and tr[4]["size"] == 20 * MiB
+    names = [f["name"] for f in alloc["frames"]]
+    assert "make_block" in names, alloc["frames"]
+    assert all(e["time_us"] >= tr[0]["time_us"] for e in tr)
+    # live blocks carry the stack that allocated them
+    b = make_block()
+    snap = M._snapshot()
+    blk = [bl for s in snap["segments"] for bl in s["blocks"] if bl["address"] == b][0]
+    assert blk["state"] == "active_allocated" and blk["requested_size"] == 3 * MiB
+    assert "make_block" in [f["name"] for f in blk["frames"]]
+    assert set(snap["allocator_settings"]) >= {"max_split_size", "expandable_segments"}
+    C._allocator_free(b)
+    # a ring of 4 entries keeps the last 4 events
+    M._record_memory_history("all", max_entries=4)
+    for _ in range(3):
+        C._allocator_free(make_block())
+    tr = M._snapshot()["device_traces"][0]
+    assert len(tr) == 4 and tr[-1]["action"] == "snapshot", [e["action"] for e in tr]
+    # context=None: events but no stacks (stopping first drops the history)
+    M._record_memory_history(None)
+    M._record_memory_history("all", context=None)
+    C._allocator_free(make_block())
+    tr = M._snapshot()["device_traces"][0]
+    assert tr and all(e["frames"] == [] for e in tr)
+    M._record_memory_history(None)
+    assert not C._is_history_enabled()
+    C._allocator_free(make_block())
+    assert M._snapshot()["device_traces"][0] == []
+    # the legacy boolean form
+    M._record_memory_history(True, trace_alloc_max_entries=100, trace_alloc_record_context=True)
+    C._allocator_free(make_block())
+    assert [e["action"] for e in M._snapshot()["device_traces"][0]][:2] == ["alloc", "free_requested"]
+    M._record_memory_history(False)
+    for bad in [dict(enabled="x"), dict(context="x"), dict(stacks="x")]:
+        try:
+            M._record_memory_history(**{**dict(enabled="all"), **bad})
+            raise SystemExit("accepted " + repr(bad))
+        except RuntimeError:
+            pass
+    ''')
+
+
+def test_dump_snapshot_pickle_and_summary(tmp_path):
+    out = run(f'''
+    import pickle
+    import torch_gcu.gcu.memory as M
+    M._record_memory_history("all")
+    a = C._allocator_alloc(0, 4096, S1)
+    M._dump_snapshot({str(tmp_path / "snap.pickle")!r})
+    with open({str(tmp_path / "snap.pickle")!r}, "rb") as f:
+        s = pickle.load(f)
+    assert [e["action"] for e in s["device_traces"][0]] == ["segment_alloc", "alloc", "snapshot"]
+    assert s["segments"][0]["blocks"][0]["address"] == a
+    nested = M.memory_stats_as_nested_dict(0)
+    assert nested["allocated_bytes"]["all"]["current"] == 4096
+    assert nested["segment"]["small_pool"]["current"] == 1
+    assert nested["num_device_alloc"] == 1
+    text = M.memory_summary(0)
+    assert "Allocated memory" in text and "from small pool" in text
+    row = [l for l in text.splitlines() if l.startswith("| Allocations")][0]
+    assert row.split("|")[2].strip() == "1", row
+    assert "from small pool" not in M.memory_summary(0, abbreviated=True)
+    print("ok")
+    ''')
+    assert "ok" in out
+
+
+def test_mem_pool_routes_one_threads_allocations():
+    """use_mem_pool (memory.py:914-934): inside the block the calling
+    thread's allocations come from the pool's own segments; another thread's
+    do not; after the block the pool's memory returns once it is freed."""
+    run("""
+    import threading
+    import torch_gcu.gcu.memory as M
+    pool = M.MemPool()
+    other = []
+    with M.use_mem_pool(pool, device=0):
+        assert pool.use_count() == 1
+        a = C._caching_allocator_alloc(0, 4096, S1)
+        t = threading.Thread(target=lambda: other.append(C._caching_allocator_alloc(0, 4096, S1)))
+        t.start(); t.join()
+    assert pool.use_count() == 0
+    owner = {bl["address"]: tuple(s["segment_pool_id"]) for s in C._memory_snapshot()
+             for bl in s["blocks"]}
+    assert owner[a] == pool.id and owner[other[0]] == (0, 0), (owner, pool.id)
+    assert [s["address"] for s in pool.snapshot()] == [a]
+    b = C._caching_allocator_alloc(0, 4096, S1)       # outside the block: default pool
+    assert b != a and {tuple(s["segment_pool_id"]) for s in C._memory_snapshot()
+                       if s["address"] <= b < s["address"] + s["total_size"]} == {(0, 0)}
+    C._caching_allocator_delete(a)                     # the released pool's segment goes back
+    assert pool.snapshot() == []
+    C._caching_allocator_delete(b); C._caching_allocator_delete(other[0])
+    """)

@@ -26,6 +26,8 @@
 #include <c10/util/Exception.h>
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cstdlib>
 #include <deque>
 #include <map>
@@ -65,6 +67,8 @@ struct Block {
   Block* next = nullptr;
   std::vector<hipStream_t> stream_uses;
   int event_count = 0;
+  Context context;      // stack of the allocation (history with context on)
+  Context seg_context;  // on a segment's first block: stack of the segment's creation
   bool is_split() const { return prev != nullptr || next != nullptr; }
 };
 
@@ -101,6 +105,25 @@ bool g_fake = false;
 size_t g_fake_capacity = 0;
 size_t g_fake_used = 0;
 
+// History settings shared by every device: read outside the device locks
+// (to gather a stack before taking one), so kept in atomics.
+std::atomic<bool> g_hist_on{false};
+std::atomic<int> g_hist_when{(int)RecordContext::NEVER};
+std::atomic<ContextFn> g_hist_fn{nullptr};
+std::atomic<size_t> g_hist_max{1};
+
+Context gather_if(RecordContext level) {
+  if (!g_hist_on.load() || g_hist_when.load() < (int)level) return nullptr;
+  const ContextFn fn = g_hist_fn.load();
+  return fn ? fn() : nullptr;
+}
+
+int64_t now_us() {
+  return std::chrono::duration_cast<std::chrono::microseconds>(
+             std::chrono::system_clock::now().time_since_epoch())
+      .count();
+}
+
 size_t stat_index(bool small) { return small ? 1 : 2; }
 
 std::string fmt_bytes(size_t n) {
@@ -126,10 +149,14 @@ size_t round_power2_divisions(size_t size, size_t divisions) {
 
 class DeviceAllocator {
  public:
-  explicit DeviceAllocator(int device) : device_(device), large_(false, nullptr), small_(true, nullptr) {}
+  explicit DeviceAllocator(int device)
+      : device_(device), large_(false, nullptr), small_(true, nullptr), trace_max_(g_hist_max.load()) {}
 
-  Block* malloc(size_t orig, hipStream_t stream) {
+  // `ctx`: the caller's stack, gathered before the lock when history keeps
+  // contexts (null otherwise).
+  Block* malloc(size_t orig, hipStream_t stream, Context ctx = nullptr) {
     std::lock_guard<std::recursive_mutex> g(mu_);
+    OpContext oc(this, ctx);
     if (capturing_.empty()) process_events();
     const size_t size = round_size(orig);
     BlockPool& pool = get_pool(size, stream);
@@ -145,42 +172,15 @@ class DeviceAllocator {
       }
       if (block == nullptr) raise_oom(orig, alloc_size);
     } else {
-      pool.blocks.erase(block);
-      if (block->is_split()) {  // it was counted as an inactive split
-        stat_sub(stats_.inactive_split, pool.is_small, 1);
-        stat_sub(stats_.inactive_split_bytes, pool.is_small, (int64_t)block->size);
-      }
+      take_free(pool, block);
     }
     // split off the remainder when it is worth keeping
     const size_t remaining = block->size - size;
     const bool split = pool.is_small ? remaining >= kMinBlockSize
                                      : (remaining > kSmallSize && size < g_config.max_split_size);
-    if (split) {
-      Block* rest = new Block(*block);
-      rest->ptr = (char*)block->ptr + size;
-      rest->size = remaining;
-      rest->prev = block;
-      rest->next = block->next;
-      rest->allocated = false;
-      rest->stream_uses.clear();
-      rest->event_count = 0;
-      if (rest->next) rest->next->prev = rest;
-      block->next = rest;
-      block->size = size;
-      pool.blocks.insert(rest);
-      stat_add(stats_.inactive_split, pool.is_small, 1);
-      stat_add(stats_.inactive_split_bytes, pool.is_small, (int64_t)remaining);
-    }
-    block->allocated = true;
-    block->requested = orig;
-    block->stream = stream;
-    active_[block->ptr] = block;
-    if (pool.owner) pool.owner->allocation_count++;
-    stat_add(stats_.allocation, pool.is_small, 1);
-    stat_add(stats_.allocated_bytes, pool.is_small, (int64_t)block->size);
-    stat_add(stats_.active, pool.is_small, 1);
-    stat_add(stats_.active_bytes, pool.is_small, (int64_t)block->size);
-    stat_add(stats_.requested_bytes, pool.is_small, (int64_t)orig);
+    if (split) split_block(pool, block, size);
+    mark_allocated(pool, block, orig, stream);
+    record(TraceAction::ALLOC, block->ptr, (int64_t)orig, stream, RecordContext::ALLOC);
     return block;
   }
 
@@ -189,11 +189,14 @@ class DeviceAllocator {
     return active_.count(p) != 0;
   }
 
-  void free(void* p) {
+  void free(void* p, Context ctx = nullptr) {
     std::lock_guard<std::recursive_mutex> g(mu_);
+    OpContext oc(this, ctx);
     auto it = active_.find(p);
     TORCH_CHECK(it != active_.end(), "gcu allocator: invalid device pointer ", p);
     Block* b = it->second;
+    record(TraceAction::FREE_REQUESTED, b->ptr, (int64_t)b->requested, b->stream,
+           RecordContext::ALL);
     active_.erase(it);
     b->allocated = false;
     const bool small = b->pool->is_small;
@@ -224,8 +227,9 @@ class DeviceAllocator {
       b->stream_uses.push_back(s);
   }
 
-  void empty_cache() {
+  void empty_cache(Context ctx = nullptr) {
     std::lock_guard<std::recursive_mutex> g(mu_);
+    OpContext oc(this, ctx);
     if (!capturing_.empty()) return;
     release_cached();
   }
@@ -265,24 +269,183 @@ class DeviceAllocator {
     stats_.num_ooms = 0;
   }
 
-  void snapshot(std::vector<SegmentInfo>& out) {
+  // Segments in address order.  `mark`: record a SNAPSHOT history event.
+  void snapshot(std::vector<SegmentInfo>& out, bool mark = false) {
     std::lock_guard<std::recursive_mutex> g(mu_);
-    for (Block* head : segments_) {
+    std::vector<Block*> heads(segments_.begin(), segments_.end());
+    std::sort(heads.begin(), heads.end(),
+              [](const Block* a, const Block* b) { return (uintptr_t)a->ptr < (uintptr_t)b->ptr; });
+    for (Block* head : heads) {
       SegmentInfo si;
       si.device = device_;
       si.address = (uintptr_t)head->ptr;
       si.is_large = !head->pool->is_small;
       si.stream = (uintptr_t)head->stream;
-      for (auto& kv : graph_pools_)
-        if (head->pool->owner == kv.second.get()) si.owner_pool = kv.first;
+      si.context = head->seg_context;
+      si.owner_pool = pool_id_of(head->pool->owner);
       for (Block* b = head; b; b = b->next) {
+        BlockInfo bi;
+        bi.address = (uintptr_t)b->ptr;
+        bi.size = b->size;
+        bi.allocated = b->allocated;
+        bi.active = b->allocated || b->event_count > 0;
+        bi.requested_size = bi.active ? b->requested : 0;
+        bi.context = bi.active ? b->context : nullptr;
         si.total_size += b->size;
         if (b->allocated) si.allocated_size += b->size;
-        if (b->allocated || b->event_count > 0) si.active_size += b->size;
-        si.blocks.push_back({b->size, b->allocated});
+        if (bi.active) {
+          si.active_size += b->size;
+          si.requested_size += b->requested;
+        }
+        si.blocks.push_back(std::move(bi));
       }
-      out.push_back(si);
+      out.push_back(std::move(si));
     }
+    if (mark) record(TraceAction::SNAPSHOT, nullptr, 0, nullptr, RecordContext::NEVER);
+  }
+
+  // The history, oldest entry first.
+  std::vector<TraceEntry> trace() {
+    std::lock_guard<std::recursive_mutex> g(mu_);
+    std::vector<TraceEntry> out;
+    out.reserve(trace_.size());
+    for (size_t i = 0; i < trace_.size(); ++i) out.push_back(trace_[(trace_next_ + i) % trace_.size()]);
+    return out;
+  }
+
+  void set_history(bool enabled, size_t max_entries) {
+    std::lock_guard<std::recursive_mutex> g(mu_);
+    if (!enabled || max_entries < trace_.size()) {
+      trace_.clear();
+      trace_next_ = 0;
+    }
+    trace_max_ = std::max<size_t>(1, max_entries);
+  }
+
+  void cache_info(size_t* largest) {
+    std::lock_guard<std::recursive_mutex> g(mu_);
+    if (*largest == 0) {
+      size_t total = 0;
+      device_mem_info(largest, &total);  // optimistic start: the device's free memory
+    }
+    auto scan = [&](const BlockPool& p) {
+      for (const Block* b : p.blocks) *largest = std::max(*largest, b->size);
+    };
+    scan(large_);
+    scan(small_);
+    for (auto& kv : graph_pools_) {
+      scan(kv.second->large);
+      scan(kv.second->small);
+    }
+  }
+
+  void* base_allocation(void* p, size_t* size) {
+    std::lock_guard<std::recursive_mutex> g(mu_);
+    auto it = active_.find(p);
+    TORCH_CHECK(it != active_.end(), "gcu allocator: invalid device pointer ", p);
+    Block* b = it->second;
+    while (b->prev) b = b->prev;
+    if (size) {
+      size_t n = 0;
+      for (Block* c = b; c; c = c->next) n += c->size;
+      *size = n;
+    }
+    return b->ptr;
+  }
+
+  bool check_pool_live(MempoolId id, const std::unordered_set<void*>& expected) {
+    std::lock_guard<std::recursive_mutex> g(mu_);
+    auto it = graph_pools_.find(id);
+    TORCH_CHECK(it != graph_pools_.end(), "gcu allocator: no memory pool (", id.first, ", ",
+                id.second, ")");
+    size_t live = 0;
+    for (const auto& kv : active_) {
+      if (kv.second->pool->owner != it->second.get()) continue;
+      if (!expected.count(kv.first)) return false;
+      ++live;
+    }
+    return live == expected.size();
+  }
+
+  std::shared_ptr<PoolState> checkpoint(MempoolId id) {
+    std::lock_guard<std::recursive_mutex> g(mu_);
+    TORCH_CHECK(!freeable_.count(id), "gcu allocator: pool (", id.first, ", ", id.second,
+                ") was released; it cannot be checkpointed");
+    auto it = graph_pools_.find(id);
+    TORCH_CHECK(it != graph_pools_.end(), "gcu allocator: no memory pool (", id.first, ", ",
+                id.second, ")");
+    auto st = std::make_shared<PoolState>();
+    st->device = device_;
+    st->id = id;
+    for (Block* head : pool_segments(it->second.get())) {
+      std::vector<BlockState> seg;
+      for (Block* b = head; b; b = b->next)
+        seg.push_back({(uintptr_t)b->ptr, b->size, b->allocated, (uintptr_t)b->stream});
+      st->segments.push_back(std::move(seg));
+    }
+    return st;
+  }
+
+  // Returns the pool to a checkpointed layout: every block of the pool
+  // allocated now is freed, then each checkpointed segment is cut into its
+  // recorded blocks again and the blocks that were allocated are allocated.
+  CheckpointDelta restore(const PoolState& st) {
+    std::lock_guard<std::recursive_mutex> g(mu_);
+    OpContext oc(this, nullptr);
+    TORCH_CHECK(!freeable_.count(st.id), "gcu allocator: pool (", st.id.first, ", ",
+                st.id.second, ") was released; it cannot be restored");
+    auto it = graph_pools_.find(st.id);
+    TORCH_CHECK(it != graph_pools_.end(), "gcu allocator: no memory pool (", st.id.first, ", ",
+                st.id.second, ")");
+    PrivatePool* pool = it->second.get();
+    CheckpointDelta delta;
+    // 1. free what the pool holds now (no stream may still be using it)
+    for (Block* head : pool_segments(pool)) {
+      std::vector<Block*> live;
+      for (Block* b = head; b; b = b->next)
+        if (b->allocated) live.push_back(b);
+      for (Block* b : live) {
+        TORCH_CHECK(b->stream_uses.empty() && b->event_count == 0,
+                    "gcu allocator: a block of the pool is still in use on another stream");
+        delta.freed.push_back(b->ptr);
+        free(b->ptr);
+      }
+    }
+    // 2. every segment of the pool is now one free block
+    std::unordered_map<uintptr_t, Block*> free_heads;
+    for (BlockPool* bp : {&pool->small, &pool->large})
+      for (Block* b : bp->blocks) free_heads[(uintptr_t)b->ptr] = b;
+    // 3. cut and allocate each checkpointed segment
+    for (const auto& seg : st.segments) {
+      TORCH_CHECK(!seg.empty(), "gcu allocator: empty segment in a pool checkpoint");
+      auto fh = free_heads.find(seg[0].ptr);
+      TORCH_CHECK(fh != free_heads.end(), "gcu allocator: segment ", (void*)seg[0].ptr,
+                  " of the checkpoint is not a free segment of the pool");
+      Block* cur = fh->second;
+      BlockPool& bp = *cur->pool;
+      std::vector<Block*> blocks;
+      for (size_t i = 0; i < seg.size(); ++i) {
+        TORCH_CHECK(cur != nullptr && (uintptr_t)cur->ptr == seg[i].ptr && cur->size >= seg[i].size,
+                    "gcu allocator: the pool's segment does not match the checkpoint");
+        take_free(bp, cur);
+        if (i + 1 < seg.size()) split_block(bp, cur, seg[i].size);
+        TORCH_CHECK(cur->size == seg[i].size,
+                    "gcu allocator: the pool's segment does not match the checkpoint");
+        mark_allocated(bp, cur, seg[i].size, (hipStream_t)seg[i].stream);
+        blocks.push_back(cur);
+        cur = cur->next;
+      }
+      TORCH_CHECK(cur == nullptr, "gcu allocator: the pool's segment is longer than the checkpoint");
+      // 4. free the blocks that were free in the checkpoint
+      for (size_t i = 0; i < seg.size(); ++i) {
+        if (seg[i].allocated) {
+          delta.allocated.push_back(blocks[i]->ptr);
+          continue;
+        }
+        free(blocks[i]->ptr);
+      }
+    }
+    return delta;
   }
 
   void begin_pool(MempoolId id, std::function<bool(hipStream_t)> filter) {
@@ -292,6 +455,7 @@ class DeviceAllocator {
       graph_pools_[id] = std::make_unique<PrivatePool>();
     } else {
       it->second->use_count++;
+      freeable_.erase(id);  // used again before its memory was returned
     }
     capturing_.push_back({id, std::move(filter)});
   }
@@ -319,6 +483,95 @@ class DeviceAllocator {
   }
 
  private:
+  // The stack of the public call in progress (set under the lock), for the
+  // history entries of the helpers it runs.
+  struct OpContext {
+    OpContext(DeviceAllocator* a, Context c) : a_(a), prev_(std::move(a->op_ctx_)) {
+      a_->op_ctx_ = std::move(c);
+    }
+    ~OpContext() { a_->op_ctx_ = std::move(prev_); }
+    DeviceAllocator* a_;
+    Context prev_;
+  };
+
+  void record(TraceAction action, const void* addr, int64_t size, hipStream_t stream,
+              RecordContext level) {
+    if (!g_hist_on.load()) return;
+    TraceEntry e;
+    e.action = action;
+    e.device = device_;
+    e.addr = (uintptr_t)addr;
+    e.size = size;
+    e.stream = (uintptr_t)stream;
+    e.time_us = now_us();
+    if (level != RecordContext::NEVER && g_hist_when.load() >= (int)level) e.context = op_ctx_;
+    if (trace_.size() < trace_max_) {
+      trace_.push_back(std::move(e));
+    } else {
+      trace_[trace_next_] = std::move(e);
+      trace_next_ = (trace_next_ + 1) % trace_max_;
+    }
+  }
+
+  MempoolId pool_id_of(const PrivatePool* p) const {
+    if (p == nullptr) return {0, 0};
+    for (const auto& kv : graph_pools_)
+      if (kv.second.get() == p) return kv.first;
+    return {0, 0};
+  }
+
+  // First blocks of the pool's segments, in address order.
+  std::vector<Block*> pool_segments(const PrivatePool* p) const {
+    std::vector<Block*> out;
+    for (Block* head : segments_)
+      if (head->pool->owner == p) out.push_back(head);
+    std::sort(out.begin(), out.end(),
+              [](const Block* a, const Block* b) { return (uintptr_t)a->ptr < (uintptr_t)b->ptr; });
+    return out;
+  }
+
+  // Takes a cached free block out of its pool.
+  void take_free(BlockPool& pool, Block* block) {
+    pool.blocks.erase(block);
+    if (block->is_split()) {  // it was counted as an inactive split
+      stat_sub(stats_.inactive_split, pool.is_small, 1);
+      stat_sub(stats_.inactive_split_bytes, pool.is_small, (int64_t)block->size);
+    }
+  }
+
+  // Cuts `block` (out of the pool) to `size`; the rest goes back to the pool.
+  void split_block(BlockPool& pool, Block* block, size_t size) {
+    const size_t remaining = block->size - size;
+    Block* rest = new Block();
+    rest->device = block->device;
+    rest->stream = block->stream;
+    rest->pool = block->pool;
+    rest->ptr = (char*)block->ptr + size;
+    rest->size = remaining;
+    rest->prev = block;
+    rest->next = block->next;
+    if (rest->next) rest->next->prev = rest;
+    block->next = rest;
+    block->size = size;
+    pool.blocks.insert(rest);
+    stat_add(stats_.inactive_split, pool.is_small, 1);
+    stat_add(stats_.inactive_split_bytes, pool.is_small, (int64_t)remaining);
+  }
+
+  void mark_allocated(BlockPool& pool, Block* block, size_t orig, hipStream_t stream) {
+    block->allocated = true;
+    block->requested = orig;
+    block->stream = stream;
+    block->context = g_hist_when.load() >= (int)RecordContext::STATE ? op_ctx_ : nullptr;
+    active_[block->ptr] = block;
+    if (pool.owner) pool.owner->allocation_count++;
+    stat_add(stats_.allocation, pool.is_small, 1);
+    stat_add(stats_.allocated_bytes, pool.is_small, (int64_t)block->size);
+    stat_add(stats_.active, pool.is_small, 1);
+    stat_add(stats_.active_bytes, pool.is_small, (int64_t)block->size);
+    stat_add(stats_.requested_bytes, pool.is_small, (int64_t)orig);
+  }
+
   void stat_add(std::array<Stat, 3>& s, bool small, int64_t n) {
     s[0].inc(n);
     s[stat_index(small)].inc(n);
@@ -406,6 +659,8 @@ class DeviceAllocator {
     b->size = size;
     b->ptr = p;
     b->pool = &pool;
+    b->seg_context = g_hist_when.load() >= (int)RecordContext::STATE ? op_ctx_ : nullptr;
+    record(TraceAction::SEGMENT_ALLOC, p, (int64_t)size, stream, RecordContext::ALLOC);
     reserved_total_ += size;
     segments_.insert(b);
     stat_add(stats_.segment, pool.is_small, 1);
@@ -472,6 +727,9 @@ class DeviceAllocator {
     BlockPool& pool = *b->pool;
     const bool small = pool.is_small;
     const int64_t orig_size = (int64_t)b->size;
+    record(TraceAction::FREE_COMPLETED, b->ptr, (int64_t)b->requested, b->stream,
+           RecordContext::ALL);
+    b->context.reset();
     int64_t merged_inactive = 0;
     for (Block* nb : {b->prev, b->next}) {
       if (nb == nullptr || nb->allocated || nb->event_count > 0) continue;
@@ -483,7 +741,10 @@ class DeviceAllocator {
         b->ptr = nb->ptr;
         b->prev = nb->prev;
         if (b->prev) b->prev->next = b;
-        if (segments_.erase(nb)) segments_.insert(b);
+        if (segments_.erase(nb)) {
+          segments_.insert(b);
+          b->seg_context = std::move(nb->seg_context);
+        }
       } else {
         b->next = nb->next;
         if (b->next) b->next->prev = b;
@@ -517,6 +778,7 @@ class DeviceAllocator {
   }
 
   void release_segment(Block* b) {
+    record(TraceAction::SEGMENT_FREE, b->ptr, (int64_t)b->size, b->stream, RecordContext::ALL);
     if (g_fake) {
       std::free(b->ptr);
       g_fake_used -= b->size;
@@ -576,6 +838,10 @@ class DeviceAllocator {
   std::deque<std::pair<hipEvent_t, Block*>> events_;
   std::vector<Block*> deferred_;
   DeviceStats stats_;
+  Context op_ctx_;
+  std::vector<TraceEntry> trace_;  // ring of at most trace_max_ entries
+  size_t trace_max_;
+  size_t trace_next_ = 0;          // oldest entry once the ring is full
   size_t limit_ = SIZE_MAX;
   double fraction_ = 1.0;
   size_t reserved_total_ = 0;
@@ -601,6 +867,8 @@ void DeviceAllocator::raise_oom(size_t requested, size_t alloc_size) {
   ++stats_.num_ooms;
   size_t free_b = 0, total = 0;
   device_mem_info(&free_b, &total);
+  record(TraceAction::OOM, (const void*)(uintptr_t)free_b, (int64_t)alloc_size, nullptr,
+         RecordContext::STATE);
   {
     std::lock_guard<std::mutex> g(g_obs_mu);
     for (auto& o : g_observers) o(device_, alloc_size, total, free_b);
@@ -701,7 +969,7 @@ bool host_memory_mode() { return g_fake; }
 void* alloc_on(int device, size_t nbytes, hipStream_t stream) {
   if (nbytes == 0) return nullptr;
   config();
-  Block* b = dev_alloc(device).malloc(nbytes, stream);
+  Block* b = dev_alloc(device).malloc(nbytes, stream, gather_if(RecordContext::STATE));
   std::lock_guard<std::mutex> g(g_owner_mu);
   g_owner[b->ptr] = device;
   return b->ptr;
@@ -741,7 +1009,7 @@ void raw_delete(void* ptr) {
     d = it->second;
     g_owner.erase(it);
   }
-  dev_alloc(d).free(ptr);
+  dev_alloc(d).free(ptr, gather_if(RecordContext::ALL));
 }
 
 void record_stream(const c10::DataPtr& ptr, c10::Stream stream) {
@@ -764,7 +1032,7 @@ void empty_cache() {
     for (auto& d : g_devices)
       if (d) devs.push_back(d.get());
   }
-  for (auto* d : devs) d->empty_cache();
+  for (auto* d : devs) d->empty_cache(gather_if(RecordContext::ALL));
 }
 
 void release_all_cached(int device) {
@@ -795,6 +1063,70 @@ std::vector<SegmentInfo> snapshot() {
   for (auto* d : devs) d->snapshot(out);
   return out;
 }
+
+namespace {
+std::vector<DeviceAllocator*> all_devices() {
+  std::vector<DeviceAllocator*> devs;
+  std::lock_guard<std::mutex> g(g_devices_mu);
+  for (auto& d : g_devices)
+    if (d) devs.push_back(d.get());
+  return devs;
+}
+}  // namespace
+
+Snapshot full_snapshot() {
+  Snapshot s;
+  for (auto* d : all_devices()) d->snapshot(s.segments, /*mark=*/true);
+  for (auto* d : all_devices()) s.device_traces.push_back(d->trace());
+  return s;
+}
+
+void record_history(bool enabled, ContextFn fn, size_t max_entries, RecordContext when) {
+  TORCH_CHECK(when == RecordContext::NEVER || fn != nullptr,
+              "gcu allocator: recording stacks needs a context function");
+  g_hist_on.store(false);  // entries stop while the settings change
+  g_hist_fn.store(enabled ? fn : nullptr);
+  g_hist_when.store(enabled ? (int)when : (int)RecordContext::NEVER);
+  g_hist_max.store(std::max<size_t>(1, max_entries));
+  for (auto* d : all_devices()) d->set_history(enabled, std::max<size_t>(1, max_entries));
+  g_hist_on.store(enabled);
+}
+
+bool history_enabled() { return g_hist_on.load(); }
+
+void cache_info(int device, size_t* largest) { dev_alloc(device).cache_info(largest); }
+
+void* get_base_allocation(void* ptr, size_t* size) {
+  int d;
+  {
+    std::lock_guard<std::mutex> g(g_owner_mu);
+    auto it = g_owner.find(ptr);
+    TORCH_CHECK(it != g_owner.end(), "gcu allocator: invalid device pointer ", ptr);
+    d = it->second;
+  }
+  return dev_alloc(d).base_allocation(ptr, size);
+}
+
+bool check_pool_live_allocations(int device, MempoolId id,
+                                 const std::unordered_set<void*>& expected) {
+  return dev_alloc(device).check_pool_live(id, expected);
+}
+
+std::shared_ptr<PoolState> get_checkpoint_state(int device, MempoolId id) {
+  return dev_alloc(device).checkpoint(id);
+}
+
+CheckpointDelta set_checkpoint_pool_state(int device, const PoolState& state) {
+  TORCH_CHECK(state.device == device, "gcu allocator: the checkpoint is of device ", state.device,
+              ", not ", device);
+  CheckpointDelta delta = dev_alloc(device).restore(state);
+  std::lock_guard<std::mutex> g(g_owner_mu);
+  for (void* p : delta.freed) g_owner.erase(p);
+  for (void* p : delta.allocated) g_owner[p] = device;
+  return delta;
+}
+
+c10::DeleterFnPtr raw_deleter() { return &delete_fn; }
 
 MempoolId new_pool_id() {
   static std::atomic<uint64_t> next{1};

@@ -5,8 +5,9 @@
 // (torch_gcu/csrc/gcu/gcu_caching_allocator.h:231-425): allocate / raw_alloc /
 // raw_delete, recordStream, emptyCache, memory stats, per-process memory
 // fraction, and the graph private-pool calls (beginAllocateToPool,
-// endAllocateToPool, releasePool) that GCUGraph uses.  Design notes are in
-// gcu_caching_allocator.cpp.
+// endAllocateToPool, releasePool) that GCUGraph uses, memory history and
+// snapshots, graph-pool checkpoints, cacheInfo, getBaseAllocation and
+// checkPoolLiveAllocations.  Design notes are in gcu_caching_allocator.cpp.
 #pragma once
 
 #include <c10/core/Allocator.h>
@@ -16,7 +17,9 @@
 #include <array>
 #include <cstdint>
 #include <functional>
+#include <memory>
 #include <string>
+#include <unordered_set>
 #include <utility>
 #include <vector>
 
@@ -59,16 +62,74 @@ struct DeviceStats {
   int64_t max_split_size = 0;
 };
 
+// Stack context of an allocator event (a torch::CapturedTraceback when
+// recorded from Python; symbolised only when a snapshot is taken).
+using Context = std::shared_ptr<c10::GatheredContext>;
+using ContextFn = Context (*)();
+
+struct BlockInfo {
+  uintptr_t address = 0;
+  size_t size = 0;
+  size_t requested_size = 0;
+  bool allocated = false;
+  bool active = false;  // allocated, or freed but awaiting other streams' events
+  Context context;      // where it was allocated (history with context on)
+};
+
 struct SegmentInfo {
   int device = 0;
   uintptr_t address = 0;
   size_t total_size = 0;
+  size_t requested_size = 0;
   size_t allocated_size = 0;
   size_t active_size = 0;
   bool is_large = false;
   MempoolId owner_pool{0, 0};
   uintptr_t stream = 0;
-  std::vector<std::pair<size_t, bool>> blocks;  // (size, allocated)
+  std::vector<BlockInfo> blocks;
+  Context context;  // where the segment was created
+};
+
+// Memory history (gcu_caching_allocator.h:136-185): one entry per allocator
+// event while recording is on, kept in a ring of at most max_entries.
+enum class TraceAction { ALLOC, FREE_REQUESTED, FREE_COMPLETED, SEGMENT_ALLOC, SEGMENT_FREE,
+                         SNAPSHOT, OOM };
+struct TraceEntry {
+  TraceAction action;
+  int device = 0;
+  uintptr_t addr = 0;  // for OOM: the device's free bytes
+  int64_t size = 0;
+  uintptr_t stream = 0;
+  int64_t time_us = 0;  // wall clock, microseconds since the epoch
+  Context context;
+};
+// Which events keep a stack: NEVER; STATE (live blocks and segments);
+// ALLOC (also alloc entries of the history); ALL (also free entries).
+enum class RecordContext { NEVER = 0, STATE = 1, ALLOC = 2, ALL = 3 };
+
+struct Snapshot {
+  std::vector<SegmentInfo> segments;
+  std::vector<std::vector<TraceEntry>> device_traces;  // index = device
+};
+
+// A graph pool's block layout, restorable later (getCheckpointState,
+// gcu_caching_allocator.cpp:1007-1222).
+struct BlockState {
+  uintptr_t ptr = 0;
+  size_t size = 0;
+  bool allocated = false;
+  uintptr_t stream = 0;
+};
+struct PoolState {
+  int device = 0;
+  MempoolId id{0, 0};
+  std::vector<std::vector<BlockState>> segments;  // blocks of each segment, in address order
+};
+// What setCheckpointPoolState changed: pointers whose blocks it freed and
+// pointers of blocks it allocated (a pointer may be in both).
+struct CheckpointDelta {
+  std::vector<void*> freed;
+  std::vector<void*> allocated;
 };
 
 // c10 allocator registered for DeviceType::PrivateUse1.
@@ -86,6 +147,27 @@ DeviceStats get_stats(int device);
 void reset_peak_stats(int device);
 void reset_accumulated_stats(int device);
 std::vector<SegmentInfo> snapshot();
+// Segments plus each device's history; records a SNAPSHOT event.
+Snapshot full_snapshot();
+// Turns history recording on or off on every device (recordHistory,
+// gcu_caching_allocator.cpp:531-546).  `fn` gathers a stack; it is called
+// outside the allocator's lock.  Turning it off clears the history.
+void record_history(bool enabled, ContextFn fn, size_t max_entries, RecordContext when);
+bool history_enabled();
+// Largest free cached block of the device (cacheInfo, :936-950); a zero
+// *largest starts from the device's free memory.
+void cache_info(int device, size_t* largest);
+// Start and size of the segment holding an allocated pointer
+// (getBaseAllocation, :861-880).
+void* get_base_allocation(void* ptr, size_t* size);
+// True when the allocated blocks of a graph pool are exactly `expected`
+// (checkPoolLiveAllocations, :547-566).
+bool check_pool_live_allocations(int device, MempoolId id,
+                                 const std::unordered_set<void*>& expected);
+std::shared_ptr<PoolState> get_checkpoint_state(int device, MempoolId id);
+CheckpointDelta set_checkpoint_pool_state(int device, const PoolState& state);
+// The deleter of every DataPtr this allocator hands out.
+c10::DeleterFnPtr raw_deleter();
 // Releases every cached block back to HIP and synchronises the device.
 void release_all_cached(int device);
 

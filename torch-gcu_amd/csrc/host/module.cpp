@@ -15,6 +15,7 @@ namespace torch_gcu {
 void ensure_initialized();
 bool is_initialized();
 void register_library_workspace();
+void bind_memory(pybind11::module& m);  // memory_bindings.cpp
 }
 
 namespace py = pybind11;
@@ -161,11 +162,14 @@ PYBIND11_MODULE(_C, m) {
       d["segment_type"] = s.is_large ? "large" : "small";
       d["segment_pool_id"] = py::make_tuple(s.owner_pool.first, s.owner_pool.second);
       d["stream"] = s.stream;
+      d["requested_size"] = s.requested_size;
       py::list blocks;
       for (const auto& b : s.blocks) {
         py::dict bd;
-        bd["size"] = b.first;
-        bd["state"] = b.second ? "active_allocated" : "inactive";
+        bd["address"] = b.address;
+        bd["size"] = b.size;
+        bd["requested_size"] = b.requested_size;
+        bd["state"] = b.allocated ? "active_allocated" : (b.active ? "active_pending_free" : "inactive");
         blocks.append(bd);
       }
       d["blocks"] = blocks;
@@ -173,6 +177,7 @@ PYBIND11_MODULE(_C, m) {
     }
     return out;
   });
+  bind_memory(m);
   m.def("_parse_alloc_conf", [](const std::string& s) {
     const auto c = allocator::parse_config(s);
     py::dict d;

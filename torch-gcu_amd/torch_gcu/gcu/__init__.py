@@ -12,11 +12,15 @@ import torch
 from .. import _C
 from .graphs import GCUGraph, graph, graph_pool_handle  # noqa: F401
 from .memory import (  # noqa: F401
-    empty_cache, get_per_process_memory_fraction, host_empty_cache, host_memory_stats,
-    max_memory_allocated, max_memory_reserved, mem_get_info, memory_allocated, memory_reserved, memory_snapshot, memory_stats,
-    reset_accumulated_memory_stats, reset_max_memory_allocated, reset_peak_memory_stats,
-    set_per_process_memory_fraction,
+    MemPool, caching_allocator_alloc, caching_allocator_delete, empty_cache,
+    get_allocator_backend, get_per_process_memory_fraction, host_empty_cache, host_memory_stats,
+    max_memory_allocated, max_memory_cached, max_memory_reserved, mem_get_info,
+    memory_allocated, memory_cached, memory_reserved, memory_snapshot, memory_stats,
+    memory_stats_as_nested_dict, memory_summary, reset_accumulated_memory_stats,
+    reset_max_memory_allocated, reset_max_memory_cached, reset_peak_memory_stats,
+    set_per_process_memory_fraction, use_mem_pool,
 )
+from . import memory  # noqa: F401
 
 _DeviceLike = Union[torch.device, str, int, None]
 
