@@ -413,6 +413,11 @@ mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out,
 mi_status_t mi_silu_mul(const mi_tensor_t* out, const mi_tensor_t* gate,
                         const mi_tensor_t* up, mi_stream_t stream);
 
+/* out = silu(self) = self / (1 + exp(-self)), fp32 math, one rounding; self
+ * broadcast to out, one dtype (bf16, f16, f32).  Replaces topsatenSilu
+ * (yaml silu.out :561). */
+mi_status_t mi_silu(const mi_tensor_t* out, const mi_tensor_t* self, mi_stream_t stream);
+
 /* grad_input = dy * s * (1 + x * (1 - s)), s = sigmoid(x), fp32 math; dy and
  * x broadcast to grad_input, all one dtype.  Replaces topsatenSiluBackward
  * (yaml silu_backward.grad_input :563). */

@@ -213,6 +213,14 @@ PYBIND11_MODULE(_C, m) {
   });
 
   // graphs
+  // graphs.py:28-34: capture state of the current stream, false (and no
+  // runtime initialisation) before the device is used
+  m.def("_is_current_stream_capturing", []() {
+    if (!is_initialized()) return false;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    GCU_HIP_CHECK(hipStreamIsCapturing(current_hip_stream(), &st));
+    return st == hipStreamCaptureStatusActive;
+  });
   m.def("_graph_pool_handle", []() {
     const auto id = allocator::new_pool_id();
     return py::make_tuple(id.first, id.second);

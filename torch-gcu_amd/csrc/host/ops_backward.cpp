@@ -1,6 +1,6 @@
 // The training-side backward ops the reference registers natively but sends
 // to CPU on its s60 hardware (codegen/gcu_op_fallback.yaml:22-41):
-// silu_backward, _log_softmax_backward_data / _softmax_backward_data and
+// silu and silu_backward, _log_softmax_backward_data / _softmax_backward_data and
 // native_layer_norm_backward, and the layer-norm forward whose statistics
 // that backward takes (native_layer_norm, yaml :481).  Shape and dtype rules are ATen's (the
 // structured meta functions where the op has one); the arithmetic is the
@@ -65,6 +65,45 @@ using LogSoftmaxBwdMeta = OneOutput<at::meta::structured__log_softmax_backward_d
 using SoftmaxBwdMeta = OneOutput<at::meta::structured__softmax_backward_data>;
 
 }  // namespace
+
+// silu (yaml silu.out :561 of the reference's list): out = self * sigmoid(self)
+// with TensorIterator's unary rules (out resized to self, result cast into out).
+namespace {
+void silu_into(const at::Tensor& self, at::Tensor& out) {
+  if (out.numel() == 0) return;
+  at::Tensor target = out.scalar_type() == self.scalar_type()
+                          ? out
+                          : at::empty(out.sizes(), out.options().dtype(self.scalar_type()));
+  const mi_tensor_t o = desc(target), x = desc(self);
+  check_mi(mi_silu(&o, &x, mi_stream(out)), "silu");
+  if (!target.is_same(out)) out.copy_(target);
+}
+}  // namespace
+
+at::Tensor silu(const at::Tensor& self) {
+  if (!float_kernel_dtype(self.scalar_type()))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP(silu)>::call(self);
+  at::Tensor out = at::empty(self.sizes(), self.options().memory_format(self.suggest_memory_format()));
+  silu_into(self, out);
+  return out;
+}
+
+at::Tensor& silu_(at::Tensor& self) {
+  if (!float_kernel_dtype(self.scalar_type()))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP(silu_)>::call(self);
+  silu_into(self, self);
+  return self;
+}
+
+at::Tensor& silu_out(const at::Tensor& self, at::Tensor& out) {
+  if (!float_kernel_dtype(self.scalar_type()) || !float_kernel_dtype(out.scalar_type()))
+    return at::native::call_fallback_fn<&gcu_cpu_fallback, ATEN_OP2(silu, out)>::call(self, out);
+  TORCH_CHECK(at::canCast(self.scalar_type(), out.scalar_type()), "result type ",
+              self.scalar_type(), " can't be cast to the desired output type ", out.scalar_type());
+  at::native::resize_output(out, self.sizes());
+  silu_into(self, out);
+  return out;
+}
 
 at::Tensor silu_backward(const at::Tensor& grad_output, const at::Tensor& self) {
   const at::ScalarType dt = at::result_type(grad_output, self);

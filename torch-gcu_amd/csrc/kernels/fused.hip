@@ -333,16 +333,19 @@ mi_status_t rope_view(const mi_tensor_t* o, const mi_tensor_t* in, int64_t token
 
 // ---- SiLU-mul ---------------------------------------------------------------------
 
-// The two elementwise SiLU pairs: silu(a) * b (the fused SwiGLU product) and
-// silu's derivative applied to a gradient, a * s * (1 + b * (1 - s)) with
+// The elementwise SiLU ops: silu(a) * b (the fused SwiGLU product), silu's
+// derivative applied to a gradient, a * s * (1 + b * (1 - s)) with
 // s = sigmoid(b), a = grad_output, b = the forward input (ATen's
-// silu_backward formula, aten/src/ATen/native/cpu/Activation.cpp).
-enum PairOp { P_SILU_MUL = 0, P_SILU_BWD = 1 };
+// silu_backward formula, aten/src/ATen/native/cpu/Activation.cpp), and
+// silu(a) itself (one operand: b is neither loaded nor used).
+enum PairOp { P_SILU_MUL = 0, P_SILU_BWD = 1, P_SILU = 2 };
 
 template <int OP>
 __device__ __forceinline__ float pair_op(float a, float b) {
   if constexpr (OP == P_SILU_MUL) {
     return a * __builtin_amdgcn_rcpf(1.0f + fast_exp(-a)) * b;
+  } else if constexpr (OP == P_SILU) {
+    return a * __builtin_amdgcn_rcpf(1.0f + fast_exp(-a));
   } else {
     const float sg = __builtin_amdgcn_rcpf(1.0f + fast_exp(-b));
     return a * sg * (1.0f + b * (1.0f - sg));
@@ -369,7 +372,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(typename FT<Tag>::storage
     const int64_t i = base + k * 256;
     if (i < nvec) {
       vg[k] = ld_stream((const V*)g + i);
-      vu[k] = ld_stream((const V*)u + i);
+      if constexpr (OP != P_SILU) vu[k] = ld_stream((const V*)u + i);
     }
   }
 #pragma unroll
@@ -379,7 +382,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(typename FT<Tag>::storage
       V o;
 #pragma unroll
       for (int e = 0; e < VEC; ++e)
-        o.s[e] = FT<Tag>::store(pair_op<OP>(FT<Tag>::load(vg[k].s[e]), FT<Tag>::load(vu[k].s[e])));
+        o.s[e] = FT<Tag>::store(pair_op<OP>(
+            FT<Tag>::load(vg[k].s[e]), OP == P_SILU ? 0.f : FT<Tag>::load(vu[k].s[e])));
       st_stream((V*)out + i, o);
     }
   }
@@ -388,7 +392,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(typename FT<Tag>::storage
   const int64_t rem = n - nvec * VEC;
   if (blockIdx.x == 0 && t < rem) {
     const int64_t i = nvec * VEC + t;
-    out[i] = FT<Tag>::store(pair_op<OP>(FT<Tag>::load(g[i]), FT<Tag>::load(u[i])));
+    out[i] = FT<Tag>::store(pair_op<OP>(FT<Tag>::load(g[i]), OP == P_SILU ? 0.f : FT<Tag>::load(u[i])));
   }
 }
 
@@ -401,8 +405,8 @@ __global__ __launch_bounds__(256) void silu_mul_strided_kernel(char* out, const 
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
     int64_t off[3];
     oc.get(i, off);
-    ((St*)out)[off[0]] = FT<Tag>::store(
-        pair_op<OP>(FT<Tag>::load(((const St*)g)[off[1]]), FT<Tag>::load(((const St*)u)[off[2]])));
+    ((St*)out)[off[0]] = FT<Tag>::store(pair_op<OP>(
+        FT<Tag>::load(((const St*)g)[off[1]]), OP == P_SILU ? 0.f : FT<Tag>::load(((const St*)u)[off[2]])));
   }
 }
 
@@ -546,6 +550,21 @@ mi_status_t mi_silu_mul(const mi_tensor_t* out, const mi_tensor_t* gate, const m
     case MI_F16: return silu_mul_t<F16, P_SILU_MUL>(out, gate, up, stream);
     case MI_F32: return silu_mul_t<float, P_SILU_MUL>(out, gate, up, stream);
     default: MI_FAIL(MI_ERR_UNSUPPORTED, "silu_mul: dtype %s", dtype_name(out->dtype));
+  }
+}
+
+mi_status_t mi_silu(const mi_tensor_t* out, const mi_tensor_t* self, mi_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = (hipStream_t)stream_;
+  MI_RETURN_IF(validate(out, "out"));
+  MI_RETURN_IF(validate(self, "self"));
+  MI_CHECK_ARG(out->dtype == self->dtype, "silu: self and out must share a dtype");
+  // self is passed as both operands of the pair iterator; the kernels read it once
+  switch (out->dtype) {
+    case MI_BF16: return silu_mul_t<BF16, P_SILU>(out, self, self, stream);
+    case MI_F16: return silu_mul_t<F16, P_SILU>(out, self, self, stream);
+    case MI_F32: return silu_mul_t<float, P_SILU>(out, self, self, stream);
+    default: MI_FAIL(MI_ERR_UNSUPPORTED, "silu: dtype %s", dtype_name(out->dtype));
   }
 }
 

@@ -73,6 +73,7 @@ _SIGNATURES = {
     "mi_copy": ([_T, _T, _S], ctypes.c_int),
     "mi_fill": ([_T, MiScalar, _S], ctypes.c_int),
     "mi_cat": ([_T, ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_int32, _S], ctypes.c_int),
+    "mi_silu": ([_T, _T, _S], ctypes.c_int),
     "mi_silu_backward": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_foreach_add_scalar": ([ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_double, _S], ctypes.c_int),
     "mi_foreach_mul_scalar": ([ctypes.POINTER(_T), ctypes.c_int32, ctypes.c_double, _T, _S],
@@ -305,6 +306,11 @@ def amp_update_scale_(scale, growth_tracker, found_inf, growth_factor, backoff_f
         desc(scale), desc(growth_tracker), desc(found_inf), float(growth_factor),
         float(backoff_factor), int(interval), stream_of(scale)))
     return scale
+
+
+def silu(out, self):
+    check("mi_silu", lib().mi_silu(desc(out), desc(self), stream_of(out)))
+    return out
 
 
 def silu_backward(grad_input, grad_output, self):

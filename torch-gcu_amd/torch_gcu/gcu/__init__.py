@@ -10,7 +10,9 @@ from typing import Any, Optional, Union
 import torch
 
 from .. import _C
-from .graphs import GCUGraph, graph, graph_pool_handle  # noqa: F401
+from .graphs import (  # noqa: F401
+    GCUGraph, graph, graph_pool_handle, is_current_stream_capturing, make_graphed_callables,
+)
 from .memory import (  # noqa: F401
     MemPool, caching_allocator_alloc, caching_allocator_delete, empty_cache,
     get_allocator_backend, get_per_process_memory_fraction, host_empty_cache, host_memory_stats,
