@@ -407,7 +407,10 @@ def gemm_ops(torch, _abi):
                         bound="mfma"))
     del A, B, Bt, out, sets
     N, K = 11008, 4096
-    W = [torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8).cuda() for _ in range(4)]
+    # 13 weight copies (586 MB) rotated, past the 256 MiB MALL: every launch
+    # streams its weight from HBM
+    W = [torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int8).cuda()]
+    W += [W[0].roll(k, 0) for k in range(1, 13)]
     scales = (torch.rand(N, generator=gen) * 0.009 + 0.001).cuda()
     for M in (16, 256, 4096):
         x = torch.randn(M, K, generator=gen).bfloat16().cuda()
@@ -475,8 +478,9 @@ def config3_ops(torch, _abi, synthetic):
                         lambda s: _abi.rms_norm(s["o"], s["x"], w, 1e-6), 268443648))
     del xs, x
     q, k, pos = c3["q"].cuda(), c3["k"].cuda(), c3["pos"].cuda()
-    qs = [{"q": q, "k": k, "qo": torch.empty_like(q), "ko": torch.empty_like(k)},
-          {"q": k, "k": q, "qo": torch.empty_like(q), "ko": torch.empty_like(k)}]
+    # three distinct (q, k) sets (768 MiB of input) rotated, past the MALL
+    qs = [{"q": q.roll(j, 0), "k": k.roll(j, 0), "qo": torch.empty_like(q),
+           "ko": torch.empty_like(k)} for j in range(3)]
     res.append(bench_op(torch, "c3.rope q,k bf16 [16384,32,128]", qs,
                         lambda s: _abi.rope(s["qo"], s["ko"], s["q"], s["k"], pos, 10000.0),
                         536870912))
@@ -726,6 +730,11 @@ def run_section(name):
     _abi.install_workspace()
     import torch_gcu  # noqa: F401
 
+    # one plain 512 MiB device copy (untimed): under rocprofv3 --pmc its
+    # FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes
+    cal = torch.empty(CAL_COPY_BYTES // 2, dtype=torch.int16, device="cuda")
+    _abi.copy_(torch.empty_like(cal), cal)
+    del cal
     for r in SECTIONS[name](torch, _abi):
         print(json.dumps(r), flush=True)
     return 0
