@@ -215,14 +215,71 @@ def test_dl_kernel_batched_strided_and_odd_ldc():
     assert (big[:, N:].cpu() == 0).all()
 
 
-def test_row_major_b_transpose_path():
-    """B as a row-major [K, N] matrix (config 4's layout) goes through the
-    tiled transpose into a K-contiguous copy, then the large-tile kernel."""
-    M, N, K = 4096, 4160, 320
-    a, b, bias = rn((M, K), 59, std=1.0), rn((K, N), 60, std=1.0), rn((N,), 61, std=1.0)
+def _gcu_allocations():
+    import torch_gcu
+    return torch_gcu._C._memory_stats(0)["allocation.all.allocated"]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K,bias", [(4096, 4160, 320, True), (2048, 8200, 192, False),
+                                        (4000, 4096, 64, True)])
+def test_row_major_b_read_in_place(dtype, M, N, K, bias):
+    """B as a row-major [K, N] matrix with M <= 4096 is read in place by the
+    large-tile kernel (transposed fragment reads from LDS): no workspace is
+    taken, ragged last row and column tiles included."""
+    a, b = rn((M, K), 59, dtype, 1.0), rn((K, N), 60, dtype, 1.0)
+    bi = rn((N,), 61, dtype, 1.0) if bias else None
+    out = torch.empty(M, N, dtype=dtype, device="cuda")
+    ad, bd, bid = a.cuda(), b.cuda(), (bi.cuda() if bias else None)
+    torch.cuda.synchronize()
+    n0 = _gcu_allocations()
+    if bias:
+        _abi.addmm(out, bid, ad, bd)
+    else:
+        _abi.mm(out, ad, bd)
+    torch.cuda.synchronize()
+    assert _gcu_allocations() == n0, "row-major B took workspace (the transpose copy)"
+    assert_close(out, aten.addmm(bi, a, b, beta=1.0 if bias else 0.0), "bf16",
+                 f"row-major B {M}x{N}x{K}")
+
+
+def test_row_major_b_strided_batched_and_fallback():
+    """Row-major B inside a wider buffer (row stride > N), a batched product
+    with row-major B, and an N that is not a multiple of 8 (whole 16-byte
+    column chunks are required), which goes through the transpose copy."""
+    M, N, K = 4096, 4096, 192
+    a = rn((M, K), 65, std=1.0)
+    wide = rn((K, N + 64), 66, std=1.0)
     out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-    _abi.addmm(out, bias.cuda(), a.cuda(), b.cuda())
-    assert_close(out, aten.addmm(bias, a, b), "bf16", "row-major B")
+    _abi.mm(out, a.cuda(), wide.cuda()[:, 16:16 + N])
+    assert_close(out, aten.addmm(None, a, wide[:, 16:16 + N], beta=0.0), "bf16",
+                 "row-major B, row stride > N")
+    Bn, M, N, K = 64, 512, 512, 128
+    a, b = rn((Bn, M, K), 67, std=1.0), rn((Bn, K, N), 68, std=1.0)
+    out = torch.empty(Bn, M, N, dtype=torch.bfloat16, device="cuda")
+    _abi.bmm(out, a.cuda(), b.cuda())
+    assert_close(out, aten.bmm(a, b), "bf16", "batched row-major B")
+    M, N, K = 4096, 4098, 128
+    a, b = rn((M, K), 69, std=1.0), rn((K, N), 70, std=1.0)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ad, bd = a.cuda(), b.cuda()
+    torch.cuda.synchronize()
+    n0 = _gcu_allocations()
+    _abi.mm(out, ad, bd)
+    torch.cuda.synchronize()
+    assert _gcu_allocations() > n0, "N % 8 != 0 should take the transpose copy"
+    assert_close(out, aten.addmm(None, a, b, beta=0.0), "bf16", "row-major B, N % 8 != 0")
+    # M > 4096: the K-contiguous copy of B, then the large-tile kernel
+    M, N, K = 8192, 4096, 128
+    a, b, bias = rn((M, K), 71, std=1.0), rn((K, N), 72, std=1.0), rn((N,), 73, std=1.0)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ad, bd, bid = a.cuda(), b.cuda(), bias.cuda()
+    torch.cuda.synchronize()
+    n0 = _gcu_allocations()
+    _abi.addmm(out, bid, ad, bd)
+    torch.cuda.synchronize()
+    assert _gcu_allocations() > n0, "M > 4096 should take the transpose copy"
+    assert_close(out, aten.addmm(bias, a, b), "bf16", "row-major B, M > 4096")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (16, 11008, 4096), (33, 520, 1024),
