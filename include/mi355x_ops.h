@@ -112,6 +112,16 @@ mi_status_t mi_set_workspace_allocator(mi_alloc_fn alloc_fn, mi_free_fn free_fn,
  * negative on error. */
 int32_t mi_device_cu_count(void);
 
+/* Out-of-range indices met by mi_index_select and mi_index on `device`
+ * since the last call: returns 1 and stores one offending index and the size
+ * of the dimension it indexed, or returns 0; clears the record.  The kernels
+ * write the record into pinned host-coherent memory, so this reads host
+ * memory only and must follow a synchronisation with the work it covers.
+ * No counterpart in the reference's TopsAten seam, whose index kernels check
+ * their indices themselves; the host layer raises the IndexError that CPU
+ * ATen would, at the next synchronisation. */
+int32_t mi_index_fault_take(int32_t device, int64_t* index, int64_t* dim_size);
+
 /* ---- copies and fills --------------------------------------------------- */
 
 /* out[...] = (out.dtype) src[...]; src broadcasts to out.  Same-dtype
@@ -239,7 +249,7 @@ mi_status_t mi_amp_update_scale(const mi_tensor_t* scale, const mi_tensor_t* gro
 /* out = self.index_select(dim, index); index is 1-D (or 0-D) int32/int64;
  * negative indices are not wrapped (as in ATen).  The kernel never reads
  * outside self: a row whose index is out of range is written as zeros and
- * the host layer raises the IndexError (the reference validates shapes in
+ * recorded for mi_index_fault_take (the reference validates shapes in
  * torch_gcu/csrc/aten/shape_inference/indexing.cpp:20-69).  Replaces
  * topsatenIndexSelect (yaml index_select.out :379). */
 mi_status_t mi_index_select(const mi_tensor_t* out, const mi_tensor_t* self,
@@ -255,8 +265,8 @@ mi_status_t mi_index_select(const mi_tensor_t* out, const mi_tensor_t* self,
  * out.shape = B + the other dims of self in order.  out is contiguous, of
  * self's dtype.  int32 indices are read as int32 (no widening to int64).
  * Negative indices count from the end of their dim; an index still out of
- * range writes its out row as zeros (the kernel never reads outside self;
- * the host layer raises the IndexError for host-side indices).  Replaces
+ * range writes its out row as zeros (the kernel never reads outside self)
+ * and is recorded for mi_index_fault_take.  Replaces
  * topsatenIndex behind device_int32_indices_index
  * (torch_gcu/csrc/efficient_ops/ops.cpp:335-342, bridge_topsatenIndex_out1). */
 mi_status_t mi_index(const mi_tensor_t* out, const mi_tensor_t* self,

@@ -91,13 +91,46 @@ def test_gcu_index_empty_and_out_of_range_device_index():
     z = table((0, 7), torch.float32, 401)
     assert gcu_index(z.to("gcu"), [torch.empty(0, 3, dtype=torch.int32, device="gcu")]).shape == (0, 3, 7)
     # a device index out of range is not range-checked on the host (that
-    # would synchronise); its row is written as zeros and nothing outside
-    # self is read
+    # would synchronise): its row is written as zeros, nothing outside self
+    # is read, and the kernel's record raises CPU ATen's IndexError at the
+    # next synchronisation (here the copy to the host), once
     idx = torch.tensor([2, 40, -1, -13], dtype=torch.int32)
-    got = gcu_index(x.to("gcu"), [idx.to("gcu")]).cpu()
+    with pytest.raises(IndexError, match="out of bounds for dimension with size 12"):
+        gcu_index(x.to("gcu"), [idx.to("gcu")]).cpu()
+    with pytest.raises(IndexError):
+        aten.int32_indices_index(x, [idx])
+    got = gcu_index(x.to("gcu"), [idx.to("gcu")])
+    with pytest.raises(IndexError, match="reported at the next synchronization"):
+        torch.gcu.synchronize()
+    torch.gcu.synchronize()  # cleared: no second error
+    got = got.cpu()
     assert_exact(got[0], x[2], "in range")
     assert_exact(got[2], x[-1], "negative index")
     assert bool((got[1] == 0).all()) and bool((got[3] == 0).all())
+
+
+def test_index_select_out_of_range_device_index_raises_at_sync():
+    """index_select through the dispatcher with a device index past the
+    table: CPU ATen raises IndexError at the call; on gcu the gather writes
+    zeros and the error is raised at the next synchronisation (the value
+    read by .item() here)."""
+    x = table((64, 8), torch.int64, 402)
+    bad = torch.tensor([3, 64, 5])
+    with pytest.raises(IndexError):
+        torch.index_select(x, 0, bad)
+    y = torch.index_select(x.to("gcu"), 0, bad.to("gcu"))
+    with pytest.raises(IndexError, match="index 64 is out of bounds for dimension with size 64"):
+        y[0, 0].item()
+    assert_exact(y.cpu()[0], x[3], "row before the bad one")
+    assert bool((y.cpu()[1] == 0).all())
+    # op_sync_mode reports it at the op that read it
+    torch_gcu._C._set_op_debug_config("op_sync_mode=true")
+    try:
+        with pytest.raises(IndexError, match="out of bounds"):
+            torch.index_select(x.to("gcu"), 0, bad.to("gcu"))
+    finally:
+        torch_gcu._C._set_op_debug_config("")
+    torch.gcu.synchronize()
 
 
 def test_gcu_index_errors_follow_the_reference():

@@ -269,13 +269,18 @@ def test_index_select_embedding_rows_and_edges():
     out = empty_like_ref(ref)
     _abi.index_select(out, dev(emb), 0, dev(e))
     assert out.shape == (0, 4096)
-    # out-of-range rows are written as zeros, never read
+    # out-of-range rows are written as zeros, never read, and recorded for
+    # mi_index_fault_take (one of the bad indices, with the dim size)
+    assert _abi.index_fault_take(0) is None
     bad = torch.tensor([0, 320, -1, 5])
     out = torch.full((4, 4096), 7.0, dtype=torch.bfloat16, device=DEV)
     _abi.index_select(out, dev(emb), 0, dev(bad))
     o = out.cpu()
     assert torch.equal(o[0], emb[0]) and torch.equal(o[3], emb[5])
     assert (o[1] == 0).all() and (o[2] == 0).all()
+    fault = _abi.index_fault_take(0)
+    assert fault is not None and fault[0] in (320, -1) and fault[1] == emb.shape[0], fault
+    assert _abi.index_fault_take(0) is None  # the record was cleared
 
 
 # ---- reductions -------------------------------------------------------------------

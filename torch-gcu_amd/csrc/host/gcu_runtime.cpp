@@ -1,4 +1,5 @@
 #include "gcu_runtime.h"
+#include "mi355x_ops.h"
 
 #include <c10/core/impl/DeviceGuardImplInterface.h>
 #include <c10/core/impl/GPUTrace.h>
@@ -48,6 +49,19 @@ void device_synchronize(c10::DeviceIndex d) {
   maybe_set_device(d);
   GCU_HIP_CHECK(hipDeviceSynchronize());
   maybe_set_device(prev);
+  check_index_faults(d);
+}
+
+// The gather kernels record an out-of-range index instead of reading outside
+// their source; once the work has been waited for, the record is raised
+// here as CPU ATen raises it for the same input (IndexError), as a CUDA
+// device-side assertion is reported at the next synchronisation.
+void check_index_faults(c10::DeviceIndex d) {
+  int64_t index = 0, size = 0;
+  if (mi_index_fault_take((int32_t)d, &index, &size) != 0)
+    TORCH_CHECK_INDEX(false, "index ", index, " is out of bounds for dimension with size ", size,
+                      " (read by an index_select or index kernel on gcu:", (int)d,
+                      "; reported at the next synchronization)");
 }
 
 // ---- streams ------------------------------------------------------------------
@@ -169,8 +183,10 @@ c10::Stream wrap_external_stream(c10::DeviceIndex d, hipStream_t h) {
 hipStream_t current_hip_stream(c10::DeviceIndex d) { return stream_handle(current_stream(d)); }
 
 void maybe_sync_after_op(hipStream_t s) {
-  if (OpDebugConfig::get().op_sync_mode && !stream_is_capturing(s))
+  if (OpDebugConfig::get().op_sync_mode && !stream_is_capturing(s)) {
     GCU_HIP_CHECK(hipStreamSynchronize(s));
+    check_index_faults(current_device());
+  }
 }
 
 bool stream_is_capturing(hipStream_t s) {
@@ -278,6 +294,7 @@ struct GCUGuardImpl final : public c10::impl::DeviceGuardImplInterface {
   }
   void synchronizeStream(const c10::Stream& s) const override {
     GCU_HIP_CHECK(hipStreamSynchronize(stream_handle(s)));
+    check_index_faults(s.device_index());
   }
   void synchronizeEvent(void* event) const override {
     if (event) GCU_HIP_CHECK(hipEventSynchronize((hipEvent_t)event));

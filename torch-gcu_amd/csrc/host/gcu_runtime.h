@@ -41,6 +41,9 @@ void set_device(c10::DeviceIndex d);
 // Sets the device only when it differs (no runtime call otherwise).
 void maybe_set_device(c10::DeviceIndex d);
 void device_synchronize(c10::DeviceIndex d);
+// Raises IndexError for an out-of-range index a gather kernel met on device
+// d since the last check (call after the work is synchronised).
+void check_index_faults(c10::DeviceIndex d);
 
 // ---- streams ------------------------------------------------------------------
 // Number of pool streams per device (ENFLAME_PT_STREAM_NUM, default 32, as

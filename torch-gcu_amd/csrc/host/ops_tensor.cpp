@@ -257,6 +257,7 @@ at::Tensor copy_d2h(const at::Tensor& dst, const at::Tensor& src, bool non_block
     return dst;
   }
   GCU_HIP_CHECK(hipStreamSynchronize(s));
+  check_index_faults((c10::DeviceIndex)dev);
   if (!dense) dst.copy_(h);
   return dst;
 }
@@ -314,6 +315,7 @@ at::Scalar _local_scalar_dense(const at::Tensor& self) {
   GCU_HIP_CHECK(hipMemcpyAsync(host.data_ptr(), self.data_ptr(), self.dtype().itemsize(),
                                hipMemcpyDeviceToHost, s));
   GCU_HIP_CHECK(hipStreamSynchronize(s));
+  check_index_faults(self.device().index());
   return host.item();
 }
 

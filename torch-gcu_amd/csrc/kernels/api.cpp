@@ -100,6 +100,48 @@ mi_status_t Workspace::alloc(size_t bytes, hipStream_t stream) {
   return MI_OK;
 }
 
+namespace {
+std::mutex g_fault_mu;
+std::vector<IndexFault*> g_faults;  // per device, host pointers (coherent, mapped)
+
+IndexFault* fault_of(int dev, bool create) {
+  std::lock_guard<std::mutex> g(g_fault_mu);
+  if ((int)g_faults.size() <= dev) g_faults.resize(dev + 1, nullptr);
+  if (g_faults[dev] == nullptr && create) {
+    // host allocation is legal inside a stream capture only in relaxed mode
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    void* p = nullptr;
+    const hipError_t e =
+        hipHostMalloc(&p, sizeof(IndexFault), hipHostMallocMapped | hipHostMallocCoherent);
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    volatile IndexFault* v = static_cast<volatile IndexFault*>(p);
+    v->flag = 0;
+    v->index = 0;
+    v->size = 0;
+    g_faults[dev] = static_cast<IndexFault*>(p);
+  }
+  return g_faults[dev];
+}
+}  // namespace
+
+IndexFault* index_fault_word() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  IndexFault* h = fault_of(dev, true);
+  if (h == nullptr) return nullptr;
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return static_cast<IndexFault*>(d);
+}
+
 int cu_count() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
@@ -232,5 +274,17 @@ mi_status_t mi_set_workspace_allocator(mi_alloc_fn alloc_fn, mi_free_fn free_fn,
 }
 
 int32_t mi_device_cu_count(void) { return mi::cu_count(); }
+
+int32_t mi_index_fault_take(int32_t device, int64_t* index, int64_t* dim_size) {
+  if (device < 0) return 0;
+  mi::IndexFault* f = mi::fault_of(device, false);
+  if (f == nullptr) return 0;
+  volatile mi::IndexFault* v = f;
+  if (v->flag == 0) return 0;
+  if (index) *index = v->index;
+  if (dim_size) *dim_size = v->size;
+  v->flag = 0;
+  return 1;
+}
 
 }  // extern "C"

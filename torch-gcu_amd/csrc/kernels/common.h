@@ -75,6 +75,29 @@ void set_scratch_arena(ScratchArena* arena);  // nullptr clears it
 
 int cu_count();
 
+// Out-of-range index record of one device (index_select / index kernels):
+// flag set to 1, the offending index and the size of the dimension it
+// indexes (any one of them when several lanes write).  Lives in pinned,
+// host-coherent memory, so recording costs nothing until an index is bad
+// and the host reads it after a synchronisation without a device call.
+struct IndexFault {
+  int64_t flag;
+  int64_t index;
+  int64_t size;
+};
+// The current device's record (device-accessible pointer), allocated on
+// first use; nullptr if pinned memory cannot be had (then nothing is
+// recorded).
+IndexFault* index_fault_word();
+// Records a bad index (vector stores of per-lane data).
+__device__ __forceinline__ void record_index_fault(IndexFault* f, int64_t index, int64_t size) {
+  if (f != nullptr) {
+    f->index = index;
+    f->size = size;
+    f->flag = 1;
+  }
+}
+
 // ---- dtypes -------------------------------------------------------------------
 
 inline int dtype_size(int dt) {

@@ -30,7 +30,7 @@ template <typename W, typename IdxT>
 __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
     W* __restrict__ out, const W* __restrict__ self, const IdxT* __restrict__ idx,
     int64_t istride, int64_t outer, int64_t n_idx, int64_t src_rows, int64_t words_per_row,
-    int log2_wpr) {
+    int log2_wpr, IndexFault* fault) {
   const int64_t total = outer * n_idx * words_per_row;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   const bool small = total < 0x7fffffffLL;
@@ -76,6 +76,7 @@ __global__ __launch_bounds__(kBlock) void gather_rows_kernel(
 #pragma unroll
   for (int u = 0; u < kGatherU; ++u) {
     if (tt[u] < total) {
+      if (!ok[u]) record_index_fault(fault, s[u], src_rows);
       const W r = ok[u] ? v[u] : W{};
       if constexpr (sizeof(W) == 16) st_stream(out + tt[u], r);
       else out[tt[u]] = r;
@@ -97,7 +98,8 @@ template <typename T, typename IdxT>
 __global__ __launch_bounds__(kBlock) void gather_general_kernel(T* out, const T* self,
                                                                 const IdxT* idx,
                                                                 int64_t istride,
-                                                                GatherGeneral g, int64_t n) {
+                                                                GatherGeneral g, int64_t n,
+                                                                IndexFault* fault) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < n; t += stride) {
     int64_t lin = t, oo = 0, so = 0;
@@ -109,6 +111,7 @@ __global__ __launch_bounds__(kBlock) void gather_general_kernel(T* out, const T*
       if (d == g.dim) {
         const int64_t s = read_index(idx, c, istride);
         ok = s >= 0 && s < g.src_dim_size;
+        if (!ok) record_index_fault(fault, s, g.src_dim_size);
         so += s * g.sstrides[d];
       } else {
         so += c * g.sstrides[d];
@@ -146,7 +149,7 @@ mi_status_t launch_rows(const mi_tensor_t* out, const mi_tensor_t* self, const I
     MI_CHECK_ARG(nb <= 0x7fffffffLL, "index_select: too many rows");
     hipLaunchKernelGGL((gather_rows_kernel<W, IdxT>), dim3((unsigned)nb), dim3(kBlock), 0,
                        stream, (W*)out->data, (const W*)self->data, idx, istride, outer, n_idx,
-                       src_rows, wpr, log2_wpr);
+                       src_rows, wpr, log2_wpr, index_fault_word());
     return check_launch("index_select rows");
   };
   if (row_bytes % 16 == 0 && align % 16 == 0) return go(uint4{});
@@ -170,11 +173,12 @@ mi_status_t launch_general(const mi_tensor_t* out, const mi_tensor_t* self, int 
   g.src_dim_size = self->sizes[dim];
   const int64_t n = numel(*out);
   const unsigned grid = grid_for(n);
+  IndexFault* fault = index_fault_word();
   switch (dtype_size(out->dtype)) {
-    case 1: hipLaunchKernelGGL((gather_general_kernel<uint8_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint8_t*)out->data, (const uint8_t*)self->data, idx, istride, g, n); break;
-    case 2: hipLaunchKernelGGL((gather_general_kernel<uint16_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint16_t*)out->data, (const uint16_t*)self->data, idx, istride, g, n); break;
-    case 4: hipLaunchKernelGGL((gather_general_kernel<uint32_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint32_t*)out->data, (const uint32_t*)self->data, idx, istride, g, n); break;
-    default: hipLaunchKernelGGL((gather_general_kernel<uint64_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint64_t*)out->data, (const uint64_t*)self->data, idx, istride, g, n); break;
+    case 1: hipLaunchKernelGGL((gather_general_kernel<uint8_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint8_t*)out->data, (const uint8_t*)self->data, idx, istride, g, n, fault); break;
+    case 2: hipLaunchKernelGGL((gather_general_kernel<uint16_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint16_t*)out->data, (const uint16_t*)self->data, idx, istride, g, n, fault); break;
+    case 4: hipLaunchKernelGGL((gather_general_kernel<uint32_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint32_t*)out->data, (const uint32_t*)self->data, idx, istride, g, n, fault); break;
+    default: hipLaunchKernelGGL((gather_general_kernel<uint64_t, IdxT>), dim3(grid), dim3(kBlock), 0, stream, (uint64_t*)out->data, (const uint64_t*)self->data, idx, istride, g, n, fault); break;
   }
   return check_launch("index_select general");
 }
@@ -235,7 +239,8 @@ struct AdvIndex {
 
 // Byte offset into self of a row (out coordinates decoded from `row`), or -1
 // when an index is out of range.
-__device__ __forceinline__ int64_t adv_row_offset(const AdvIndex& a, int64_t row) {
+__device__ __forceinline__ int64_t adv_row_offset(const AdvIndex& a, int64_t row,
+                                                  IndexFault* fault) {
   int64_t off = 0;
   int64_t ioff[kMaxIdx];
 #pragma unroll
@@ -255,8 +260,12 @@ __device__ __forceinline__ int64_t adv_row_offset(const AdvIndex& a, int64_t row
     if (k < a.n_idx) {
       int64_t v = ((a.idx64 >> k) & 1) ? ((const int64_t*)a.idx[k])[ioff[k]]
                                        : (int64_t)((const int32_t*)a.idx[k])[ioff[k]];
+      const int64_t v0 = v;
       if (v < 0) v += a.limit[k];
-      if (v < 0 || v >= a.limit[k]) return -1;
+      if (v < 0 || v >= a.limit[k]) {
+        record_index_fault(fault, v0, a.limit[k]);
+        return -1;
+      }
       off += v * a.sel_bstride[k];
     }
   }
@@ -268,13 +277,13 @@ template <typename W>
 __global__ __launch_bounds__(kBlock) void adv_index_words_kernel(W* __restrict__ out,
                                                                  const char* __restrict__ src,
                                                                  AdvIndex a, int64_t rows,
-                                                                 int64_t wpr) {
+                                                                 int64_t wpr, IndexFault* fault) {
   const int64_t total = rows * wpr;
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
     const int64_t row = wpr == 1 ? t : t / wpr;
     const int64_t w = t - row * wpr;
-    const int64_t off = adv_row_offset(a, row);
+    const int64_t off = adv_row_offset(a, row, fault);
     out[t] = off >= 0 ? ((const W*)(src + off))[w] : W{};
   }
 }
@@ -285,12 +294,12 @@ template <typename W>
 __global__ __launch_bounds__(kBlock) void adv_index_rows_kernel(W* __restrict__ out,
                                                                 const char* __restrict__ src,
                                                                 AdvIndex a, int64_t rows,
-                                                                int64_t wpr) {
+                                                                int64_t wpr, IndexFault* fault) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
   const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
   for (int64_t row = wave; row < rows; row += nwaves) {
-    const int64_t off = adv_row_offset(a, row);
+    const int64_t off = adv_row_offset(a, row, lane == 0 ? fault : nullptr);
     const W* s = (const W*)(src + (off >= 0 ? off : 0));
     W* o = out + row * wpr;
     for (int64_t w0 = lane; w0 < wpr; w0 += 4 * 64) {
@@ -413,12 +422,12 @@ mi_status_t run_adv_index(const mi_tensor_t* out, const mi_tensor_t* self,
       const int64_t want = (rows + 3) / 4;  // four waves per block
       const unsigned grid = (unsigned)(want < cap ? want : cap);
       hipLaunchKernelGGL((adv_index_rows_kernel<W>), dim3(grid), dim3(kBlock), 0, stream,
-                         (W*)out->data, (const char*)self->data, a, rows, wpr);
+                         (W*)out->data, (const char*)self->data, a, rows, wpr, index_fault_word());
     } else {
       const int64_t want = (rows * wpr + kBlock - 1) / kBlock;
       const unsigned grid = (unsigned)(want < cap ? want : cap);
       hipLaunchKernelGGL((adv_index_words_kernel<W>), dim3(grid), dim3(kBlock), 0, stream,
-                         (W*)out->data, (const char*)self->data, a, rows, wpr);
+                         (W*)out->data, (const char*)self->data, a, rows, wpr, index_fault_word());
     }
     return check_launch("index");
   };

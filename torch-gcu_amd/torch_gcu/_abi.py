@@ -96,6 +96,8 @@ _SIGNATURES = {
     "mi_div_scalar": ([_T, _T, MiScalar, _S], ctypes.c_int),
     "mi_index_select": ([_T, _T, ctypes.c_int64, _T, _S], ctypes.c_int),
     "mi_index": ([_T, _T, ctypes.POINTER(_T), ctypes.c_int32, _S], ctypes.c_int),
+    "mi_index_fault_take": ([ctypes.c_int32, ctypes.POINTER(ctypes.c_int64),
+                             ctypes.POINTER(ctypes.c_int64)], ctypes.c_int32),
     "mi_sum": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
                ctypes.c_int),
     "mi_amax": ([_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.c_int32, _S],
@@ -426,6 +428,16 @@ def mean_noalloc(out, self, dims: Iterable[int] = (), keepdim=False):
     """mi_mean_noalloc: mean with its temporary memory in the library's
     static per-GPU scratch (no allocation)."""
     return _reduce("mi_mean_noalloc", out, self, dims, keepdim)
+
+
+def index_fault_take(device: int = 0):
+    """mi_index_fault_take: (index, dim size) of an out-of-range index the
+    gather kernels met on `device` since the last call, or None; clears it.
+    Call after synchronising with the work."""
+    idx, size = ctypes.c_int64(0), ctypes.c_int64(0)
+    if lib().mi_index_fault_take(device, ctypes.byref(idx), ctypes.byref(size)):
+        return idx.value, size.value
+    return None
 
 
 def softmax(out, self, dim):
