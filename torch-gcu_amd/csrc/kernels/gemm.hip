@@ -409,16 +409,15 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_mfma_kernel(GemmArgs p) 
 // rounds once, stages each wave's 64 x 128 tile through LDS and stores whole
 // 256-byte row segments.
 namespace dl {
-constexpr int BK = 64, STAGES = 2, WM = 4, WN = 2, FM = 2, FN = 4;
+constexpr int BK = 64, STAGES = 2, WM = 4, WN = 2;
 constexpr int NW = WM * WN, NT = 64 * NW;
-constexpr int BM = WM * FM * 32, BN = WN * FN * 32;  // 256 x 256
+constexpr int TM = 64, TN = 128, EP = TN + 8;          // wave tile, epilogue LDS pitch
+constexpr int BM = WM * TM, BN = WN * TN;              // 256 x 256
 constexpr int CH = BK / 8;                             // 16-byte chunks per row
 constexpr int RPK = 512 / BK;                          // rows per 1 KiB wave load
 constexpr int NQA = BM / RPK / NW, NQB = BN / RPK / NW;
 constexpr int LPS = NQA + NQB;                         // wave loads per step
 constexpr int TA = BM * BK, TB = BN * BK;
-constexpr int KS = BK / 16;
-constexpr int TM = FM * 32, TN = FN * 32, EP = TN + 8;  // epilogue tile, LDS pitch
 constexpr size_t LDS_BYTES =
     (size_t)STAGES * (TA + TB) * 2 > (size_t)NW * TM * EP * 2 ? (size_t)STAGES * (TA + TB) * 2
                                                                 : (size_t)NW * TM * EP * 2;
@@ -472,15 +471,27 @@ __device__ __forceinline__ int dl_swz64(int r, int c) { return c ^ (((r >> 1) & 
 template <typename T, bool HAS_BIAS, bool B_INT8, bool SPLIT = false, bool B_KN = false>
 __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* part, int64_t ldp) {
   static_assert(!B_KN || (!B_INT8 && !SPLIT), "row-major B: 16-bit, no split");
-  constexpr int BK = dl::BK, STAGES = dl::STAGES, WN = dl::WN, FM = dl::FM, FN = dl::FN;
+  // MFMA shape: 16 x 16 x 32 (MD = 16) for K-contiguous operands, 32 x 32 x 16
+  // for the transposed row-major B reads, whose lane layout is built for it
+  constexpr bool M16 = !B_KN;
+  constexpr int MD = M16 ? 16 : 32, KPM = 512 / MD;  // MFMA tile edge, k per MFMA
+  constexpr int BK = dl::BK, STAGES = dl::STAGES, WN = dl::WN, TM = dl::TM, TN = dl::TN;
+  constexpr int FM = TM / MD, FN = TN / MD, KS = BK / KPM;
   constexpr int BM = dl::BM, BN = dl::BN, CH = dl::CH, RPK = dl::RPK, NQA = dl::NQA,
-                TA = dl::TA, KS = dl::KS, TM = dl::TM, TN = dl::TN, EP = dl::EP,
-                GROUP_M = dl::GROUP_M;
+                TA = dl::TA, EP = dl::EP, GROUP_M = dl::GROUP_M;
   // the B tile: 16-bit rows of 128 B, or int8 rows of 64 B (widened at fragment read)
   constexpr int NQB = B_INT8 ? dl::NQB8 : dl::NQB;
   constexpr int TB = B_INT8 ? dl::TB8 : dl::TB;
   constexpr int LPS = NQA + NQB;
   typedef typename MfmaOp<T>::vec vec;
+  typedef typename std::conditional<M16, f32x4_t, f32x16>::type acc_t;
+  auto mma = [](vec a, vec b, acc_t c) __attribute__((always_inline)) {
+    if constexpr (!M16) return MfmaOp<T>::mma(a, b, c);
+    else if constexpr (std::is_same<T, BF16>::value)
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  };
   extern __shared__ __align__(16) uint16_t smem[];
   // XCD-aware tile order (round-robin dispatch over 8 XCDs), then groups of
   // GROUP_M row panels so the tiles an XCD runs together share A and B panels
@@ -552,20 +563,22 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
       __builtin_amdgcn_global_load_lds((const void*)(Bb + bo[q]),
                                        (lds_void_t*)(bs + (wave * NQB + q) * 512), 16, 0, 0);
   };
-  // fragment read offsets: lane supplies row l % 32, k chunk 2 s + l / 32
+  // fragment read offsets: lane supplies row l % MD, 16-byte k chunk
+  // (KPM / 8) s + l / MD of substep s
   int roff[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    roff[s] = (lane & 31) * BK + dl_swz(lane & 31, 2 * s + (lane >> 5)) * 8;
+    roff[s] = (lane % MD) * BK + dl_swz(lane % MD, (KPM / 8) * s + lane / MD) * 8;
   }
 
   // acc[j][i] = D^T tile (n rows j, m cols i): B fragments are the MFMA's A
-  // operand, so a lane ends up owning one output row m and 4 runs of 4 n
-  f32x16 acc[FN][FM];
+  // operand, so a lane ends up owning one output row m and runs of 4 n
+  // (4 runs for 32 x 32 tiles, one for 16 x 16)
+  acc_t acc[FN][FM];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int i = 0; i < FM; ++i) acc[j][i] = f32x16{};
+    for (int i = 0; i < FM; ++i) acc[j][i] = acc_t{};
   vec af[2][FM], bfr[2][FN];
   // row-major B: lane (G = lane / 16, j = lane % 16) reads k row
   // 8 (G / 2) + j / 4 (+ 4 for the second half) of a substep, columns
@@ -583,7 +596,7 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
   auto read_frags = [&](int st, int s, int buf) __attribute__((always_inline)) {
     const uint16_t* as = smem + st * (TA + TB) + wm * TM * BK + roff[s];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) af[buf][i] = *(const vec*)(as + i * 32 * BK);
+    for (int i = 0; i < FM; ++i) af[buf][i] = *(const vec*)(as + i * MD * BK);
     if constexpr (B_KN) {
       typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
       const uint16_t* bs = smem + st * (TA + TB) + TA + 16 * s * BN;
@@ -598,18 +611,18 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
       // the bf16 copy of the stage's W rows (converted once per block)
       const uint16_t* bs = smem + STAGES * (TA + TB) + st * dl::TB + wn * TN * BK + roff[s];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * 32 * BK);
+      for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * MD * BK);
     } else {
       const uint16_t* bs = smem + st * (TA + TB) + TA + wn * TN * BK + roff[s];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * 32 * BK);
+      for (int j = 0; j < FN; ++j) bfr[buf][j] = *(const vec*)(bs + j * MD * BK);
     }
   };
   auto mfmas = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int i = 0; i < FM; ++i) acc[j][i] = MfmaOp<T>::mma(bfr[buf][j], af[buf][i], acc[j][i]);
+      for (int i = 0; i < FM; ++i) acc[j][i] = mma(bfr[buf][j], af[buf][i], acc[j][i]);
   };
   // int8 W: wave w copied rows 32 w .. 32 w + 31 of every stage itself, so
   // once its own loads have landed it widens exactly those rows into the
@@ -631,9 +644,80 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
     }
   };
   constexpr int NMF = FM * FN, NDS = FM + FN;
+  // 16 x 16 x 32 schedule, in an order the compiler keeps (a scheduling fence
+  // after every MFMA): A fragments double-buffered, read for the next
+  // substep during the first FM MFMAs; B fragments single-buffered, fragment
+  // j of the next substep read right after its last MFMA (j FM + FM - 1) of
+  // this one, so each read has most of a substep to land; the refill loads
+  // one per NMF / LPS MFMAs of the step's last substep.  Against the 32 x 32
+  // tiles with grouped reads this is 4-10 % faster on the decoder-layer and
+  // config-4 shapes, with bit-identical results.
+  auto issue_one = [&](int st, int k0, int q) __attribute__((always_inline)) {
+    uint16_t* as = smem + st * (TA + TB);
+    uint16_t* bs = as + TA;
+    if (q < NQA) {
+      __builtin_amdgcn_global_load_lds((const void*)((const char*)(A + k0) + ao[q]),
+                                       (lds_void_t*)(as + (wave * NQA + q) * 512), 16, 0, 0);
+    } else {
+      const char* Bb = Bbase + (int64_t)k0 * (B_INT8 ? 1 : 2);
+      __builtin_amdgcn_global_load_lds((const void*)(Bb + bo[q - NQA]),
+                                       (lds_void_t*)(bs + (wave * NQB + q - NQA) * 512), 16, 0,
+                                       0);
+    }
+  };
+  auto read_a = [&](int st, int s, int buf, int i) __attribute__((always_inline)) {
+    const uint16_t* as = smem + st * (TA + TB) + wm * TM * BK + roff[s];
+    af[buf][i] = *(const vec*)(as + i * MD * BK);
+  };
+  auto read_b = [&](int st, int s, int j) __attribute__((always_inline)) {
+    const uint16_t* bs = B_INT8 ? smem + STAGES * (TA + TB) + st * dl::TB + wn * TN * BK + roff[s]
+                                : smem + st * (TA + TB) + TA + wn * TN * BK + roff[s];
+    bfr[0][j] = *(const vec*)(bs + j * MD * BK);
+  };
+  auto mfma_one = [&](int buf, int m) __attribute__((always_inline)) {
+    const int j = m / FM, i = m % FM;
+    acc[j][i] = mma(bfr[0][j], af[buf][i], acc[j][i]);
+  };
   // one K step over stage st.  ISSUE: refill stage st with step kt + STAGES;
   // NEXT: step kt + 1 exists and its first fragments are read here.
   auto step = [&](int st, int kt, bool ISSUE, bool NEXT) __attribute__((always_inline)) {
+    if constexpr (M16) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < KS) {
+#pragma unroll
+          for (int m = 0; m < NMF; ++m) {
+            mfma_one(buf, m);
+            if (m < FM) read_a(st, s + 1, buf ^ 1, m);
+            if (m % FM == FM - 1) read_b(st, s + 1, m / FM);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+          const int nst = st + 1 == STAGES ? 0 : st + 1;
+          if (NEXT) {
+            // as below: step kt + 1 has landed and every wave is done with
+            // stage st (its last fragments were read in the previous substep)
+            if (ISSUE) wait_vmcnt<(STAGES - 2) * LPS>();
+            else wait_vmcnt<0>();
+            convert(nst);
+            __syncthreads();
+          }
+          constexpr int MPL = NMF / LPS > 0 ? NMF / LPS : 1;  // MFMAs per refill load
+#pragma unroll
+          for (int m = 0; m < NMF; ++m) {
+            mfma_one(buf, m);
+            if (ISSUE && m % MPL == 0 && m / MPL < LPS) issue_one(st, (kt + STAGES) * BK, m / MPL);
+            if (NEXT) {
+              if (m < FM) read_a(nst, 0, buf ^ 1, m);
+              if (m % FM == FM - 1) read_b(nst, 0, m / FM);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int buf = s & 1;
@@ -695,11 +779,11 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t n = n0 + wn * TN + j * 32 + 8 * g + 4 * (lane >> 5);
+      for (int g = 0; g < MD * MD / 256; ++g) {
+        const int64_t n = n0 + wn * TN + j * MD + (M16 ? 4 * (lane >> 4) : 8 * g + 4 * (lane >> 5));
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-          const int64_t m = m0 + wm * TM + i * 32 + (lane & 31);
+          const int64_t m = m0 + wm * TM + i * MD + (lane % MD);
           if (m < p.M && n < p.N) {
             const f32x4_t v = {acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2],
                                acc[j][i][4 * g + 3]};
@@ -725,15 +809,15 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int nl = j * 32 + 8 * g + 4 * (lane >> 5);
+    for (int g = 0; g < MD * MD / 256; ++g) {
+      const int nl = j * MD + (M16 ? 4 * (lane >> 4) : 8 * g + 4 * (lane >> 5));
       const int64_t n = n0 + wn * TN + nl;
       f32x4_t sc4 = {1.f, 1.f, 1.f, 1.f}, bb4 = {};
       if constexpr (B_INT8) sc4 = load_col4(p.scale, MI_F32, n, 1, p.N);
       if (row_bias) bb4 = load_col4(p.bias, p.bias_dtype, n, p.bias_sn, p.N, batch * p.bias_sb);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        const int ml = i * 32 + (lane & 31);
+        const int ml = i * MD + (lane % MD);
         const int64_t m = m0 + wm * TM + ml;
         u16x4_t v;
 #pragma unroll
