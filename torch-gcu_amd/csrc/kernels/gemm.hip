@@ -649,7 +649,7 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
   // substep during the first FM MFMAs; B fragments single-buffered, fragment
   // j of the next substep read right after its last MFMA (j FM + FM - 1) of
   // this one, so each read has most of a substep to land; the refill loads
-  // one per NMF / LPS MFMAs of the step's last substep.  Against the 32 x 32
+  // one per two MFMAs of the step's last substep.  Against the 32 x 32
   // tiles with grouped reads this is 4-10 % faster on the decoder-layer and
   // config-4 shapes, with bit-identical results.
   auto issue_one = [&](int st, int k0, int q) __attribute__((always_inline)) {
@@ -703,7 +703,11 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
             convert(nst);
             __syncthreads();
           }
-          constexpr int MPL = NMF / LPS > 0 ? NMF / LPS : 1;  // MFMAs per refill load
+          // one refill load per two MFMAs, from the substep's first MFMA (the
+          // loads spread over all of it measured 1-3 % slower on the decoder
+          // shapes, back to back 2-4 % slower)
+          constexpr int MPL = 2;
+          static_assert(MPL * LPS <= NMF, "every refill load is issued in the substep");
 #pragma unroll
           for (int m = 0; m < NMF; ++m) {
             mfma_one(buf, m);
