@@ -116,14 +116,17 @@ template <typename T, int D>
 __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   typedef typename AttnOp<T>::vec vec;
   typedef FlashCfg<D> C;
-  constexpr int DF = D / 16;  // k-steps of S^T = K Q^T
-  constexpr int DT = D / 32;  // 32-row d tiles of O^T
-  // two stages as separate arrays: with the loop unrolled by two, each
-  // half-iteration reads one and copies into the other, so the compiler can
-  // tell the next tile's copies from this tile's fragment reads (through one
-  // array it made every transposed read wait for the copies in flight)
-  __shared__ __align__(16) uint16_t stage0[C::STAGE];
-  __shared__ __align__(16) uint16_t stage1[C::STAGE];
+  constexpr int DF = D / 16;   // k-steps of S^T = K Q^T
+  constexpr int DT = D / 32;   // 32-row d tiles of O^T
+  constexpr int PS = KT / 16;  // k-steps of O^T += V^T P^T
+  // K and V each in a ring of two slots, as four arrays: the loop below is
+  // unrolled by two so that every LDS access names its array, and the
+  // compiler can tell the copies in flight from the fragment reads (through
+  // one array it made every read wait for all copies)
+  __shared__ __align__(16) uint16_t ks0[C::TILE];
+  __shared__ __align__(16) uint16_t ks1[C::TILE];
+  __shared__ __align__(16) uint16_t vs0[C::TILE];
+  __shared__ __align__(16) uint16_t vs1[C::TILE];
 
   // block -> (b, h, query tile); head-major, longest query tile first
   int bid = (int)blockIdx.x;
@@ -137,10 +140,18 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   const int64_t q0 = (int64_t)qt * QT;
   const int64_t wq0 = q0 + wave * 32;  // this wave's first query row
   const int64_t qrow = wq0 + col;      // the query this lane owns
-
+  // K and V bases are wave-uniform: pinned to scalar registers (the head
+  // index's division would otherwise leave them in VGPRs, and every tile
+  // copy would rebuild its scalar base from them)
+  auto uniform = [](const uint16_t* ptr) __attribute__((always_inline)) {
+    const uint64_t v = (uint64_t)ptr;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const uint16_t*)(((uint64_t)hi << 32) | lo);
+  };
   const uint16_t* Q = p.q + b * p.q_sb + h * p.q_sh;
-  const uint16_t* K = p.k + b * p.k_sb + hk * p.k_sh;
-  const uint16_t* V = p.v + b * p.v_sb + hk * p.v_sh;
+  const uint16_t* K = uniform(p.k + b * p.k_sb + hk * p.k_sh);
+  const uint16_t* V = uniform(p.v + b * p.v_sb + hk * p.v_sh);
 
   // B operand of S^T: lane supplies Q[qrow][16 t + 8 half + i], rows clamped
   vec qf[DF];
@@ -157,55 +168,66 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   // A full tile's copies are a tile base (scalar) plus these per-lane byte
   // offsets of key row `key` of the tile, fixed for the whole loop: no
-  // per-tile address arithmetic on the VALU, which the softmax saturates
-  // (the clamped form cost 33 VALU per tile, 8 of them quarter-rate
-  // multiplies).  Only a last tile that runs past Sk clamps per lane.
-  uint32_t kob[C::NINS / 4], vob[C::NINS / 4];
+  // per-tile address arithmetic on the VALU, which the softmax saturates.
+  // Only a last tile that runs past Sk clamps per lane.
+  // V's chunk swizzle depends only on the key's row within a wave copy, so
+  // V's copies share one per-lane offset (the copy's first key goes into
+  // the scalar base); K's depends on the copy too (one offset per copy).
+  uint32_t kob[C::NINS / 4], vob1;
 #pragma unroll
   for (int i = 0; i < C::NINS / 4; ++i) {
     const int q = wv * (C::NINS / 4) + i;
     const int key = q * C::RPI + lane / C::CPR, cp = lane % C::CPR;
     kob[i] = (uint32_t)(((int64_t)key * k_ss + 8 * (cp ^ C::swz_k(key))) * 2);
-    vob[i] = (uint32_t)(((int64_t)key * v_ss + 8 * (cp ^ C::swz_v(key))) * 2);
   }
-  auto issue_kv = [&](int kv0, uint16_t* ks) __attribute__((always_inline)) {
-    uint16_t* vs = ks + C::TILE;
+  {
+    const int r = lane / C::CPR, cp = lane % C::CPR;
+    vob1 = (uint32_t)(((int64_t)r * v_ss + 8 * (cp ^ C::swz_v(r))) * 2);
+  }
+  auto copy_tile = [&](const uint16_t* G, int g_ss, bool is_v, int kv0,
+                       uint16_t* dst) __attribute__((always_inline)) {
     if (kv0 + KT <= Sk) {
-      const char* kb = (const char*)(K + (int64_t)kv0 * k_ss);
-      const char* vb = (const char*)(V + (int64_t)kv0 * v_ss);
 #pragma unroll
       for (int i = 0; i < C::NINS / 4; ++i) {
         const int q = wv * (C::NINS / 4) + i;
-        // the offsets enter each copy as 32-bit registers (hoisted out of the
-        // loop as 64-bit values they cost a 64-bit add per copy); the copy
-        // then takes the scalar base + 32-bit offset form
-        uint32_t ko = kob[i], vo = vob[i];
-        asm volatile("" : "+v"(ko), "+v"(vo));
-        __builtin_amdgcn_global_load_lds((const void*)(kb + ko), (lds_void_t*)(ks + q * 512), 16, 0,
-                                         0);
-        __builtin_amdgcn_global_load_lds((const void*)(vb + vo), (lds_void_t*)(vs + q * 512), 16, 0,
-                                         0);
+        // the offset enters each copy as a 32-bit register (hoisted out of
+        // the loop as a 64-bit value it costs a 64-bit add per copy); the
+        // copy then takes the scalar base + 32-bit offset form
+        const char* gb = (const char*)(G + (int64_t)(kv0 + (is_v ? q * C::RPI : 0)) * g_ss);
+        uint32_t o = is_v ? vob1 : kob[i];
+        asm volatile("" : "+v"(o));
+        __builtin_amdgcn_global_load_lds((const void*)(gb + o), (lds_void_t*)(dst + q * 512), 16,
+                                         0, 0);
       }
     } else {
+      // (the lane id passes through an empty asm so that nothing of this
+      // rare path is hoisted into registers held across the loop)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
 #pragma unroll
       for (int i = 0; i < C::NINS / 4; ++i) {
         const int q = wv * (C::NINS / 4) + i;
-        const int key = q * C::RPI + lane / C::CPR, cp = lane % C::CPR;
+        const int key = q * C::RPI + ln / C::CPR, cp = ln % C::CPR;
         const int gk = min(kv0 + key, Sk - 1);
-        __builtin_amdgcn_global_load_lds((const void*)(K + gk * k_ss + 8 * (cp ^ C::swz_k(key))),
-                                         (lds_void_t*)(ks + q * 512), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(V + gk * v_ss + 8 * (cp ^ C::swz_v(key))),
-                                         (lds_void_t*)(vs + q * 512), 16, 0, 0);
+        const int sw = is_v ? C::swz_v(key) : C::swz_k(key);
+        __builtin_amdgcn_global_load_lds((const void*)(G + gk * g_ss + 8 * (cp ^ sw)),
+                                         (lds_void_t*)(dst + q * 512), 16, 0, 0);
       }
     }
   };
+  auto copy_k = [&](int kv0, uint16_t* dst) __attribute__((always_inline)) {
+    copy_tile(K, k_ss, false, kv0, dst);
+  };
+  auto copy_v = [&](int kv0, uint16_t* dst) __attribute__((always_inline)) {
+    copy_tile(V, v_ss, true, kv0, dst);
+  };
   // K fragment k-step t of sub-tile st: key 32 st + col, chunk 2 t + half
   // (swz_k(32 + col) == swz_k(col))
-  int koff[DF];
+  int koff[DF];  // bytes
   {
     const int sk = C::swz_k(col);
 #pragma unroll
-    for (int t = 0; t < DF; ++t) koff[t] = col * D + 8 * ((2 * t + half) ^ sk);
+    for (int t = 0; t < DF; ++t) koff[t] = (col * D + 8 * ((2 * t + half) ^ sk)) * 2;
   }
   // V^T fragment (k-step t, d tile dt) by two transposed reads: in each 16-lane
   // group G, lane j names row key 16 t + 4 (G / 2) + j / 4 (then + 8), columns
@@ -219,147 +241,227 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
     const int sv = C::swz_v(key) >> 2;        // swz_v(key + 16 t) == swz_v(key)
     const int low = 2 * (G & 1) + ((j & 3) >> 1), within = 4 * (j & 1);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) voff[dt] = key * D + 8 * (4 * (dt ^ sv) + low) + within;
+    for (int dt = 0; dt < DT; ++dt) voff[dt] = (key * D + 8 * (4 * (dt ^ sv) + low) + within) * 2;
   }
+  // The offsets pass through an empty asm at each read: the compiler then
+  // adds the array (a constant LDS address) in the read's immediate offset
+  // instead of keeping array + offset for every array and offset in
+  // registers across the loop (48 more VGPRs, and spills)
+  auto read_k = [&](const uint16_t* ks, int t, vec* kf) __attribute__((always_inline)) {
+    int ko = koff[t];
+    asm volatile("" : "+v"(ko));
+    kf[0] = *(const vec*)((const char*)ks + ko);
+    kf[1] = *(const vec*)((const char*)(ks + 32 * D) + ko);
+  };
+  auto read_v = [&](const uint16_t* vs, int t, vec* vf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      int vo = voff[d];
+      asm volatile("" : "+v"(vo));
+      const uint16_t* vb = (const uint16_t*)((const char*)(vs + 16 * t * D) + vo);
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)vb);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 8 * D));
+      vf[d] = __builtin_bit_cast(vec, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
 
   f32x16 o[DT];
 #pragma unroll
   for (int d = 0; d < DT; ++d) o[d] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;
+  // m_run: the exact running row max of the scaled scores (log2 units);
+  // corr: the factor that takes O and l from the previous max to m_run
+  float m_run = -INFINITY, l_run = 0.f, corr = 1.f;
+  const float sc = p.scale_log2;
+  const bool neg = sc < 0.f;
 
   const int kv_end = (int)(p.causal ? min(p.Sk, q0 + QT) : p.Sk);
   const int n_tiles = (kv_end + KT - 1) / KT;
   const int wq = (int)wq0, qr = (int)qrow;
-  issue_kv(0, stage0);
-  // the Q fragments and the first tile have landed: inside the loop the only
-  // outstanding global loads are the next tile's K / V copies
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  auto tile = [&](int it, const uint16_t* ks, uint16_t* next) __attribute__((always_inline)) {
-    const int kv0 = it * KT;
-    const bool more = it + 1 < n_tiles;
-    if (more) issue_kv(kv0 + KT, next);
-    __builtin_amdgcn_sched_barrier(0);
-    const uint16_t* vs = ks + C::TILE;
-    if (!p.causal || kv0 <= wq + 31) {
-      // ---- S^T = K Q^T: two 32-key tiles x this wave's 32 queries, the two
-      // accumulator chains interleaved ----
-      f32x16 s[2] = {f32x16{}, f32x16{}};
-      const uint16_t* kb1 = ks + 32 * D;
-      // K fragments double-buffered one k-step ahead of their MFMAs
-      vec kf[2][2];
-      kf[0][0] = *(const vec*)(ks + koff[0]);
-      kf[0][1] = *(const vec*)(kb1 + koff[0]);
+  // the last key tile with a key this wave's queries see (tiles above the
+  // diagonal are skipped; the wave still copies and meets the barriers)
+  const int last = p.causal ? min(n_tiles - 1, (wq + 31) / KT) : n_tiles - 1;
+
+  // S^T = K Q^T of one tile: two 32-key MFMA tiles x this wave's 32 queries.
+  // VALU work of the previous tile is interleaved by the caller.
+  // Scores: accumulator r of sub-tile st holds key kv0 + 32 st + 8 (r / 4) +
+  // 4 half + r % 4.  Masked keys get the raw score whose scaled value is -inf.
+  // A key is dead at or past min(Sk, qr + 1) (causal) or Sk; per element
+  // the test compares a constant with one per-lane limit.  The lane id is
+  // read afresh by an asm statement (mbcnt), so no per-lane value of this
+  // rare path stays in a register across the loop.
+  auto mask = [&](f32x16* s, int kv0) __attribute__((always_inline)) {
+    if ((kv0 + KT > Sk) || (p.causal && kv0 + KT - 1 > wq)) {
+      const float dead_s = neg ? INFINITY : -INFINITY;
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+      const int key_end = p.causal ? min(Sk, wq + (ln & 31) + 1) : Sk;
+      const int lim = key_end - kv0 - 4 * (ln >> 5);
 #pragma unroll
-      for (int t = 0; t < DF; ++t) {
-        if (t + 1 < DF) {
-          kf[(t + 1) & 1][0] = *(const vec*)(ks + koff[t + 1]);
-          kf[(t + 1) & 1][1] = *(const vec*)(kb1 + koff[t + 1]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        s[0] = AttnOp<T>::mma(kf[t & 1][0], qf[t], s[0]);
-        s[1] = AttnOp<T>::mma(kf[t & 1][1], qf[t], s[1]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // ---- mask, online softmax in the log2 domain ----
-      // accumulator r of tile st holds key kv0 + 32 st + 8 (r / 4) + 4 half + r % 4.
-      // The max is taken over the raw scores times the sign of the scale (a
-      // free source negation) and the scale is folded into the exponent:
-      // p = exp2(s * scale_log2 - m_run).  Dead keys get the raw score whose
-      // scaled value is -inf.
-      const bool neg = p.scale_log2 < 0.f;
-      float mx = -INFINITY;
-      if ((kv0 + KT > Sk) || (p.causal && kv0 + KT - 1 > wq)) {
-        const float dead_s = neg ? INFINITY : -INFINITY;
+      for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+        for (int r = 0; r < 16; ++r)
+          s[st][r] = 32 * st + 8 * (r >> 2) + (r & 3) >= lim ? dead_s : s[st][r];
+    }
+  };
+  // max over sub-tile st's 16 scores (sign-adjusted: the scale's sign is a
+  // free source negation, the scale itself is folded into the exponent)
+  auto part_max = [&](const f32x16* s, int st, float mx) __attribute__((always_inline)) {
+    if (!neg) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + 32 * st + 8 * (r >> 2) + 4 * half + (r & 3);
-            const bool dead = key >= Sk || (p.causal && key > qr);
-            const float x = dead ? dead_s : s[st][r];
-            s[st][r] = x;
-            mx = fmaxf(mx, neg ? -x : x);
-          }
-      } else if (!neg) {
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
+    } else {
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, -s[st][r]);
+    }
+    return mx;
+  };
+  // the new running max: O and l are rescaled whenever it grows, so the key
+  // at the max gets p = 1 exactly (with a stale max that dominant weight
+  // carried the rounding to the input type too, and keys whose scores ramp
+  // up along a 1024-key sequence missed the bf16 bar)
+  auto update_max = [&](float mx) __attribute__((always_inline)) {
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * fabsf(sc);
+    corr = 1.f;
+    if (mx > m_run) {
+      corr = __builtin_amdgcn_exp2f(m_run - mx);  // 0 when nothing was visible yet
+      m_run = mx;
+    }
+  };
+  // P as the B operand of O^T += V^T P^T: k-step t (16 keys) takes
+  // accumulators 8 (t % 2) .. 8 (t % 2) + 7 of sub-tile t / 2.  Score e
+  // (0..31) of the tile is accumulator e % 16 of sub-tile e / 16; p is
+  // computed in place and rounded to the input type per k-step.
+  vec pk[PS];
+  float rs = 0.f, m_use = 0.f;
+  auto exp_range = [&](f32x16* s, int e0, int e1) __attribute__((always_inline)) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
-      } else {
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, -s[st][r]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * fabsf(p.scale_log2);
-      // m_run is the exact running row max (scaled, log2 units); O and l are
-      // rescaled whenever it grows.  P is rounded to the input type, and the
-      // key at the running max gets p = 1 exactly: with a stale max (rescaled
-      // only when a row max grew by more than 2^8) that dominant weight
-      // carried the rounding too, and on keys whose scores ramp up along a
-      // 1024-key sequence the output was 1.5x further from the float64
-      // result than CPU ATen's (one element past the bf16 bar).
-      float corr = 1.0f;
-      if (mx > m_run) {
-        corr = __builtin_amdgcn_exp2f(m_run - mx);  // 0 when nothing was visible yet
-        m_run = mx;
-      }
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;  // nothing visible yet
-      const float sc = p.scale_log2;
-      // P as the B operand of O^T += V^T P^T: k-step t (16 keys) takes
-      // accumulators 8 (t % 2) .. 8 (t % 2) + 7 of tile t / 2
-      vec pk[KT / 16];
-      float rs = 0.f;
-#pragma unroll
-      for (int t = 0; t < KT / 16; ++t) {
+    for (int e = e0; e < e1; ++e) {
+      const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e >> 4][e & 15], sc, -m_use));
+      s[e >> 4][e & 15] = x;
+      rs += x;
+      if ((e & 7) == 7) {
         f32x8 pf;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t >> 1][8 * (t & 1) + i], sc, -m_use));
-          rs += pf[i];
-        }
-        pk[t] = __builtin_convertvector(pf, vec);
-      }
-      l_run = l_run * corr + rs;
-      if (__ballot(corr != 1.0f)) {
-#pragma unroll
-        for (int d = 0; d < DT; ++d) o[d] *= corr;
-      }
-      // ---- O^T += V^T P^T: the lane reads V^T[d][key] for the same keys:
-      // 16 t + 4 half + 0..3 and 16 t + 8 + 4 half + 0..3; a k-step's DT
-      // fragments are read before its MFMAs ----
-      vec vf[2][DT];
-      auto read_v = [&](int t, int buf) __attribute__((always_inline)) {
-#pragma unroll
-        for (int d = 0; d < DT; ++d) {
-          typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-          const uint16_t* vb = vs + 16 * t * D + voff[d];
-          const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)vb);
-          const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 8 * D));
-          const s16x4 lo = a0, hi = a1;
-          vf[buf][d] = __builtin_bit_cast(vec, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
-      };
-      read_v(0, 0);
-#pragma unroll
-      for (int t = 0; t < KT / 16; ++t) {
-        if (t + 1 < KT / 16) read_v(t + 1, (t + 1) & 1);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int d = 0; d < DT; ++d) o[d] = AttnOp<T>::mma(vf[t & 1][d], pk[t], o[d]);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 8; ++i) pf[i] = s[e >> 4][(e & 8) + i];
+        pk[e >> 3] = __builtin_convertvector(pf, vec);
       }
     }
-    // this wave's copies of the next tile have landed; the barrier publishes
-    // every wave's and retires this tile's stage for the copy after next
-    if (more) __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
   };
-  for (int it = 0; it < n_tiles; it += 2) {
-    tile(it, stage0, stage1);
-    if (it + 1 < n_tiles) tile(it + 1, stage1, stage0);
+  auto rescale_range = [&](int i0, int i1) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) o[i >> 4][i & 15] *= corr;
+  };
+
+  // one key tile j, software-pipelined: its scores sc_ (masked, their max
+  // already in m_run) are turned into P while the MFMAs compute the next
+  // tile's scores into sn (NXT: the wave sees a key of tile j + 1), and its
+  // V^T P^T MFMAs run while the next tile's max is taken.  kr / vr: the
+  // slots holding K(j + 1) and V(j); kw / vw: the slots that receive
+  // K(j + 2) and V(j + 1).
+  constexpr int RPG = DT * 16 / DF;  // O rescales per S^T k-step
+  constexpr int EPG = 16 / DF;       // exponentials per S^T k-step (first half of P)
+  auto sync_and_copy = [&](int j, uint16_t* kw, uint16_t* vw) __attribute__((always_inline)) {
+    // this wave's copies of K(j + 1) and V(j) have landed; the barrier
+    // publishes every wave's and tells that all are done with K(j) and V(j - 1)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (j + 2 < n_tiles) copy_k((j + 2) * KT, kw);
+    if (j + 1 < n_tiles) copy_v((j + 1) * KT, vw);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto iter = [&](auto nxt_c, int j, const uint16_t* kr, const uint16_t* vr, uint16_t* kw,
+                  uint16_t* vw, f32x16* sc_, f32x16* sn) __attribute__((always_inline)) {
+    constexpr bool NXT = decltype(nxt_c)::value;
+    sync_and_copy(j, kw, vw);
+    m_use = m_run == -INFINITY ? 0.f : m_run;  // nothing visible yet
+    l_run *= corr;
+    rs = 0.f;
+    // each group: its fragment reads, then VALU work that does not need
+    // them (covering part of the LDS latency), then its MFMAs
+    vec kf[2], vf[DT];
+    // ---- phase 1: S^T(j + 1) on the MFMAs; O *= corr and the first half of P(j) ----
+    if constexpr (NXT) {
+      sn[0] = f32x16{};
+      sn[1] = f32x16{};
+#pragma unroll
+      for (int t = 0; t < DF; ++t) {
+        read_k(kr, t, kf);
+        rescale_range(t * RPG, (t + 1) * RPG);
+        exp_range(sc_, t * EPG, (t + 1) * EPG);
+        sn[0] = AttnOp<T>::mma(kf[0], qf[t], sn[0]);
+        sn[1] = AttnOp<T>::mma(kf[1], qf[t], sn[1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      rescale_range(0, DT * 16);
+      exp_range(sc_, 0, 16);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // ---- phase 2: O^T += V^T P^T(j) on the MFMAs; the second half of P(j),
+    // then the mask and max of S(j + 1) ----
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < PS; ++t) {
+      read_v(vr, t, vf);
+      if (t == 0) exp_range(sc_, 16, 24);
+      if (t == 1) {
+        exp_range(sc_, 24, 32);
+        l_run += rs;
+      }
+      if constexpr (NXT) {
+        if (t == 2) {
+          mask(sn, (j + 1) * KT);
+          mx = part_max(sn, 0, mx);
+        }
+        if (t == 3) {
+          mx = part_max(sn, 1, mx);
+          update_max(mx);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < DT; ++d) o[d] = AttnOp<T>::mma(vf[d], pk[t], o[d]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  typedef std::integral_constant<bool, true> Yes;
+  typedef std::integral_constant<bool, false> No;
+
+  // prologue: K(0), V(0) landed, K(1) in flight; S(0) and its max (every
+  // wave sees key 0)
+  copy_k(0, ks0);
+  copy_v(0, vs0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (n_tiles > 1) copy_k(KT, ks1);
+  f32x16 sa[2] = {f32x16{}, f32x16{}}, sb[2];
+  {
+    vec kf[2];
+#pragma unroll
+    for (int t = 0; t < DF; ++t) {
+      read_k(ks0, t, kf);
+      sa[0] = AttnOp<T>::mma(kf[0], qf[t], sa[0]);
+      sa[1] = AttnOp<T>::mma(kf[1], qf[t], sa[1]);
+    }
+    mask(sa, 0);
+    update_max(part_max(sa, 1, part_max(sa, 0, -INFINITY)));
   }
+  // tiles 0 .. last with compute (even tiles read K from slot 1 and V from
+  // slot 0), then barriers and copies only up to the block's last tile
+  int j = 0;
+  for (; j + 1 < last; j += 2) {
+    iter(Yes(), j, ks1, vs0, ks0, vs1, sa, sb);
+    iter(Yes(), j + 1, ks0, vs1, ks1, vs0, sb, sa);
+  }
+  if (j < last) {
+    iter(Yes(), j, ks1, vs0, ks0, vs1, sa, sb);
+    iter(No(), j + 1, ks0, vs1, ks1, vs0, sb, sa);
+    j += 2;
+  } else {
+    iter(No(), j, ks1, vs0, ks0, vs1, sa, sb);
+    j += 1;
+  }
+  for (; j < n_tiles; ++j) sync_and_copy(j, (j & 1) ? ks1 : ks0, (j & 1) ? vs0 : vs1);
 
   // ---- normalise and store: accumulator r of d tile dt is
   // O[qrow][32 dt + 8 (r / 4) + 4 half + r % 4] ----
