@@ -453,7 +453,19 @@ __device__ __forceinline__ void wait_later(int later) {
   }
 }
 
-__device__ __forceinline__ int dl_swz(int r, int c) { return c ^ ((r & 7) ^ ((r >> 3) & 1)); }
+// 128-byte rows (8 chunks of 16 B): chunk c of row r at c ^ f(r), with
+// f(r) = (r & 3) ^ 5 (bit 2 of r) ^ 4 (bit 3 of r): bit 0 = r0 ^ r2, bit 1 =
+// r1, bit 2 = r2 ^ r3.  Chosen by timing every linear map of the row's low 4
+// bits to a chunk mask on this LDS (a 64-lane ds_read_b128 takes 4 cycles
+// without conflicts, 5.5 with the 2-way ones): it reads without conflicts
+// 16 x 16 x 32 fragments (row l % 16, chunk 4 s + l / 16), 32 x 32 x 16
+// fragments (row l % 32, chunk 2 s + l / 32), and the int8 widening's
+// patterns (2 lanes a row x 4 chunks, 4 lanes a row x 2 chunks).  The mask
+// (r & 7) ^ (r >> 3 & 1) it replaces made every 16 x 16 x 32 fragment read
+// two-way conflicted (SQ_LDS_BANK_CONFLICT half of the LDS-active cycles).
+__device__ __forceinline__ int dl_swz(int r, int c) {
+  return c ^ (r & 3) ^ (((r >> 2) & 1) * 5) ^ ((r >> 1) & 4);
+}
 // 64-byte rows: chunk c of row r at c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1), conflict-free for
 // 16-byte reads of 16 consecutive rows under 32- or 64-bank LDS
 __device__ __forceinline__ int dl_swz64(int r, int c) { return c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1)); }
