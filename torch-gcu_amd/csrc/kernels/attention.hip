@@ -223,33 +223,40 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   };
   // K fragment k-step t of sub-tile st: key 32 st + col, chunk 2 t + half
   // (swz_k(32 + col) == swz_k(col))
-  int koff[DF];  // bytes
+  // byte offset (col D + 8 ((2 t + half) ^ sk)) 2 = 2 col D + 16 (half ^ (sk & 1))
+  // + 32 (t ^ (sk >> 1)); the three terms occupy disjoint bits, so it is
+  // kbm ^ 32 t with kbm the t = 0 offset: one register, one XOR per read
+  int kbm;
   {
     const int sk = C::swz_k(col);
-#pragma unroll
-    for (int t = 0; t < DF; ++t) koff[t] = (col * D + 8 * ((2 * t + half) ^ sk)) * 2;
+    kbm = 2 * col * D + 16 * (half ^ (sk & 1)) + 32 * (sk >> 1);
   }
   // V^T fragment (k-step t, d tile dt) by two transposed reads: in each 16-lane
   // group G, lane j names row key 16 t + 4 (G / 2) + j / 4 (then + 8), columns
   // d0 = 32 dt + 16 (G % 2) + 4 (j % 4) .. + 3, and receives d = 32 dt +
   // 16 (G % 2) + j for 4 consecutive keys: the A operand of O^T += V^T P^T
   // for keys 16 t + 4 half + 0..3 and 16 t + 8 + 4 half + 0..3
-  int voff[DT];
+  int vbm;
   {
     const int G = lane >> 4, j = lane & 15;
     const int key = 4 * (G >> 1) + (j >> 2);  // plus 16 t
     const int sv = C::swz_v(key) >> 2;        // swz_v(key + 16 t) == swz_v(key)
     const int low = 2 * (G & 1) + ((j & 3) >> 1), within = 4 * (j & 1);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) voff[dt] = (key * D + 8 * (4 * (dt ^ sv) + low) + within) * 2;
+    // bytes 2 key D + 64 (dt ^ sv) + 16 low + 2 within: disjoint bits again,
+    // so vbm ^ 64 dt
+    vbm = 2 * key * D + 64 * sv + 16 * low + 2 * within;
   }
-  // The offsets pass through an empty asm at each read: the compiler then
-  // adds the array (a constant LDS address) in the read's immediate offset
-  // instead of keeping array + offset for every array and offset in
-  // registers across the loop (48 more VGPRs, and spills)
+  // Each read's offset is made by an asm XOR of the one base register: the
+  // compiler then adds the array (a constant LDS address) in the read's
+  // immediate offset instead of keeping array + offset for every array and
+  // offset in registers across the loop (48 more VGPRs, and spills)
+  auto xor_off = [](int base, int m) __attribute__((always_inline)) {
+    int r;
+    asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "i"(m), "v"(base));
+    return r;
+  };
   auto read_k = [&](const uint16_t* ks, int t, vec* kf) __attribute__((always_inline)) {
-    int ko = koff[t];
-    asm volatile("" : "+v"(ko));
+    const int ko = xor_off(kbm, 32 * t);
     kf[0] = *(const vec*)((const char*)ks + ko);
     kf[1] = *(const vec*)((const char*)(ks + 32 * D) + ko);
   };
@@ -257,8 +264,7 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
       typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-      int vo = voff[d];
-      asm volatile("" : "+v"(vo));
+      const int vo = xor_off(vbm, 64 * d);
       const uint16_t* vb = (const uint16_t*)((const char*)(vs + 16 * t * D) + vo);
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)vb);
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + 8 * D));
@@ -379,18 +385,20 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
     rs = 0.f;
     // each group: its fragment reads, then VALU work that does not need
     // them (covering part of the LDS latency), then its MFMAs
-    vec kf[2], vf[DT];
-    // ---- phase 1: S^T(j + 1) on the MFMAs; O *= corr and the first half of P(j) ----
+    vec kf[2][2], vf[DT];
+    // ---- phase 1: S^T(j + 1) on the MFMAs; O *= corr and the first half of P(j);
+    // K fragments read one k-step ahead of their MFMAs ----
     if constexpr (NXT) {
       sn[0] = f32x16{};
       sn[1] = f32x16{};
+      read_k(kr, 0, kf[0]);
 #pragma unroll
       for (int t = 0; t < DF; ++t) {
-        read_k(kr, t, kf);
+        if (t + 1 < DF) read_k(kr, t + 1, kf[(t + 1) & 1]);
         rescale_range(t * RPG, (t + 1) * RPG);
         exp_range(sc_, t * EPG, (t + 1) * EPG);
-        sn[0] = AttnOp<T>::mma(kf[0], qf[t], sn[0]);
-        sn[1] = AttnOp<T>::mma(kf[1], qf[t], sn[1]);
+        sn[0] = AttnOp<T>::mma(kf[t & 1][0], qf[t], sn[0]);
+        sn[1] = AttnOp<T>::mma(kf[t & 1][1], qf[t], sn[1]);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
