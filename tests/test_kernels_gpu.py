@@ -368,10 +368,14 @@ def test_reduce_long_rows_and_noncontiguous():
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64, torch.int64,
                                    torch.int32, torch.uint8])
 @pytest.mark.parametrize("shape,dims", [((3000, 257), (0,)), ((2, 1500, 1024), (1,)),
-                                        ((1024, 4099), (0,)), ((700, 8, 3), (0,))])
+                                        ((1024, 4099), (0,)), ((700, 8, 3), (0,)),
+                                        ((2, 600, 4096), (1,)), ((600, 2052), (0,))])
 def test_column_reduce_split_pass(dtype, shape, dims):
     """Column reductions long enough to be split over blocks and finished by
-    the second pass over partials, with aligned (vector) and odd widths."""
+    the second pass over partials, with aligned (vector) and odd widths; the
+    last two shapes take 1024-lane column blocks (two outer slices; a row of
+    513 column vectors, half a block idle) and, in fp32 accumulation, the
+    float4 finish over several outer slices and a ragged last block."""
     x = rand(shape, dtype, 29)
     ref = aten.sum_(x, list(dims))
     out = empty_like_ref(ref)

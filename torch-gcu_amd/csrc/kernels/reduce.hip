@@ -77,6 +77,14 @@ template <typename A>
 __device__ __forceinline__ A red_combine(int op, A a, A b) {
   return op == R_MAX ? nan_max(a, b) : a + b;
 }
+// The same with the operation fixed at compile time (MX: max, else sum).  In
+// the column kernels the run-time form became a scalar branch and a wait per
+// element, so every add waited for its own load.
+template <bool MX, typename A>
+__device__ __forceinline__ A red_comb(A a, A b) {
+  if constexpr (MX) return nan_max(a, b);
+  else return a + b;
+}
 
 template <typename A>
 __device__ __forceinline__ A wave_red(int op, A v) {
@@ -112,8 +120,11 @@ constexpr int kRowUnroll = 8;
 // Block (row, split) reduces elements [split*chunk, min(R, (split+1)*chunk)):
 // 512 lanes, eight 16-byte non-temporal loads in flight per lane (a config-2
 // row of 64,000 B is one batch), a wave64 shuffle reduction, then the
-// per-wave results in a fixed order.
-template <typename Tag>
+// per-wave results in a fixed order.  The loads are unconditional (a vector
+// past the end re-reads the last one, whose values are then not added) and
+// the operation is fixed at compile time (MX: max, else sum), so the eight
+// loads are issued back to back and the adds wait on them in turn.
+template <typename Tag, bool MX>
 __global__ __launch_bounds__(kRowBlock) void row_reduce_kernel(
     const typename RT<Tag>::storage* __restrict__ in, int64_t R, int64_t row_stride,
     int64_t chunk, int op, RedOut out) {
@@ -143,20 +154,20 @@ __global__ __launch_bounds__(kRowBlock) void row_reduce_kernel(
       for (int u = 0; u < kRowUnroll; ++u) {
         const int64_t v = v0 + (int64_t)u * kRowBlock;
         ok[u] = v < nv;
-        if (ok[u]) x[u] = ld_stream(pv + v);
+        x[u] = ld_stream(pv + (ok[u] ? v : nv - 1));
       }
 #pragma unroll
       for (int u = 0; u < kRowUnroll; ++u) {
         if (ok[u]) {
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) acc = red_combine(op, acc, RT<Tag>::load(x[u].s[e]));
+          for (int e = 0; e < VEC; ++e) acc = red_comb<MX>(acc, RT<Tag>::load(x[u].s[e]));
         }
       }
     }
     i = beg + nv * VEC;
   }
   for (int64_t j = i + threadIdx.x; j < end; j += kRowBlock)
-    acc = red_combine(op, acc, RT<Tag>::load(p[j]));
+    acc = red_comb<MX>(acc, RT<Tag>::load(p[j]));
   // block combine
   acc = wave_red(op, acc);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -185,25 +196,29 @@ __global__ __launch_bounds__(256) void row_reduce_wave_kernel(
   if (lane == 0) red_store(out, op, row, acc);
 }
 
-constexpr int kColBlock = 256;
-constexpr int kColUnroll = 4;
+constexpr int kColUnroll = 4;  // rows a batch for narrow loads (two batches in flight)
 
-// [outer, R, inner] column reduction over R, first pass: 256 lanes side by
-// side along a row (a lane owns VEC adjacent columns, so a block reads
-// 256 * VEC contiguous elements of each row), each walking the rows of its
-// split in batches of four rows, two batches in flight.  Output layout
-// [outer, splits, inner] (Acc partials, or the final value when there is one
-// split).
-template <typename Tag, int VEC>
-__global__ __launch_bounds__(kColBlock) void col_reduce_kernel(
+// [outer, R, inner] column reduction over R, first pass: NTH lanes (256, 512
+// or 1024) side by side along a row (a lane owns VEC adjacent columns, so a
+// block reads NTH * VEC contiguous elements of each row: up to a whole
+// 16 KiB row of config 2's fp32 [16384, 4096]), each walking the rows of its
+// split in batches of U rows, two batches in flight (U = 2 for 16-byte
+// loads, kColUnroll for narrower ones).  Output layout [outer, splits,
+// inner] (Acc partials, or the final value when there is one split).
+// (On config 2's mean(0), 1024-lane blocks with two 16-byte loads a batch
+// ran the pass in 40.2 us, against 42.7 us for 256-lane blocks with four
+// and 43.9 us for 1024 lanes with eight: whole-row blocks read each row as
+// one 16 KiB run, and more loads in flight only queued.)
+template <typename Tag, int VEC, int NTH, bool MX>
+__global__ __launch_bounds__(NTH) void col_reduce_kernel(
     const typename RT<Tag>::storage* __restrict__ in, int64_t R, int64_t inner,
     int64_t chunk, int op, RedOut out) {
   typedef typename RT<Tag>::storage St;
   typedef typename RT<Tag>::acc A;
   const int64_t ncv = inner / VEC;  // column vectors
-  const int64_t ncb = (ncv + kColBlock - 1) / kColBlock;
+  const int64_t ncb = (ncv + NTH - 1) / NTH;
   const int64_t o = blockIdx.x / ncb;
-  const int64_t cv = (blockIdx.x - o * ncb) * kColBlock + threadIdx.x;
+  const int64_t cv = (blockIdx.x - o * ncb) * NTH + threadIdx.x;
   if (cv >= ncv) return;
   const int64_t split = blockIdx.y;
   const int64_t beg = split * chunk;
@@ -216,42 +231,43 @@ __global__ __launch_bounds__(kColBlock) void col_reduce_kernel(
   };
   const V* base = (const V*)(in + (o * R) * inner) + cv;
   int64_t r = beg;
-  // two batches of kColUnroll rows: the loads of batch b + 1 are issued
-  // before batch b is added, so up to 2 * kColUnroll loads are in flight;
-  // rows are still added in ascending order
-  V xa[kColUnroll], xb[kColUnroll];
+  // two batches of U rows: the loads of batch b + 1 are issued before batch
+  // b is added, so up to 2 U loads are in flight; rows are still added in
+  // ascending order
+  constexpr int U = sizeof(V) == 16 ? 2 : kColUnroll;
+  V xa[U], xb[U];
   auto fetch = [&](V* x, int64_t r0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < kColUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       if constexpr (sizeof(V) == 16) x[u] = ld_stream(base + (r0 + u) * ncv);
       else x[u] = base[(r0 + u) * ncv];
     }
   };
   auto add = [&](const V* x) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < kColUnroll; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = red_combine(op, acc[e], RT<Tag>::load(x[u].s[e]));
+      for (int e = 0; e < VEC; ++e) acc[e] = red_comb<MX>(acc[e], RT<Tag>::load(x[u].s[e]));
   };
-  if (r + kColUnroll <= end) {
+  if (r + U <= end) {
     fetch(xa, r);
     while (true) {
-      const bool nb = r + 2 * kColUnroll <= end;
-      if (nb) fetch(xb, r + kColUnroll);
+      const bool nb = r + 2 * U <= end;
+      if (nb) fetch(xb, r + U);
       add(xa);
-      r += kColUnroll;
+      r += U;
       if (!nb) break;
-      const bool na = r + 2 * kColUnroll <= end;
-      if (na) fetch(xa, r + kColUnroll);
+      const bool na = r + 2 * U <= end;
+      if (na) fetch(xa, r + U);
       add(xb);
-      r += kColUnroll;
+      r += U;
       if (!na) break;
     }
   }
   for (; r < end; ++r) {
     const V x = base[r * ncv];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] = red_combine(op, acc[e], RT<Tag>::load(x.s[e]));
+    for (int e = 0; e < VEC; ++e) acc[e] = red_comb<MX>(acc[e], RT<Tag>::load(x.s[e]));
   }
 #pragma unroll
   for (int e = 0; e < VEC; ++e)
@@ -261,16 +277,20 @@ __global__ __launch_bounds__(kColBlock) void col_reduce_kernel(
 // Second pass over Acc partials [outer, S, inner]: a block is 16 columns x
 // 16 lanes down the S partials; the 16 lane results are combined in a fixed
 // order through LDS, so the result does not depend on scheduling.
-template <typename A>
+// (Loads are unconditional: a lane past the last column reads the last one
+// and stores nothing; loads under the guard were each waited for in turn.)
+template <typename A, bool MX>
 __global__ __launch_bounds__(256) void col_finish_kernel(const A* __restrict__ part, int64_t outer,
                                                          int64_t S, int64_t inner, int op,
                                                          RedOut out) {
   __shared__ A red[16][17];
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-  const int64_t c = (int64_t)blockIdx.x * 16 + tx;  // flattened (outer, inner) column
-  const bool live = c < outer * inner;
+  const int64_t total = outer * inner;
+  const int64_t cl = (int64_t)blockIdx.x * 16 + tx;  // flattened (outer, inner) column
+  const bool live = cl < total;
+  const int64_t c = live ? cl : total - 1;
   A acc = red_ident<A>(op);
-  if (live) {
+  {
     const int64_t o = c / inner, i = c - o * inner;
     const A* p = part + o * S * inner + i;
     int64_t s = ty;
@@ -280,17 +300,65 @@ __global__ __launch_bounds__(256) void col_finish_kernel(const A* __restrict__ p
 #pragma unroll
       for (int u = 0; u < 16; ++u) x[u] = p[(s + 16 * u) * inner];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) acc = red_combine(op, acc, x[u]);
+      for (int u = 0; u < 16; ++u) acc = red_comb<MX>(acc, x[u]);
     }
-    for (; s < S; s += 16) acc = red_combine(op, acc, p[s * inner]);
+    for (; s < S; s += 16) acc = red_comb<MX>(acc, p[s * inner]);
   }
   red[ty][tx] = acc;
   __syncthreads();
   if (ty == 0 && live) {
     A r = red[0][tx];
 #pragma unroll
-    for (int y = 1; y < 16; ++y) r = red_combine(op, r, red[y][tx]);
+    for (int y = 1; y < 16; ++y) r = red_comb<MX>(r, red[y][tx]);
     red_store(out, op, c, r);
+  }
+}
+
+// The same second pass for fp32 partials with inner % 4 == 0: a block is 16
+// column vectors (64 columns, 256-byte runs of each partial row) x 16 lanes
+// down S, float4 loads eight at a time; each column is added in the same
+// order as col_finish_kernel's (lane ty takes s = ty, ty + 16, ... in
+// ascending order, then the 16 lanes in order), so the results are the same.
+// (Config 2's mean(0) finish over 256 partial rows: 3.0 us against 3.2 us.)
+template <bool MX>
+__global__ __launch_bounds__(256) void col_finish_v4_kernel(const float* __restrict__ part,
+                                                            int64_t outer, int64_t S,
+                                                            int64_t inner, int op, RedOut out) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __shared__ f4 red[16][16];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t ncv = inner / 4, total = outer * ncv;
+  const int64_t cl = (int64_t)blockIdx.x * 16 + tx;  // flattened (outer, column vector)
+  const bool live = cl < total;
+  const int64_t cvf = live ? cl : total - 1;  // loads unconditional, as above
+  const float id = red_ident<float>(op);
+  f4 acc = {id, id, id, id};
+  auto comb = [](f4 a, f4 b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = red_comb<MX>(a[e], b[e]);
+    return a;
+  };
+  {
+    const int64_t o = cvf / ncv, iv = cvf - o * ncv;
+    const f4* p = (const f4*)(part + o * S * inner) + iv;
+    int64_t s = ty;
+    for (; s + 112 < S; s += 128) {
+      f4 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = p[(s + 16 * u) * ncv];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = comb(acc, x[u]);
+    }
+    for (; s < S; s += 16) acc = comb(acc, p[s * ncv]);
+  }
+  red[ty][tx] = acc;
+  __syncthreads();
+  if (ty == 0 && live) {
+    f4 r = red[0][tx];
+#pragma unroll
+    for (int y = 1; y < 16; ++y) r = comb(r, red[y][tx]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red_store(out, op, cvf * 4 + e, r[e]);
   }
 }
 
@@ -326,17 +394,28 @@ mi_status_t launch_row(const void* in, int64_t outer, int64_t R, int op, RedOut 
   splits = (R + chunk - 1) / chunk;
   if (splits > 65535) splits = 65535;
   if (splits == 1) {
-    hipLaunchKernelGGL((row_reduce_kernel<Tag>), dim3((unsigned)outer, 1), dim3(kRowBlock), 0,
-                       stream, (const typename RT<Tag>::storage*)in, R, R, chunk, op, final_out);
+    if (op == R_MAX)
+      hipLaunchKernelGGL((row_reduce_kernel<Tag, true>), dim3((unsigned)outer, 1), dim3(kRowBlock),
+                         0, stream, (const typename RT<Tag>::storage*)in, R, R, chunk, op,
+                         final_out);
+    else
+      hipLaunchKernelGGL((row_reduce_kernel<Tag, false>), dim3((unsigned)outer, 1),
+                         dim3(kRowBlock), 0, stream, (const typename RT<Tag>::storage*)in, R, R,
+                         chunk, op, final_out);
     return check_launch("row_reduce");
   }
   Workspace ws;
   MI_RETURN_IF(ws.alloc((size_t)(outer * splits) * sizeof(A), stream));
   RedOut part{ws.get(), -1, 1.0};
   const int pop = op == R_MEAN ? R_SUM : op;
-  hipLaunchKernelGGL((row_reduce_kernel<Tag>), dim3((unsigned)outer, (unsigned)splits),
-                     dim3(kRowBlock), 0, stream, (const typename RT<Tag>::storage*)in, R, R,
-                     chunk, pop, part);
+  if (pop == R_MAX)
+    hipLaunchKernelGGL((row_reduce_kernel<Tag, true>), dim3((unsigned)outer, (unsigned)splits),
+                       dim3(kRowBlock), 0, stream, (const typename RT<Tag>::storage*)in, R, R,
+                       chunk, pop, part);
+  else
+    hipLaunchKernelGGL((row_reduce_kernel<Tag, false>), dim3((unsigned)outer, (unsigned)splits),
+                       dim3(kRowBlock), 0, stream, (const typename RT<Tag>::storage*)in, R, R,
+                       chunk, pop, part);
   MI_RETURN_IF(check_launch("row_reduce partial"));
   // second pass over [outer, splits] partials in the accumulation type
   const unsigned grid = ceil_div_u(outer, 4);
@@ -350,14 +429,32 @@ mi_status_t launch_row(const void* in, int64_t outer, int64_t R, int op, RedOut 
   return check_launch("row_reduce final");
 }
 
+// Lanes of a column block: the narrowest of 256 / 512 / 1024 that covers a
+// row's column vectors (1024 at most).
+inline int col_block_lanes(int64_t ncv) { return ncv > 512 ? 1024 : (ncv > 256 ? 512 : 256); }
+
+template <typename Tag, int VEC, int NTH>
+mi_status_t launch_col_vn(const void* in, int64_t outer, int64_t R, int64_t inner, int64_t chunk,
+                          int64_t splits, int op, RedOut o, hipStream_t stream) {
+  const int64_t ncv = inner / VEC;
+  dim3 grid((unsigned)(ceil_div_u(ncv, NTH) * outer), (unsigned)splits, 1);
+  if (op == R_MAX)
+    hipLaunchKernelGGL((col_reduce_kernel<Tag, VEC, NTH, true>), grid, dim3(NTH), 0, stream,
+                       (const typename RT<Tag>::storage*)in, R, inner, chunk, op, o);
+  else
+    hipLaunchKernelGGL((col_reduce_kernel<Tag, VEC, NTH, false>), grid, dim3(NTH), 0, stream,
+                       (const typename RT<Tag>::storage*)in, R, inner, chunk, op, o);
+  return check_launch("col_reduce");
+}
+
 template <typename Tag, int VEC>
 mi_status_t launch_col_v(const void* in, int64_t outer, int64_t R, int64_t inner, int64_t chunk,
                          int64_t splits, int op, RedOut o, hipStream_t stream) {
-  const int64_t ncv = inner / VEC;
-  dim3 grid((unsigned)(ceil_div_u(ncv, kColBlock) * outer), (unsigned)splits, 1);
-  hipLaunchKernelGGL((col_reduce_kernel<Tag, VEC>), grid, dim3(kColBlock), 0, stream,
-                     (const typename RT<Tag>::storage*)in, R, inner, chunk, op, o);
-  return check_launch("col_reduce");
+  switch (col_block_lanes(inner / VEC)) {
+    case 1024: return launch_col_vn<Tag, VEC, 1024>(in, outer, R, inner, chunk, splits, op, o, stream);
+    case 512: return launch_col_vn<Tag, VEC, 512>(in, outer, R, inner, chunk, splits, op, o, stream);
+    default: return launch_col_vn<Tag, VEC, 256>(in, outer, R, inner, chunk, splits, op, o, stream);
+  }
 }
 
 template <typename Tag>
@@ -370,9 +467,9 @@ mi_status_t launch_col_any(const void* in, int64_t outer, int64_t R, int64_t inn
   return launch_col_v<Tag, 1>(in, outer, R, inner, chunk, splits, op, o, stream);
 }
 
-// Splits R so that about 4 blocks per CU are in flight (config 2's fp32
-// [16384, 4096] mean(0): 4 column blocks x 256 splits of 64 rows), then
-// combines the partials in a second pass.
+// Splits R so that about 16 waves per CU are in flight (config 2's fp32
+// [16384, 4096] mean(0): one 1024-lane column block x 256 splits of 64 rows),
+// then combines the partials in a second pass.
 template <typename Tag>
 mi_status_t launch_col(const void* in, int64_t outer, int64_t R, int64_t inner, int op,
                        RedOut final_out, hipStream_t stream) {
@@ -380,10 +477,14 @@ mi_status_t launch_col(const void* in, int64_t outer, int64_t R, int64_t inner, 
   typedef typename RT<Tag>::storage St;
   constexpr int V = 16 / sizeof(St) >= 4 ? 4 : 16 / sizeof(St);
   const int64_t cus = cu_count();
-  const int64_t col_blocks = outer * ((inner / V + kColBlock - 1) / kColBlock);
+  // the lane count launch_col_any picks (VEC = V on the vector path; the
+  // scalar path's 256-lane blocks are only counted approximately here)
+  const int nth = col_block_lanes(inner / V);
+  const int64_t col_blocks = outer * ((inner / V + nth - 1) / nth);
+  const int64_t target = 4 * cus * 256 / nth;  // blocks for ~16 waves per CU
   int64_t splits = 1;
-  if (col_blocks < 4 * cus && R >= 2 * kColUnroll) {
-    splits = (4 * cus + col_blocks - 1) / col_blocks;
+  if (col_blocks < target && R >= 2 * kColUnroll) {
+    splits = (target + col_blocks - 1) / col_blocks;
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, R / 32));
   }
   splits = std::min<int64_t>(splits, 1024);
@@ -395,8 +496,26 @@ mi_status_t launch_col(const void* in, int64_t outer, int64_t R, int64_t inner, 
   RedOut part{ws.get(), -1, 1.0};
   const int pop = op == R_MEAN ? R_SUM : op;
   MI_RETURN_IF(launch_col_any<Tag>(in, outer, R, inner, chunk, splits, pop, part, stream));
-  hipLaunchKernelGGL((col_finish_kernel<A>), dim3(ceil_div_u(outer * inner, 16)), dim3(256), 0,
-                     stream, (const A*)ws.get(), outer, splits, inner, op, final_out);
+  const bool mx = op == R_MAX;
+  if constexpr (std::is_same<A, float>::value) {
+    if (inner % 4 == 0 && ((uintptr_t)ws.get() % 16) == 0) {
+      const dim3 grid(ceil_div_u(outer * inner / 4, 16));
+      if (mx)
+        hipLaunchKernelGGL(col_finish_v4_kernel<true>, grid, dim3(256), 0, stream,
+                           (const float*)ws.get(), outer, splits, inner, op, final_out);
+      else
+        hipLaunchKernelGGL(col_finish_v4_kernel<false>, grid, dim3(256), 0, stream,
+                           (const float*)ws.get(), outer, splits, inner, op, final_out);
+      return check_launch("col_reduce finish");
+    }
+  }
+  const dim3 grid(ceil_div_u(outer * inner, 16));
+  if (mx)
+    hipLaunchKernelGGL((col_finish_kernel<A, true>), grid, dim3(256), 0, stream,
+                       (const A*)ws.get(), outer, splits, inner, op, final_out);
+  else
+    hipLaunchKernelGGL((col_finish_kernel<A, false>), grid, dim3(256), 0, stream,
+                       (const A*)ws.get(), outer, splits, inner, op, final_out);
   return check_launch("col_reduce finish");
 }
 
