@@ -261,6 +261,31 @@ __device__ __forceinline__ T wave_max(T v) {
 __device__ __forceinline__ float nan_max(float a, float b) {
   return (a != a || a > b) ? a : b;
 }
+
+// fp32 wave64 reductions without LDS traffic: butterflies inside each row of
+// 16 lanes by DPP (quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror,
+// row_mirror: after them every lane holds its row's total), then the four
+// row totals read into scalar registers and combined in a fixed order.
+// Each DPP step is one VALU op a few cycles long, where a __shfl_xor step is
+// an LDS permute waited for in turn (six of them per reduction); every lane
+// gets the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                            0xF, 0xF, true));
+}
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+template <typename Op>
+__device__ __forceinline__ float wave_reduce_f32(float v, Op op) {
+  v = op(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_f32<0x141>(v));  // row_half_mirror: quad 0 <-> quad 1 of each 8
+  v = op(v, dpp_f32<0x140>(v));  // row_mirror: the two 8-lane halves of each row
+  return op(op(readlane_f32(v, 0), readlane_f32(v, 16)),
+            op(readlane_f32(v, 32), readlane_f32(v, 48)));
+}
 __device__ __forceinline__ double nan_max(double a, double b) {
   return (a != a || a > b) ? a : b;
 }
@@ -274,6 +299,15 @@ __device__ __forceinline__ T wave_nan_max(T v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = nan_max(v, (T)__shfl_xor(v, off, 64));
   return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce_f32(v, [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ float wave_nan_max(float v) {
+  return wave_reduce_f32(v, [](float a, float b) { return nan_max(a, b); });
+}
+__device__ __forceinline__ float wave_fmax(float v) {
+  return wave_reduce_f32(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024); every thread gets

@@ -75,8 +75,7 @@ __device__ __forceinline__ float block_sum_f(float v, float* red) {
 template <int NTH>
 __device__ __forceinline__ float block_fmax(float v, float* red) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  v = wave_fmax(v);
   if (lane == 0) red[wid] = v;
   __syncthreads();
   float r = red[0];
