@@ -423,6 +423,26 @@ mi_status_t mi_rope(const mi_tensor_t* q_out, const mi_tensor_t* k_out,
 mi_status_t mi_silu_mul(const mi_tensor_t* out, const mi_tensor_t* gate,
                         const mi_tensor_t* up, mi_stream_t stream);
 
+/* Fused matmul epilogues of a decoder layer.  No counterpart in the
+ * reference (new efficient ops, like rms_norm, rope and silu_mul above); each
+ * gives, bit for bit, what the unfused ops give:
+ *   mi_linear_residual: out = residual + x @ weight^T, the product rounded to
+ *     out's dtype first, then added in fp32 and rounded (linear, then add);
+ *   mi_linear_silu_mul: out = silu(x @ w_gate^T) * (x @ w_up^T), both
+ *     products rounded first (two linears, then silu_mul).
+ * x [M, K], weights [N, K] (w_gate and w_up with one row stride), residual
+ * and out [M, N]; bf16 or f16, unit column strides for the fused kernel (any
+ * strides otherwise); out may be the residual itself.  The large-tile matmul
+ * kernel applies the epilogue while its output tile is in LDS when there are
+ * tiles enough to fill the CUs; other shapes run the matmul(s) into
+ * workspace and then add / silu_mul. */
+mi_status_t mi_linear_residual(const mi_tensor_t* out, const mi_tensor_t* x,
+                               const mi_tensor_t* weight, const mi_tensor_t* residual,
+                               mi_stream_t stream);
+mi_status_t mi_linear_silu_mul(const mi_tensor_t* out, const mi_tensor_t* x,
+                               const mi_tensor_t* w_gate, const mi_tensor_t* w_up,
+                               mi_stream_t stream);
+
 /* out = silu(self) = self / (1 + exp(-self)), fp32 math, one rounding; self
  * broadcast to out, one dtype (bf16, f16, f32).  Replaces topsatenSilu
  * (yaml silu.out :561). */

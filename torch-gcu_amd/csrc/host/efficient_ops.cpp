@@ -5,7 +5,8 @@
 // here every op is also a dispatcher op in the `torch_gcu` namespace
 // (torch.ops.torch_gcu.<op>) with a PrivateUse1 kernel, so it can be captured
 // in a GCUGraph and shows up in profiles.  The fused ops are new (RMSNorm,
-// RoPE, SiLU-mul); int32_indices_index keeps the reference's op.
+// RoPE, SiLU-mul, and the matmuls with a residual add or SiLU-mul epilogue);
+// int32_indices_index keeps the reference's op.
 #include <ATen/ATen.h>
 #include <ATen/ExpandUtils.h>
 #include <torch/library.h>
@@ -96,6 +97,58 @@ at::Tensor silu_mul(const at::Tensor& gate, const at::Tensor& up) {
   check_mi(mi_silu_mul(&o, &gd, &ud, mi_stream(out)), "silu_mul");
   after_op();
   return out;
+}
+
+// Fused matmul epilogues: residual + linear(x, weight), and
+// silu(linear(x, w_gate)) * linear(x, w_up), bit for bit what the unfused ops
+// give (each product rounded before the add / silu_mul).  x [..., K],
+// weights [N, K]; the leading dims of x are flattened into rows.
+namespace {
+at::Tensor rows2(const at::Tensor& x) {
+  at::Tensor r = x.reshape({-1, x.size(-1)});
+  return r.stride(-1) == 1 ? r : r.contiguous();
+}
+at::Tensor weight2(const at::Tensor& w, const char* what) {
+  TORCH_CHECK(w.dim() == 2, what, ": weights must be 2-D [N, K]");
+  return w.stride(1) == 1 ? w : w.contiguous();
+}
+}  // namespace
+
+at::Tensor linear_residual(const at::Tensor& x, const at::Tensor& weight,
+                           const at::Tensor& residual) {
+  TORCH_CHECK(is_gcu(x) && is_gcu(weight) && is_gcu(residual),
+              "linear_residual: x, weight and residual must be gcu tensors");
+  const c10::DeviceGuard g(x.device());
+  const at::Tensor x2 = rows2(x), w = weight2(weight, "linear_residual");
+  std::vector<int64_t> shape = x.sizes().vec();
+  shape.back() = w.size(0);
+  TORCH_CHECK(residual.sizes().vec() == shape, "linear_residual: residual has shape ",
+              residual.sizes(), ", expected ", at::IntArrayRef(shape));
+  const at::Tensor r2 = rows2(residual);
+  at::Tensor out = at::empty({x2.size(0), w.size(0)}, x.options());
+  const mi_tensor_t o = desc(out), xd = desc(x2), wd = desc(w), rd = desc(r2);
+  check_mi(mi_linear_residual(&o, &xd, &wd, &rd, mi_stream(out)), "linear_residual");
+  after_op();
+  return out.view(shape);
+}
+
+at::Tensor linear_silu_mul(const at::Tensor& x, const at::Tensor& w_gate, const at::Tensor& w_up) {
+  TORCH_CHECK(is_gcu(x) && is_gcu(w_gate) && is_gcu(w_up),
+              "linear_silu_mul: x, w_gate and w_up must be gcu tensors");
+  TORCH_CHECK(w_gate.sizes() == w_up.sizes(), "linear_silu_mul: w_gate and w_up shapes differ");
+  const c10::DeviceGuard g(x.device());
+  const at::Tensor x2 = rows2(x), wg = weight2(w_gate, "linear_silu_mul"),
+                   wu = weight2(w_up, "linear_silu_mul");
+  // one row stride for both weights (the fused kernel reads both with it)
+  const at::Tensor wu2 = wu.stride(0) == wg.stride(0) ? wu : wu.contiguous();
+  const at::Tensor wg2 = wu.stride(0) == wg.stride(0) ? wg : wg.contiguous();
+  at::Tensor out = at::empty({x2.size(0), wg2.size(0)}, x.options());
+  const mi_tensor_t o = desc(out), xd = desc(x2), gd = desc(wg2), ud = desc(wu2);
+  check_mi(mi_linear_silu_mul(&o, &xd, &gd, &ud, mi_stream(out)), "linear_silu_mul");
+  after_op();
+  std::vector<int64_t> shape = x.sizes().vec();
+  shape.back() = wg2.size(0);
+  return out.view(shape);
 }
 
 // int8 weight-only linear: y = (x @ weight^T) * scales (+ bias), x [..., K]
@@ -247,6 +300,8 @@ TORCH_LIBRARY(torch_gcu, m) {
   m.def("silu_mul(Tensor gate, Tensor up) -> Tensor");
   m.def("int32_indices_index(Tensor self, Tensor?[] indices) -> Tensor");
   m.def("int8_linear(Tensor x, Tensor weight, Tensor scales, Tensor? bias=None) -> Tensor");
+  m.def("linear_residual(Tensor x, Tensor weight, Tensor residual) -> Tensor");
+  m.def("linear_silu_mul(Tensor x, Tensor w_gate, Tensor w_up) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(torch_gcu, PrivateUse1, m) {
@@ -256,4 +311,6 @@ TORCH_LIBRARY_IMPL(torch_gcu, PrivateUse1, m) {
   m.impl("silu_mul", TORCH_FN(torch_gcu::efficient::silu_mul));
   m.impl("int32_indices_index", TORCH_FN(torch_gcu::efficient::int32_indices_index));
   m.impl("int8_linear", TORCH_FN(torch_gcu::efficient::int8_linear));
+  m.impl("linear_residual", TORCH_FN(torch_gcu::efficient::linear_residual));
+  m.impl("linear_silu_mul", TORCH_FN(torch_gcu::efficient::linear_silu_mul));
 }

@@ -20,6 +20,9 @@ at::Tensor int32_indices_index(const at::Tensor& self,
                                const c10::List<std::optional<at::Tensor>>& indices);
 at::Tensor int8_linear(const at::Tensor& x, const at::Tensor& weight, const at::Tensor& scales,
                        const std::optional<at::Tensor>& bias);
+at::Tensor linear_residual(const at::Tensor& x, const at::Tensor& weight,
+                           const at::Tensor& residual);
+at::Tensor linear_silu_mul(const at::Tensor& x, const at::Tensor& w_gate, const at::Tensor& w_up);
 
 }  // namespace efficient
 }  // namespace torch_gcu

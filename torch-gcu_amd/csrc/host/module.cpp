@@ -260,6 +260,8 @@ PYBIND11_MODULE(_C, m) {
   m.def("_rms_norm", &efficient::rms_norm, py::arg("x"), py::arg("weight"), py::arg("eps") = 1e-6);
   m.def("_rope", &efficient::rope);
   m.def("_silu_mul", &efficient::silu_mul);
+  m.def("_linear_residual", &efficient::linear_residual);
+  m.def("_linear_silu_mul", &efficient::linear_silu_mul);
   m.def("_int32_indices_index", [](const at::Tensor& self, std::vector<std::optional<at::Tensor>> idx) {
     c10::List<std::optional<at::Tensor>> l;
     for (auto& i : idx) l.push_back(i);

@@ -342,6 +342,18 @@ __device__ __forceinline__ float fast_exp(float x) {
 __device__ __forceinline__ float fast_log(float x) {
   return __builtin_amdgcn_logf(x) * 0.6931471805599453f;
 }
+// silu(a) * b in fp32 (a / (1 + e^-a) * b on the hardware exp2 and
+// reciprocal): the SwiGLU product of silu_mul and of the matmul epilogue
+// that fuses it, one expression so the two round alike.  The fp32 product is
+// materialised (an empty asm) before the caller converts it: with an f16
+// operand the compiler otherwise folds the last multiply and the conversion
+// into v_fma_mix, which rounds once where the fp32 product rounded to f16
+// (CPU ATen's order) rounds twice.
+__device__ __forceinline__ float silu_mul_f32(float a, float b) {
+  float r = a * __builtin_amdgcn_rcpf(1.0f + fast_exp(-a)) * b;
+  asm volatile("" : "+v"(r));
+  return r;
+}
 
 // ---- streaming 16-byte accesses ----------------------------------------------
 

@@ -343,7 +343,7 @@ enum PairOp { P_SILU_MUL = 0, P_SILU_BWD = 1, P_SILU = 2 };
 template <int OP>
 __device__ __forceinline__ float pair_op(float a, float b) {
   if constexpr (OP == P_SILU_MUL) {
-    return a * __builtin_amdgcn_rcpf(1.0f + fast_exp(-a)) * b;
+    return silu_mul_f32(a, b);
   } else if constexpr (OP == P_SILU) {
     return a * __builtin_amdgcn_rcpf(1.0f + fast_exp(-a));
   } else {

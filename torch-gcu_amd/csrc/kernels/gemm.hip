@@ -71,6 +71,10 @@ struct GemmArgs {
   int64_t sa, sb, sc;  // batch strides (elements)
   float alpha, beta;
   int tiles_m, tiles_n;
+  // fused epilogues of the large-tile kernel (EPI_SILU, EPI_RESID below)
+  const void* b2;       // EPI_SILU: the up weight, rows laid out like b's (the gate weight)
+  const uint16_t* res;  // EPI_RESID: residual, element (m, n) at res[m * ldr + n]
+  int64_t ldr;
 };
 
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
@@ -480,9 +484,25 @@ __device__ __forceinline__ int dl_swz64(int r, int c) { return c ^ (((r >> 1) & 
 // B fragments are read transposed by ds_read_b64_tr_b16, which hands each
 // lane one column for 4 consecutive k (two reads per 8-k fragment).  Per
 // read, lanes 0..31 cover 4 rows x 128 bytes and land on 64 distinct banks.
-template <typename T, bool HAS_BIAS, bool B_INT8, bool SPLIT = false, bool B_KN = false>
+// EPI: fused epilogues of two matmuls of a decoder layer, each reproducing
+// the rounding of the unfused ops bit for bit:
+//   EPI_RESID: out = residual + round(x W^T), as linear then add (the sum in
+//     fp32, rounded once), the residual read in the coalesced store pass;
+//   EPI_SILU:  out = silu(round(x Wg^T)) * round(x Wu^T), as two linears then
+//     silu_mul: a 256-wide tile holds 128 gate columns (waves 0..3 copy their
+//     B rows from Wg) and the same 128 up columns (waves 4..7 from Wu), the
+//     waves of column half 0 stage gate, those of half 1 up, and after a
+//     barrier each wave combines half of its row band's pairs.
+constexpr int EPI_NONE = 0, EPI_RESID = 1, EPI_SILU = 2;
+
+template <typename T, bool HAS_BIAS, bool B_INT8, bool SPLIT = false, bool B_KN = false,
+          int EPI = EPI_NONE>
 __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* part, int64_t ldp) {
   static_assert(!B_KN || (!B_INT8 && !SPLIT), "row-major B: 16-bit, no split");
+  static_assert(EPI == EPI_NONE || (!HAS_BIAS && !B_INT8 && !SPLIT && !B_KN),
+                "fused epilogues: plain 16-bit K-contiguous matmul");
+  static_assert(EPI != EPI_SILU || (dl::WN == 2 && dl::NQB * dl::RPK * dl::NW / 2 == dl::BN / 2),
+                "gate rows come from waves 0..NW/2-1, up rows from the others");
   // MFMA shape: 16 x 16 x 32 (MD = 16) for K-contiguous operands, 32 x 32 x 16
   // for the transposed row-major B reads, whose lane layout is built for it
   constexpr bool M16 = !B_KN;
@@ -535,8 +555,10 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
     KT = base + (sl < rem ? 1 : 0);
   }
   const uint16_t* A = p.a + batch * p.sa + (int64_t)k_first * BK;
-  const char* Bbase = (const char*)p.b + (batch * p.sb + (int64_t)k_first * BK * (B_KN ? p.ldb : 1)) *
-                                             (B_INT8 ? 1 : 2);
+  // EPI_SILU: waves 0..NW/2-1 copy gate rows, the others up rows
+  const void* bsrc = (EPI == EPI_SILU && wave >= dl::NW / 2) ? p.b2 : p.b;
+  const char* Bbase = (const char*)bsrc + (batch * p.sb + (int64_t)k_first * BK * (B_KN ? p.ldb : 1)) *
+                                              (B_INT8 ? 1 : 2);
 
   // per-lane byte offsets (the host checked they fit 32 bits); rows past the
   // matrix are clamped to its last row and only feed outputs never stored
@@ -558,7 +580,10 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
       bo[q] = (uint32_t)((int64_t)min(n0 + row, N - 1) * p.ldb + dl_swz64(row, lane % dl::CH8) * 16);
     } else {
       const int row = (wave * NQB + q) * RPK + lane / CH;
-      bo[q] = (uint32_t)(((int64_t)min(n0 + row, N - 1) * p.ldb + dl_swz(row, lane % CH) * 8) * 2);
+      // EPI_SILU: tile tn covers output columns 128 tn .. 128 tn + 127 (rows
+      // 0..127 of the tile from the gate weight, 128..255 from the up weight)
+      const int grow = EPI == EPI_SILU ? tn * (BN / 2) + (row & (BN / 2 - 1)) : n0 + row;
+      bo[q] = (uint32_t)(((int64_t)min(grow, N - 1) * p.ldb + dl_swz(row, lane % CH) * 8) * 2);
     }
   }
   auto issue = [&](int st, int k0) __attribute__((always_inline)) {
@@ -858,18 +883,60 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
   const int64_t rbase = m0 + wm * TM, cbase = n0 + wn * TN;
   constexpr int LPR = TN / 8, RPI = 64 / LPR;  // lanes per row, rows per pass
   const bool vec_ok = (p.ldc % 8) == 0 && (((uintptr_t)Cb) & 15) == 0;
+  typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
+  if constexpr (EPI == EPI_SILU) {
+    // the row band's gate values are in the staging of wave (wm, 0), its up
+    // values in that of wave (wm, 1); wave (wm, wn) takes rows 32 wn .. 32 wn + 31
+    __syncthreads();
+    const uint16_t* eg = smem + (wm * WN) * TM * EP;
+    const uint16_t* eu = eg + TM * EP;
+    const int64_t cb = (int64_t)tn * (BN / 2);
+#pragma unroll 4
+    for (int it = 0; it < TM / 2 / RPI; ++it) {
+      const int r = wn * (TM / 2) + it * RPI + lane / LPR, c = (lane % LPR) * 8;
+      const u16x8_t g8 = *(const u16x8_t*)(eg + r * EP + c);
+      const u16x8_t u8 = *(const u16x8_t*)(eu + r * EP + c);
+      u16x8_t v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        v[e] = MfmaOp<T>::store(silu_mul_f32(MfmaOp<T>::load(g8[e]), MfmaOp<T>::load(u8[e])));
+      const int64_t m = rbase + r, n = cb + c;
+      if (m < p.M) {
+        if (vec_ok && n + 7 < p.N) {
+          *(u16x8_t*)(Cb + m * p.ldc + n) = v;
+        } else {
+          for (int e = 0; e < 8; ++e)
+            if (n + e < p.N) Cb[m * p.ldc + n + e] = v[e];
+        }
+      }
+    }
+    return;
+  }
+  const bool res_vec = EPI == EPI_RESID && (p.ldr % 8) == 0 && (((uintptr_t)p.res) & 15) == 0;
 #pragma unroll 4
   for (int it = 0; it < TM / RPI; ++it) {
     const int r = it * RPI + lane / LPR, c = (lane % LPR) * 8;
-    const uint4 v = *(const uint4*)(es + r * EP + c);
+    u16x8_t v = *(const u16x8_t*)(es + r * EP + c);
     const int64_t m = rbase + r, n = cbase + c;
     if (m < p.M) {
-      if (vec_ok && n + 7 < p.N) {
-        *(uint4*)(Cb + m * p.ldc + n) = v;
-      } else {
-        const uint16_t* pv = (const uint16_t*)&v;
+      if constexpr (EPI == EPI_RESID) {
+        // residual + the rounded product, as the add kernel: fma(other, 1, self)
+        u16x8_t rv;
+        if (res_vec && n + 7 < p.N) {
+          rv = *(const u16x8_t*)(p.res + m * p.ldr + n);
+        } else {
+          for (int e = 0; e < 8; ++e) rv[e] = n + e < p.N ? p.res[m * p.ldr + n + e] : (uint16_t)0;
+        }
+#pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (n + e < p.N) Cb[m * p.ldc + n + e] = pv[e];
+          v[e] = MfmaOp<T>::store(
+              __builtin_fmaf(MfmaOp<T>::load(v[e]), 1.0f, MfmaOp<T>::load(rv[e])));
+      }
+      if (vec_ok && n + 7 < p.N) {
+        *(u16x8_t*)(Cb + m * p.ldc + n) = v;
+      } else {
+        for (int e = 0; e < 8; ++e)
+          if (n + e < p.N) Cb[m * p.ldc + n + e] = v[e];
       }
     }
   }
@@ -1688,6 +1755,28 @@ mi_status_t launch_dl(const GemmArgs& q0, int64_t batch, hipStream_t s, const ch
   return check_launch(what);
 }
 
+// The large-tile kernel with a fused epilogue (EPI_RESID, EPI_SILU): 256 x 256
+// tiles over the output, or over 128 output columns (a gate and an up half)
+// for EPI_SILU.
+template <typename T, int EPI>
+mi_status_t launch_dl_epi(const GemmArgs& q0, hipStream_t s, const char* what) {
+  constexpr size_t lds = dl::LDS_BYTES;
+  static bool attr = [] {
+    (void)hipFuncSetAttribute((const void*)gemm_dl_kernel<T, false, false, false, false, EPI>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    return true;
+  }();
+  (void)attr;
+  GemmArgs q = q0;
+  const int64_t bn = EPI == EPI_SILU ? dl::BN / 2 : dl::BN;
+  q.tiles_m = (int)((q.M + dl::BM - 1) / dl::BM);
+  q.tiles_n = (int)((q.N + bn - 1) / bn);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, false, false, false, false, EPI>),
+                     dim3((unsigned)(q.tiles_m * q.tiles_n)), dim3(dl::NT), lds, s, q, nullptr,
+                     (int64_t)0);
+  return check_launch(what);
+}
+
 // Row-major [K][N] B read in place by the large-tile kernel: enough tiles to
 // fill the CUs, K % 64 == 0, 16-byte aligned rows of both operands, N a
 // multiple of 8 (whole 16-byte column chunks) and 32-bit lane offsets.
@@ -2081,6 +2170,106 @@ mi_status_t run_gemm(const mi_tensor_t* out, const mi_tensor_t* a, const mi_tens
   return MI_OK;
 }
 
+// x [M, K] @ W^T with W [N, K] (a linear layer's weight) and a fused
+// epilogue: EPI_RESID adds `aux` (residual [M, N]) to the rounded product,
+// EPI_SILU multiplies silu(x Wg^T) by x Wu^T (W = Wg, aux = Wu), each product
+// rounded first, as the unfused ops do.  The large-tile kernel takes the whole
+// op when it applies (tiles enough to fill the CUs and its alignment and
+// 32-bit offset rules); otherwise the products go to workspace through the
+// regular matmul and the elementwise op follows, with the same results.
+mi_status_t run_linear_epi(int epi, const mi_tensor_t* out, const mi_tensor_t* x,
+                           const mi_tensor_t* w, const mi_tensor_t* aux, hipStream_t stream,
+                           const char* what) {
+  clear_error();
+  MI_CHECK_ARG(out && x && w && aux, "%s: NULL descriptor", what);
+  MI_RETURN_IF(validate(out, "out"));
+  MI_RETURN_IF(validate(x, "x"));
+  MI_RETURN_IF(validate(w, "weight"));
+  MI_RETURN_IF(validate(aux, epi == EPI_SILU ? "w_up" : "residual"));
+  MI_CHECK_ARG(x->ndim == 2 && w->ndim == 2 && out->ndim == 2 && aux->ndim == 2,
+               "%s: x, weights, residual and out must be 2-D", what);
+  const int dt = x->dtype;
+  MI_CHECK_ARG(dt == MI_BF16 || dt == MI_F16, "%s: dtype %s is not supported", what,
+               dtype_name(dt));
+  MI_CHECK_ARG(w->dtype == dt && out->dtype == dt && aux->dtype == dt,
+               "%s: x, weights, residual and out must share a dtype", what);
+  const int64_t M = x->sizes[0], K = x->sizes[1], N = w->sizes[0];
+  MI_CHECK_ARG(w->sizes[1] == K, "%s: x has %lld features, the weight expects %lld", what,
+               (long long)K, (long long)w->sizes[1]);
+  MI_CHECK_ARG(out->sizes[0] == M && out->sizes[1] == N, "%s: out must be [%lld, %lld]", what,
+               (long long)M, (long long)N);
+  MI_CHECK_ARG(aux->sizes[0] == (epi == EPI_SILU ? N : M) && aux->sizes[1] == (epi == EPI_SILU ? K : N),
+               "%s: %s has the wrong shape", what, epi == EPI_SILU ? "w_up" : "residual");
+  if (M == 0 || N == 0) return MI_OK;
+  // the fused kernel: unit column strides, enough tiles, the dl kernel's rules
+  GemmArgs q{};
+  q.a = (const uint16_t*)x->data;
+  q.b = w->data;
+  q.c = (uint16_t*)out->data;
+  q.M = M;
+  q.N = N;
+  q.K = K;
+  q.lda = x->strides[0];
+  q.ldb = w->strides[0];
+  q.ldc = out->strides[0];
+  q.alpha = 1.f;
+  q.beta = 0.f;
+  bool fused = x->strides[1] == 1 && w->strides[1] == 1 && out->strides[1] == 1 &&
+               aux->strides[1] == 1 && K > 0 && dl_eligible(q, false);
+  if (epi == EPI_SILU) {
+    q.b2 = aux->data;
+    fused = fused && aux->strides[0] == q.ldb && ((uintptr_t)aux->data & 15) == 0 &&
+            ((N - 1) * q.ldb + K) * 2 < ((int64_t)1 << 32);
+  } else {
+    q.res = (const uint16_t*)aux->data;
+    q.ldr = aux->strides[0];
+  }
+  const int64_t bn = epi == EPI_SILU ? dl::BN / 2 : dl::BN;
+  fused = fused && ((M + dl::BM - 1) / dl::BM) * ((N + bn - 1) / bn) >= cu_count();
+  if (fused) {
+    if (dt == MI_BF16)
+      return epi == EPI_SILU ? launch_dl_epi<BF16, EPI_SILU>(q, stream, what)
+                             : launch_dl_epi<BF16, EPI_RESID>(q, stream, what);
+    return epi == EPI_SILU ? launch_dl_epi<F16, EPI_SILU>(q, stream, what)
+                           : launch_dl_epi<F16, EPI_RESID>(q, stream, what);
+  }
+  // unfused: the product(s) into workspace, then the elementwise op
+  auto wt = [](const mi_tensor_t* t) {  // [K, N] view of a [N, K] weight
+    mi_tensor_t v = *t;
+    v.sizes[0] = t->sizes[1];
+    v.sizes[1] = t->sizes[0];
+    v.strides[0] = t->strides[1];
+    v.strides[1] = t->strides[0];
+    return v;
+  };
+  mi_tensor_t tmp{};
+  tmp.dtype = dt;
+  tmp.ndim = 2;
+  tmp.sizes[0] = M;
+  tmp.sizes[1] = N;
+  tmp.strides[0] = N;
+  tmp.strides[1] = 1;
+  Workspace w1, w2;
+  MI_RETURN_IF(w1.alloc((size_t)(M * N) * 2, stream));
+  tmp.data = w1.get();
+  const mi_tensor_t wv = wt(w);
+  MI_RETURN_IF(run_gemm(&tmp, x, &wv, nullptr, nullptr, nullptr, 1.0, 0.0, stream, what));
+  if (epi == EPI_RESID) {
+    mi_scalar_t one{};
+    one.dtype = MI_F64;
+    one.f = 1.0;
+    one.i = 1;
+    one.wrapped = 1;
+    return mi_add(out, aux, &tmp, one, (mi_stream_t)stream);
+  }
+  mi_tensor_t tmp2 = tmp;
+  MI_RETURN_IF(w2.alloc((size_t)(M * N) * 2, stream));
+  tmp2.data = w2.get();
+  const mi_tensor_t uv = wt(aux);
+  MI_RETURN_IF(run_gemm(&tmp2, x, &uv, nullptr, nullptr, nullptr, 1.0, 0.0, stream, what));
+  return mi_silu_mul(out, &tmp, &tmp2, (mi_stream_t)stream);
+}
+
 }  // namespace
 }  // namespace mi
 
@@ -2112,6 +2301,19 @@ mi_status_t mi_baddbmm(const mi_tensor_t* out, const mi_tensor_t* self, const mi
                        const mi_tensor_t* batch2, double beta, double alpha, mi_stream_t stream) {
   return run_gemm(out, batch1, batch2, nullptr, nullptr, self, alpha, beta, (hipStream_t)stream,
                   "baddbmm");
+}
+
+mi_status_t mi_linear_residual(const mi_tensor_t* out, const mi_tensor_t* x,
+                               const mi_tensor_t* weight, const mi_tensor_t* residual,
+                               mi_stream_t stream) {
+  return run_linear_epi(EPI_RESID, out, x, weight, residual, (hipStream_t)stream,
+                        "linear_residual");
+}
+
+mi_status_t mi_linear_silu_mul(const mi_tensor_t* out, const mi_tensor_t* x,
+                               const mi_tensor_t* w_gate, const mi_tensor_t* w_up,
+                               mi_stream_t stream) {
+  return run_linear_epi(EPI_SILU, out, x, w_gate, w_up, (hipStream_t)stream, "linear_silu_mul");
 }
 
 mi_status_t mi_int8_linear(const mi_tensor_t* out, const mi_tensor_t* x, const mi_tensor_t* weight,

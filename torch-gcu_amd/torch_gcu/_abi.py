@@ -117,6 +117,8 @@ _SIGNATURES = {
     "mi_bmm": ([_T, _T, _T, _S], ctypes.c_int),
     "mi_baddbmm": ([_T, _T, _T, _T, ctypes.c_double, ctypes.c_double, _S], ctypes.c_int),
     "mi_int8_linear": ([_T, _T, _T, _T, _T, _S], ctypes.c_int),
+    "mi_linear_residual": ([_T, _T, _T, _T, _S], ctypes.c_int),
+    "mi_linear_silu_mul": ([_T, _T, _T, _T, _S], ctypes.c_int),
     "mi_flash_attention_fwd": ([_T, _T, _T, _T, _T, ctypes.c_int32, ctypes.c_double, _S],
                                ctypes.c_int),
 }
@@ -497,6 +499,18 @@ def baddbmm(out, bias, a, b, beta=1.0, alpha=1.0):
 def int8_linear(out, x, weight, scales, bias=None):
     check("mi_int8_linear", lib().mi_int8_linear(desc(out), desc(x), desc(weight), desc(scales),
                                                  desc(bias), stream_of(out)))
+    return out
+
+
+def linear_residual(out, x, weight, residual):
+    check("mi_linear_residual", lib().mi_linear_residual(desc(out), desc(x), desc(weight),
+                                                         desc(residual), stream_of(out)))
+    return out
+
+
+def linear_silu_mul(out, x, w_gate, w_up):
+    check("mi_linear_silu_mul", lib().mi_linear_silu_mul(desc(out), desc(x), desc(w_gate),
+                                                         desc(w_up), stream_of(out)))
     return out
 
 

@@ -2,7 +2,9 @@
 
 ``gcu_index`` keeps the reference's one efficient op
 (torch_gcu/gcu/efficient/op.py:8-16 -> torch_gcu/csrc/efficient_ops/ops.cpp:335-342);
-``rms_norm``, ``rope``, ``rope_`` and ``silu_mul`` are new fused kernels.
+``rms_norm``, ``rope``, ``rope_`` and ``silu_mul`` are new fused kernels, and
+``linear_residual`` / ``linear_silu_mul`` are matmuls with the residual add or
+the SwiGLU product fused into their epilogue.
 All are dispatcher ops (``torch.ops.torch_gcu.*``) with gcu kernels only.
 """
 from __future__ import annotations
@@ -34,6 +36,18 @@ def rope_(q: torch.Tensor, k: Optional[torch.Tensor], positions: torch.Tensor,
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up with one rounding."""
     return torch.ops.torch_gcu.silu_mul(gate, up)
+
+
+def linear_residual(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """residual + F.linear(x, weight), bit for bit as the two ops (the product
+    rounded to the input dtype first)."""
+    return torch.ops.torch_gcu.linear_residual(x, weight, residual)
+
+
+def linear_silu_mul(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """silu_mul(F.linear(x, w_gate), F.linear(x, w_up)), bit for bit as the
+    three ops (both products rounded to the input dtype first)."""
+    return torch.ops.torch_gcu.linear_silu_mul(x, w_gate, w_up)
 
 
 def int8_linear(x: torch.Tensor, weight: torch.Tensor, scales: torch.Tensor,

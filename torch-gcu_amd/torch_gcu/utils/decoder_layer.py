@@ -1,8 +1,11 @@
 """The Llama-7B-shaped decoder layer of benchmark config 5, written as plain
 torch code so that on a gcu tensor every op goes through the PrivateUse1
-registrations: embedding (index_select), RMSNorm / RoPE / SiLU-mul (the fused
-efficient ops), the seven projections (mm on MFMA), causal
-scaled_dot_product_attention (the flash kernel) and the residual adds.
+registrations: embedding (index_select), RMSNorm / RoPE (the fused efficient
+ops), the q / k / v projections (mm on MFMA), causal
+scaled_dot_product_attention (the flash kernel), and the o / down projections
+with the residual add and the gate / up projections with the SiLU-mul fused
+into the matmul epilogue (efficient ops that give what linear + add and
+linear, linear + silu_mul give, bit for bit).
 
 The same module runs on CPU tensors with the ATen compositions of the fused
 ops, which is how the tests compare the two paths.
@@ -70,16 +73,34 @@ def _silu_mul(gate, up):
     return (F.silu(gate.float()) * up.float()).to(gate.dtype)
 
 
+def _linear_residual(x, w, residual):
+    """residual + linear(x, w) (the product rounded first, as two ops)."""
+    if x.device.type == "gcu":
+        return torch.gcu.efficient.linear_residual(x, w, residual)
+    return residual + F.linear(x, w)
+
+
+def _linear_silu_mul(h, w_gate, w_up):
+    """silu_mul(linear(h, w_gate), linear(h, w_up))."""
+    if h.device.type == "gcu":
+        return torch.gcu.efficient.linear_silu_mul(h, w_gate, w_up)
+    return _silu_mul(F.linear(h, w_gate), F.linear(h, w_up))
+
+
 def positions(batch: int, seq: int, device) -> torch.Tensor:
     """Token positions 0..seq-1 for each sequence, flattened (int64)."""
     return torch.arange(seq, dtype=torch.int64).repeat(batch).to(device)
 
 
 def forward(weights: dict, ids: torch.Tensor, cfg: LayerConfig,
-            pos: torch.Tensor | None = None) -> torch.Tensor:
+            pos: torch.Tensor | None = None, fused: bool = True) -> torch.Tensor:
     """One decoder layer over token ids [batch, seq]; returns [batch*seq, hidden].
     `pos` (from positions()) is passed in when the call is captured in a
-    graph, so nothing inside the captured region is created on the host."""
+    graph, so nothing inside the captured region is created on the host.
+    fused=False runs the o / gate / up / down projections as plain linears
+    followed by the adds and silu_mul (every projection then goes through the
+    dispatcher's mm, which op_check compares op by op); the result is the
+    same bit for bit."""
     B, S = ids.shape
     T = B * S
     H, D = cfg.heads, cfg.head_dim
@@ -96,10 +117,15 @@ def forward(weights: dict, ids: torch.Tensor, cfg: LayerConfig,
     vh = v.view(B, S, H, D).transpose(1, 2)
     a = F.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
     a = a.transpose(1, 2).reshape(T, H * D)
-    x = x + F.linear(a, weights["wo"])
+    if not fused:
+        x = x + F.linear(a, weights["wo"])
+        h = _rms_norm(x, weights["ffn_norm"], cfg.eps)
+        m = _silu_mul(F.linear(h, weights["w_gate"]), F.linear(h, weights["w_up"]))
+        return x + F.linear(m, weights["w_down"])
+    x = _linear_residual(a, weights["wo"], x)
     h = _rms_norm(x, weights["ffn_norm"], cfg.eps)
-    m = _silu_mul(F.linear(h, weights["w_gate"]), F.linear(h, weights["w_up"]))
-    return x + F.linear(m, weights["w_down"])
+    m = _linear_silu_mul(h, weights["w_gate"], weights["w_up"])
+    return _linear_residual(m, weights["w_down"], x)
 
 
 def flops(cfg: LayerConfig, batch: int, seq: int) -> int:
