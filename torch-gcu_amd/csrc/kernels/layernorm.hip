@@ -641,7 +641,12 @@ __global__ __launch_bounds__(kLnBlock) void ln_fwd_row_kernel(LnFwdArgs a) {
 // slower on [16384, 4096] bf16).  A wave that keeps the parameters in
 // registers and walks 2 or 4 rows, loading the next row before reducing the
 // current one, measured 40-65 % slower, and 8 rows no faster than one.
-template <typename Tag, int VPL, bool WF32>
+// LDSP: the block first copies gamma and beta into LDS (dynamic, 2 nv PW
+// 16-byte words) and the waves read their pieces from there: read per row
+// from L2, each piece's loads were waited for in turn (bf16 [16384, 4096]:
+// 51.8 -> 47.5 us in a harness; walking 2-8 rows a wave over the staged copy
+// was no faster than one).
+template <typename Tag, int VPL, bool WF32, bool LDSP>
 __global__ __launch_bounds__(256) void ln_fwd_wave_kernel(LnFwdArgs a) {
   typedef typename Num<Tag>::storage St;
   constexpr int VEC = 16 / sizeof(St);
@@ -653,11 +658,20 @@ __global__ __launch_bounds__(256) void ln_fwd_wave_kernel(LnFwdArgs a) {
     uint4 u[VEC / 4];
     float f[VEC];
   };
+  constexpr int PW = WF32 ? VEC / 4 : 1;  // 16-byte words per piece per parameter
+  extern __shared__ uint4 prm[];            // LDSP: gamma's words, then beta's
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (row >= a.M) return;
   const int64_t nv = a.N / VEC;
   const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
+  if constexpr (LDSP) {
+    for (int64_t i = threadIdx.x; i < nv * PW; i += 256) {
+      prm[i] = has_g ? ((const uint4*)a.gamma)[i] : uint4{0, 0, 0, 0};
+      prm[nv * PW + i] = has_b ? ((const uint4*)a.beta)[i] : uint4{0, 0, 0, 0};
+    }
+    __syncthreads();
+  }
+  if (row >= a.M) return;
   const V* px = (const V*)((const St*)a.x + row * a.N);
   V v[VPL];
 #pragma unroll
@@ -688,7 +702,30 @@ __global__ __launch_bounds__(256) void ln_fwd_wave_kernel(LnFwdArgs a) {
     const int64_t i = lane + (int64_t)k * 64;
     if (i < nv) {
       float g[VEC], b[VEC];
-      if (has_g) {
+      if constexpr (LDSP) {
+        P pg, pb;
+#pragma unroll
+        for (int w = 0; w < PW; ++w) {
+          pg.u[w] = prm[i * PW + w];
+          pb.u[w] = prm[nv * PW + i * PW + w];
+        }
+        if constexpr (WF32) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            g[e] = has_g ? pg.f[e] : 1.0f;
+            b[e] = pb.f[e];
+          }
+        } else {
+          V vg, vb;
+          vg.u = pg.u[0];
+          vb.u = pb.u[0];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            g[e] = has_g ? Num<Tag>::load(vg.s[e]) : 1.0f;
+            b[e] = Num<Tag>::load(vb.s[e]);
+          }
+        }
+      } else if (has_g) {
         if constexpr (WF32) {
           P pg;
 #pragma unroll
@@ -704,21 +741,23 @@ __global__ __launch_bounds__(256) void ln_fwd_wave_kernel(LnFwdArgs a) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) g[e] = 1.0f;
       }
-      if (has_b) {
-        if constexpr (WF32) {
-          P pb;
+      if constexpr (!LDSP) {
+        if (has_b) {
+          if constexpr (WF32) {
+            P pb;
 #pragma unroll
-          for (int w = 0; w < VEC / 4; ++w) pb.u[w] = ((const uint4*)((const float*)a.beta + i * VEC))[w];
+            for (int w = 0; w < VEC / 4; ++w) pb.u[w] = ((const uint4*)((const float*)a.beta + i * VEC))[w];
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) b[e] = pb.f[e];
+            for (int e = 0; e < VEC; ++e) b[e] = pb.f[e];
+          } else {
+            const V pb = ((const V*)a.beta)[i];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) b[e] = Num<Tag>::load(pb.s[e]);
+          }
         } else {
-          const V pb = ((const V*)a.beta)[i];
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) b[e] = Num<Tag>::load(pb.s[e]);
+          for (int e = 0; e < VEC; ++e) b[e] = 0.0f;
         }
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) b[e] = 0.0f;
       }
       V o;
 #pragma unroll
@@ -749,12 +788,25 @@ mi_status_t launch_ln_fwd(const LnFwdArgs& a, hipStream_t stream) {
   if (reg && params_ok && nv <= 64 * 16 && (a.M + 3) / 4 <= 0x7fffffffLL) {
     const bool wf32 = pdt == MI_F32 && !std::is_same<Tag, float>::value;
     const unsigned grid = (unsigned)((a.M + 3) / 4);
+    // parameters staged in LDS up to 32 KiB a block (more would cost occupancy)
+    const size_t lds = (size_t)2 * nv * (wf32 ? VEC / 4 : 1) * 16;
+    const bool ldsp = lds <= 32 * 1024;
     auto go = [&](auto vpl_c) -> mi_status_t {
       constexpr int VPL = decltype(vpl_c)::value;
-      if (wf32)
-        hipLaunchKernelGGL((ln_fwd_wave_kernel<Tag, VPL, true>), dim3(grid), dim3(256), 0, stream, a);
-      else
-        hipLaunchKernelGGL((ln_fwd_wave_kernel<Tag, VPL, false>), dim3(grid), dim3(256), 0, stream, a);
+      if (ldsp) {
+        if (wf32)
+          hipLaunchKernelGGL((ln_fwd_wave_kernel<Tag, VPL, true, true>), dim3(grid), dim3(256), lds,
+                             stream, a);
+        else
+          hipLaunchKernelGGL((ln_fwd_wave_kernel<Tag, VPL, false, true>), dim3(grid), dim3(256),
+                             lds, stream, a);
+      } else if (wf32) {
+        hipLaunchKernelGGL((ln_fwd_wave_kernel<Tag, VPL, true, false>), dim3(grid), dim3(256), 0,
+                           stream, a);
+      } else {
+        hipLaunchKernelGGL((ln_fwd_wave_kernel<Tag, VPL, false, false>), dim3(grid), dim3(256), 0,
+                           stream, a);
+      }
       return check_launch("layer_norm");
     };
     if (nv <= 64) return go(std::integral_constant<int, 1>());
