@@ -403,7 +403,8 @@ mi_status_t mi_flash_attention_fwd(const mi_tensor_t* out, const mi_tensor_t* ls
  * new fused ops on the same surface and have no TopsAten counterpart. */
 
 /* out[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * weight, fp32 math,
- * over the last dim; weight may be NULL data (no scale). */
+ * over the last dim; weight a dense vector of the last dim's size, or NULL
+ * data (no scale). */
 mi_status_t mi_rms_norm(const mi_tensor_t* out, const mi_tensor_t* x,
                         const mi_tensor_t* weight, double eps,
                         mi_stream_t stream);

@@ -42,7 +42,11 @@ struct FT<F16> {
 
 // ---- RMSNorm ------------------------------------------------------------------
 
-// One wave per row, VPL 16-byte vectors per lane.
+// One wave per row, VPL 16-byte vectors per lane.  The weight is copied into
+// LDS once per block (dynamic, H / VEC 16-byte words) and read from there:
+// read per row from L2 under the store guard, each piece's load was waited
+// for in turn (the layer-norm forward's parameters measured 51.8 -> 47.5 us
+// the same way).
 template <typename Tag, int VPL, bool HAS_W>
 __global__ __launch_bounds__(256) void rms_norm_wave_kernel(
     typename FT<Tag>::storage* __restrict__ out, const typename FT<Tag>::storage* __restrict__ x,
@@ -54,11 +58,16 @@ __global__ __launch_bounds__(256) void rms_norm_wave_kernel(
     uint4 u;
     St s[VEC];
   };
+  extern __shared__ uint4 wl[];
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  const int64_t nv = H / VEC;
+  if constexpr (HAS_W) {
+    for (int64_t i = threadIdx.x; i < nv; i += 256) wl[i] = ((const uint4*)w)[i];
+    __syncthreads();
+  }
   if (row >= rows) return;
   const V* px = (const V*)(x + row * x_row_stride);
-  const int64_t nv = H / VEC;
   // every load of the row is issued before the first sum (a sum inside the
   // guarded load loop makes each load wait for the one before it)
   V v[VPL];
@@ -79,13 +88,12 @@ __global__ __launch_bounds__(256) void rms_norm_wave_kernel(
   ss = wave_sum(ss);
   const float r = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
   V* po = (V*)(out + row * out_row_stride);
-  const V* pw = (const V*)w;
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int64_t i = lane + (int64_t)k * 64;
     if (i < nv) {
       V o, wv;
-      if (HAS_W) wv = pw[i];
+      if (HAS_W) wv.u = wl[i];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         float y = FT<Tag>::load(v[k].s[e]) * r;
@@ -165,9 +173,9 @@ mi_status_t rms_norm_t(const mi_tensor_t* out, const mi_tensor_t* x, const mi_te
       constexpr int VPL = decltype(vpl_c)::value;
       const unsigned grid = ceil_div_u(rows, 4);
       if (has_w)
-        hipLaunchKernelGGL((rms_norm_wave_kernel<Tag, VPL, true>), dim3(grid), dim3(256), 0,
-                           stream, (St*)out->data, (const St*)x->data, (const St*)w->data, rows,
-                           H, xs, os, eps);
+        hipLaunchKernelGGL((rms_norm_wave_kernel<Tag, VPL, true>), dim3(grid), dim3(256),
+                           (size_t)(H / (16 / sizeof(St))) * 16, stream, (St*)out->data,
+                           (const St*)x->data, (const St*)w->data, rows, H, xs, os, eps);
       else
         hipLaunchKernelGGL((rms_norm_wave_kernel<Tag, VPL, false>), dim3(grid), dim3(256), 0,
                            stream, (St*)out->data, (const St*)x->data, (const St*)nullptr, rows,
@@ -457,6 +465,7 @@ mi_status_t mi_rms_norm(const mi_tensor_t* out, const mi_tensor_t* x, const mi_t
     MI_RETURN_IF(validate(weight, "weight"));
     MI_CHECK_ARG(numel(*weight) == H, "rms_norm: weight has %lld elements, expected %lld",
                  (long long)numel(*weight), (long long)H);
+    MI_CHECK_ARG(is_contiguous(*weight), "rms_norm: weight must be dense");
   }
   switch (x->dtype) {
     case MI_BF16: return rms_norm_t<BF16>(out, x, weight, (float)eps, stream);
