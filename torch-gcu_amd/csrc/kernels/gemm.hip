@@ -435,6 +435,21 @@ static_assert(LDS_BYTES8 <= 160 * 1024 && LDS_BYTES8 >= (size_t)NW * TM * EP * 2
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
+
+// Global -> LDS copy of 16 bytes a lane (global_load_lds_dwordx4) from a
+// wave-uniform base plus a 32-bit per-lane byte offset, to the wave's 1 KiB
+// at `lds` (M0).  Written as inline assembly so that the compiler does not
+// track it: it counts such a copy as a FLAT access that may touch LDS, and
+// while one is in flight every wait for an LDS read it emits is lgkmcnt(0),
+// which at the top of each K step waited for the fragment reads just issued
+// as well as the ones the first MFMA needs.  The kernels wait for their
+// copies themselves (vmcnt) before the barrier that publishes them.  The
+// s_nop is the wait state an LDS DMA needs after M0 is written.
+__device__ __forceinline__ void lds_copy16(const void* base, uint32_t off, void* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(lds_void_t*)lds;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(m0)
+               : "memory");
+}
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 template <int N>
@@ -592,13 +607,9 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
     const char* Ab = (const char*)(A + k0);
     const char* Bb = Bbase + (int64_t)k0 * (B_KN ? p.ldb * 2 : (B_INT8 ? 1 : 2));
 #pragma unroll
-    for (int q = 0; q < NQA; ++q)
-      __builtin_amdgcn_global_load_lds((const void*)(Ab + ao[q]),
-                                       (lds_void_t*)(as + (wave * NQA + q) * 512), 16, 0, 0);
+    for (int q = 0; q < NQA; ++q) lds_copy16(Ab, ao[q], as + (wave * NQA + q) * 512);
 #pragma unroll
-    for (int q = 0; q < NQB; ++q)
-      __builtin_amdgcn_global_load_lds((const void*)(Bb + bo[q]),
-                                       (lds_void_t*)(bs + (wave * NQB + q) * 512), 16, 0, 0);
+    for (int q = 0; q < NQB; ++q) lds_copy16(Bb, bo[q], bs + (wave * NQB + q) * 512);
   };
   // fragment read offsets: lane supplies row l % MD, 16-byte k chunk
   // (KPM / 8) s + l / MD of substep s
@@ -693,13 +704,10 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
     uint16_t* as = smem + st * (TA + TB);
     uint16_t* bs = as + TA;
     if (q < NQA) {
-      __builtin_amdgcn_global_load_lds((const void*)((const char*)(A + k0) + ao[q]),
-                                       (lds_void_t*)(as + (wave * NQA + q) * 512), 16, 0, 0);
+      lds_copy16(A + k0, ao[q], as + (wave * NQA + q) * 512);
     } else {
       const char* Bb = Bbase + (int64_t)k0 * (B_INT8 ? 1 : 2);
-      __builtin_amdgcn_global_load_lds((const void*)(Bb + bo[q - NQA]),
-                                       (lds_void_t*)(bs + (wave * NQB + q - NQA) * 512), 16, 0,
-                                       0);
+      lds_copy16(Bb, bo[q - NQA], bs + (wave * NQB + q - NQA) * 512);
     }
   };
   auto read_a = [&](int st, int s, int buf, int i) __attribute__((always_inline)) {
@@ -795,6 +803,16 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
     }
   };
 
+  // The epilogue's pointers are formed (and their scalar loads waited for)
+  // before the main loop: left to the compiler, such a load (the batch
+  // stride, the int8 scales) was issued just before the loop and stayed in
+  // flight through it, and since scalar loads return out of order every LDS
+  // wait in the loop became lgkmcnt(0), so each step's first MFMA waited for
+  // reads issued after the ones it needs.
+  uint16_t* Cb = p.c + batch * p.sc;
+  asm volatile("" : : "s"(Cb));
+  const float* scale = p.scale;
+  if constexpr (B_INT8) asm volatile("" : : "s"(scale));
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < KT) issue(s, s * BK);
@@ -854,7 +872,7 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
       const int nl = j * MD + (M16 ? 4 * (lane >> 4) : 8 * g + 4 * (lane >> 5));
       const int64_t n = n0 + wn * TN + nl;
       f32x4_t sc4 = {1.f, 1.f, 1.f, 1.f}, bb4 = {};
-      if constexpr (B_INT8) sc4 = load_col4(p.scale, MI_F32, n, 1, p.N);
+      if constexpr (B_INT8) sc4 = load_col4(scale, MI_F32, n, 1, p.N);
       if (row_bias) bb4 = load_col4(p.bias, p.bias_dtype, n, p.bias_sn, p.N, batch * p.bias_sb);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
@@ -879,7 +897,6 @@ __global__ __launch_bounds__(dl::NT, 2) void gemm_dl_kernel(GemmArgs p, float* p
         *(u16x4_t*)(es + ml * EP + nl) = v;
       }
     }
-  uint16_t* Cb = p.c + batch * p.sc;
   const int64_t rbase = m0 + wm * TM, cbase = n0 + wn * TN;
   constexpr int LPR = TN / 8, RPI = 64 / LPR;  // lanes per row, rows per pass
   const bool vec_ok = (p.ldc % 8) == 0 && (((uintptr_t)Cb) & 15) == 0;
