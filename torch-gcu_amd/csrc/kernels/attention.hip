@@ -135,7 +135,9 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
   const int bh = bid / p.q_tiles;
   const int64_t h = bh % p.H, b = bh / p.H;
   const int64_t hk = h * p.Hk / p.H;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index read as wave-uniform: the loop bounds and tile bases
+  // that derive from it then stay in scalar registers
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5, col = lane & 31;
   const int64_t q0 = (int64_t)qt * QT;
   const int64_t wq0 = q0 + wave * 32;  // this wave's first query row
@@ -190,14 +192,9 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
 #pragma unroll
       for (int i = 0; i < C::NINS / 4; ++i) {
         const int q = wv * (C::NINS / 4) + i;
-        // the offset enters each copy as a 32-bit register (hoisted out of
-        // the loop as a 64-bit value it costs a 64-bit add per copy); the
-        // copy then takes the scalar base + 32-bit offset form
+        // the copy takes the scalar base + 32-bit offset form
         const char* gb = (const char*)(G + (int64_t)(kv0 + (is_v ? q * C::RPI : 0)) * g_ss);
-        uint32_t o = is_v ? vob1 : kob[i];
-        asm volatile("" : "+v"(o));
-        __builtin_amdgcn_global_load_lds((const void*)(gb + o), (lds_void_t*)(dst + q * 512), 16,
-                                         0, 0);
+        lds_copy16(gb, is_v ? vob1 : kob[i], dst + q * 512);
       }
     } else {
       // (the lane id passes through an empty asm so that nothing of this
@@ -210,8 +207,7 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
         const int key = q * C::RPI + ln / C::CPR, cp = ln % C::CPR;
         const int gk = min(kv0 + key, Sk - 1);
         const int sw = is_v ? C::swz_v(key) : C::swz_k(key);
-        __builtin_amdgcn_global_load_lds((const void*)(G + gk * g_ss + 8 * (cp ^ sw)),
-                                         (lds_void_t*)(dst + q * 512), 16, 0, 0);
+        lds_copy16(G, (uint32_t)(gk * g_ss + 8 * (cp ^ sw)) * 2u, dst + q * 512);
       }
     }
   };

@@ -355,6 +355,29 @@ __device__ __forceinline__ float silu_mul_f32(float a, float b) {
   return r;
 }
 
+// Global -> LDS copy of 16 bytes a lane (global_load_lds_dwordx4) from a
+// wave-uniform base plus a 32-bit per-lane byte offset, to the wave's 1 KiB
+// at `lds` (M0).  Written as inline assembly so that the compiler does not
+// track it: it counts such a copy as a FLAT access that may touch LDS, and
+// while one is in flight every wait for an LDS read it emits is lgkmcnt(0),
+// so a fragment read issued ahead of the MFMA before it is waited for
+// there.  Callers wait for their copies themselves (vmcnt) before the
+// barrier that publishes them.  The s_nop is the wait state an LDS DMA
+// needs after M0 is written.  The base must be wave-uniform; it is read
+// from the first lane (free when it is already in scalar registers, which
+// the "s" operand needs).
+__device__ __forceinline__ void lds_copy16(const void* base, uint32_t off, void* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+  // (readfirstlane returns int: each word goes through uint32_t so that the
+  // low word is zero-extended, not sign-extended into the high one)
+  const uint64_t b = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint64_t sb = ((uint64_t)hi << 32) | lo;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(sb), "{m0}"(m0)
+               : "memory");
+}
+
 // ---- streaming 16-byte accesses ----------------------------------------------
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));

@@ -435,21 +435,6 @@ static_assert(LDS_BYTES8 <= 160 * 1024 && LDS_BYTES8 >= (size_t)NW * TM * EP * 2
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
-
-// Global -> LDS copy of 16 bytes a lane (global_load_lds_dwordx4) from a
-// wave-uniform base plus a 32-bit per-lane byte offset, to the wave's 1 KiB
-// at `lds` (M0).  Written as inline assembly so that the compiler does not
-// track it: it counts such a copy as a FLAT access that may touch LDS, and
-// while one is in flight every wait for an LDS read it emits is lgkmcnt(0),
-// which at the top of each K step waited for the fragment reads just issued
-// as well as the ones the first MFMA needs.  The kernels wait for their
-// copies themselves (vmcnt) before the barrier that publishes them.  The
-// s_nop is the wait state an LDS DMA needs after M0 is written.
-__device__ __forceinline__ void lds_copy16(const void* base, uint32_t off, void* lds) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(lds_void_t*)lds;
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(m0)
-               : "memory");
-}
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 template <int N>
