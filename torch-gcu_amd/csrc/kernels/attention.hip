@@ -256,9 +256,9 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
     kf[0] = *(const vec*)((const char*)ks + ko);
     kf[1] = *(const vec*)((const char*)(ks + 32 * D) + ko);
   };
-  auto read_v = [&](const uint16_t* vs, int t, vec* vf) __attribute__((always_inline)) {
+  auto read_v = [&](const uint16_t* vs, int t, vec* vf, int d0, int d1) __attribute__((always_inline)) {
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {
+    for (int d = d0; d < d1; ++d) {
       typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
       const int vo = xor_off(vbm, 64 * d);
       const uint16_t* vb = (const uint16_t*)((const char*)(vs + 16 * t * D) + vo);
@@ -404,10 +404,12 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
     }
     // ---- phase 2: O^T += V^T P^T(j) on the MFMAs; the second half of P(j),
     // then the mask and max of S(j + 1) ----
+    // V^T fragments of k-step t + 1 are read as soon as the MFMAs of step t
+    // that use the same registers are issued (d tiles 0, 1, then 2, 3)
     float mx = -INFINITY;
+    read_v(vr, 0, vf, 0, DT);
 #pragma unroll
     for (int t = 0; t < PS; ++t) {
-      read_v(vr, t, vf);
       if (t == 0) exp_range(sc_, 16, 24);
       if (t == 1) {
         exp_range(sc_, 24, 32);
@@ -424,7 +426,14 @@ __global__ __launch_bounds__(NT, 2) void flash_fwd_kernel(AttnArgs p) {
         }
       }
 #pragma unroll
-      for (int d = 0; d < DT; ++d) o[d] = AttnOp<T>::mma(vf[d], pk[t], o[d]);
+      for (int d = 0; d < DT / 2; ++d) o[d] = AttnOp<T>::mma(vf[d], pk[t], o[d]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < PS) read_v(vr, t + 1, vf, 0, DT / 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int d = DT / 2; d < DT; ++d) o[d] = AttnOp<T>::mma(vf[d], pk[t], o[d]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < PS) read_v(vr, t + 1, vf, DT / 2, DT);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
